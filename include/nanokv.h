@@ -1,0 +1,216 @@
+/*
+ * nanokv.h -- C ABI of the MI355X-native NanoKV sparse-attention layer-step.
+ *
+ * One shared library (libnanokv.so, gfx950 code objects) exports the entry
+ * points below.  Every pointer is a device pointer unless the comment says
+ * otherwise; every entry point enqueues work on `stream` (a hipStream_t) and
+ * returns without synchronising.  The caller owns every buffer, including
+ * workspaces; nothing here allocates device memory.  Return value: NKV_OK, or
+ * an NKV_ERR_* code with a message available from nkv_last_error().
+ *
+ * Store layout (one allocation per field, leading layer dimension L):
+ *   hist_k / hist_v : [L][Hkv][cap][B][D]  bf16 (NKV_KV_BF16) or int8
+ *   reps            : [L][Hkv][cap][r][D]  bf16
+ *   sink_k / sink_v : [L][Hkv][S][D]       bf16
+ *   recent_k/_v     : [L][Hkv][R][D]       bf16 ring; logical slot i of the
+ *                      reference's left-aligned recent buffer lives at
+ *                      physical slot (ring_start + i) % R
+ *   k_scale         : [L][Hkv][D] fp32     (NKV_KV_INT8_CHANNEL)
+ *   v_scale         : [L][Hkv][cap] fp32   (NKV_KV_INT8_CHANNEL)
+ *   k_tscale/v_tscale: [L][Hkv][cap*B] fp16 (NKV_KV_INT8_TOKEN)
+ * B = 64 and D = 128 are fixed by the kernels; Hq/Hkv <= 16; r in {1,2,4,8}.
+ *
+ * Reference citations are to Tao20060602/nano-vllm-kv-optimizer.
+ */
+#ifndef NANOKV_H
+#define NANOKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NKV_ABI_VERSION 1
+
+enum nkv_status {
+  NKV_OK = 0,
+  NKV_ERR_ARG = 1,          /* an argument violates a documented constraint */
+  NKV_ERR_UNSUPPORTED = 2,  /* shape/format outside what the kernels handle */
+  NKV_ERR_HIP = 3           /* a HIP launch or runtime call failed */
+};
+
+enum nkv_kv_format {
+  NKV_KV_BF16 = 0,
+  NKV_KV_INT8_CHANNEL = 1,  /* K per-(Hkv,D) scale, V per-(block,Hkv) scale: m12_runtime.py:460-477 */
+  NKV_KV_INT8_TOKEN = 2     /* per-token-per-KV-head fp16 scales for K and V */
+};
+
+enum nkv_topk_order {
+  NKV_ORDER_SCORE_DESC = 0, /* torch.topk(sorted=True); ties by block id ascending */
+  NKV_ORDER_ID_ASC = 1      /* the same set, ids ascending (gather_sort) */
+};
+
+/* Plain-data view of a model's HBM-resident sparse KV store. */
+typedef struct nkv_store {
+  void* hist_k;
+  void* hist_v;
+  void* reps;
+  void* sink_k;
+  void* sink_v;
+  void* recent_k;
+  void* recent_v;
+  float* k_scale;
+  float* v_scale;
+  uint16_t* k_tscale;
+  uint16_t* v_tscale;
+  int32_t num_layers;
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t block_size;
+  int32_t r;
+  int32_t cap_blocks;
+  int32_t sink_tokens;
+  int32_t recent_tokens;
+  int32_t kv_format;
+} nkv_store;
+
+int nkv_abi_version(void);
+/* Thread-local message of the last failing call on this host thread (host memory). */
+const char* nkv_last_error(void);
+
+/*
+ * Block scoring + Top-K selection for `num_layers` layers starting at
+ * `layer0`.
+ *
+ * Replaces M12LayerRuntime._gpu_select fixed-budget path
+ * (nanovllm/sparse/m12_runtime.py:959-1055; scorer fused_select.py:23-79) and,
+ * with per_query=1, the per-query Top-K of _gpu_select_per_query
+ * (m12_runtime.py:1057-1079).
+ *
+ * q        : bf16 [num_layers][nq][Hq][D], layer stride q_layer_stride elements.
+ * score[b] = max over (n<nq, h, g, j<r) of the fp32 dot q[n][h*G+g] . reps[h][b][j],
+ *            accumulated in ascending d with fma, per_query=0;
+ *            per (n) when per_query=1.
+ * Protected ids (device int32 list, shared by all layers; ids outside
+ * [0, nblocks) are ignored) are scored -inf.  k_eff = min(k, max(1, nblocks
+ * - |protected in range|)) ids are returned per (layer[, n]), in `order`.
+ * scores_ws: fp32 workspace [num_layers][nq'][nblocks] (nq' = per_query ? nq : 1).
+ * out_ids  : int32 [num_layers][nq'][k] (entries >= k_eff untouched).
+ * out_vals : fp32  [num_layers][nq'][k] selected scores (may be NULL).
+ * Constraints: 1 <= nblocks <= cap_blocks, nblocks <= 12288, 1 <= k <= 1024.
+ */
+int nkv_select(const nkv_store* st, int layer0, int num_layers,
+               const uint16_t* q, int64_t q_layer_stride, int nq, int per_query,
+               int nblocks, const int32_t* protected_ids, int n_protected,
+               int k, int order, float* scores_ws,
+               int32_t* out_ids, float* out_vals, void* stream);
+
+/*
+ * Segmented GQA attention for few queries (decode and speculative verify).
+ *
+ * Replaces, for decode, M12LayerRuntime.decode steps 1 and 3-5
+ * (m12_runtime.py:1164-1172 recent shift/append, :1212-1311 gather + pack,
+ * :1317-1320 -> _fused_attention fast path :867-873); for verify,
+ * verify_tokens steps 2-3 (m12_runtime.py:686-758) with the masked
+ * _fused_attention path (:875-896) and the lossless per-query mask (:753-758).
+ *
+ * Keys/values attended by query t of layer l, KV head h, in this order:
+ *   n_hist selected history blocks  ids[l][i] (64 tokens each; with
+ *            `allowed` != NULL only blocks with allowed[t][i] != 0),
+ *   sink   : sink[l][h][0 .. sink_len),
+ *   recent : logical slots [rec_lo, rec_lo + rec_len) of the ring, physical
+ *            slot (ring_base + i) % R; logical slot `new_slot` (>= 0) is read
+ *            from k_new/v_new instead, which this call also writes into
+ *            physical slot `write_slot` (decode's shift+append),
+ *   chunk  : k_new/v_new tokens 0 .. n_chunk-1, causal (query t sees c <= t).
+ * q      : bf16 [num_layers][tq][Hq][D] (layer stride q_layer_stride).
+ * k_new, v_new : bf16 [num_layers][max(n_chunk,1)][Hkv][D] (layer stride kv_layer_stride).
+ * ids    : int32 [num_layers][ids_layer_stride]; allowed: uint8 [tq][n_hist] (shared by layers).
+ * out    : bf16 [num_layers][tq][Hq][D] (layer stride q_layer_stride).
+ * partial_ws : fp32 workspace, >= nkv_attend_workspace_floats(...) floats.
+ * counters   : int32 workspace of num_layers*Hkv*ceil(tq/qpw) entries, zero
+ *              before first use; every call leaves them zero.
+ * splits : workgroups per (layer, KV head, query group), 1..64.  Queries are
+ *          processed in groups of 16/G per workgroup (grid z = layers x groups).
+ * Constraints: 1 <= tq <= 65536, n_hist <= 4096, n_chunk in {0, tq};
+ *          fp32 softmax and accumulation.
+ */
+int nkv_attend(const nkv_store* st, int layer0, int num_layers,
+               const uint16_t* q, int64_t q_layer_stride, int tq,
+               const uint16_t* k_new, const uint16_t* v_new, int64_t kv_layer_stride,
+               int n_chunk, int new_slot, int write_slot,
+               const int32_t* ids, int64_t ids_layer_stride, int n_hist,
+               const uint8_t* allowed, int sink_len,
+               int ring_base, int rec_lo, int rec_len,
+               float scale, int splits,
+               float* partial_ws, int32_t* counters,
+               uint16_t* out, void* stream);
+
+/* Floats of partial_ws needed by nkv_attend for these sizes. */
+int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads, int num_heads,
+                                    int tq, int splits);
+
+/*
+ * Append one prefill chunk to the history of `num_layers` layers.
+ *
+ * Replaces the history / quantisation / sink part of M12LayerRuntime._store_kv
+ * (m12_runtime.py:420-481; quant_kv.py:27-49): tokens k[t], v[t] (bf16
+ * [num_layers][T][Hkv][D], layer stride kv_layer_stride) go to blocks
+ * start_block .. start_block + ceil(T/64) - 1, the last one zero-padded.
+ * int8 channel format: if compute_k_scale, k_scale[l] is first set from this
+ * chunk (amax/127, clamped at 1e-8/127); V gets a per-block scale.
+ * int8 token format: per-token fp16 scales.
+ * If write_sink, sink[l][h][0 .. min(S, T)) = the chunk's first tokens.
+ * Constraints: T >= 1, start_block + ceil(T/64) <= cap_blocks.
+ */
+int nkv_store_chunk(const nkv_store* st, int layer0, int num_layers,
+                    const uint16_t* k, const uint16_t* v, int64_t kv_layer_stride,
+                    int T, int start_block, int compute_k_scale, int write_sink,
+                    void* stream);
+
+/*
+ * Block representatives of the chunk's blocks.
+ *
+ * Replaces M12LayerRuntime._build_reps_gpu (m12_runtime.py:354-395): per
+ * (block, KV head) the first argmax of cos(k_t, mean direction), then r-1
+ * farthest-point steps (first argmin of the max cos to the chosen set); the
+ * chosen raw bf16 keys go to reps[l][h][start_block + b][j].
+ * k: bf16 [num_layers][T][Hkv][D] (tokens >= T of the last block are zeros).
+ */
+int nkv_build_reps(const nkv_store* st, int layer0, int num_layers,
+                   const uint16_t* k, int64_t kv_layer_stride, int T,
+                   int start_block, void* stream);
+
+/*
+ * Recent-window update on the logical buffer.
+ *
+ * Replaces the recent part of _store_kv (m12_runtime.py:486-503) and of
+ * commit_verified (m12_runtime.py:784-800): logical slots [0, carry) take the
+ * old logical slots [old_len - carry, old_len), then slots
+ * [carry, carry + n_src) take src tokens src_lo .. src_lo + n_src - 1 of k/v
+ * (bf16 [num_layers][*][Hkv][D]).  Slots >= carry + n_src keep their content.
+ */
+int nkv_recent_update(const nkv_store* st, int layer0, int num_layers,
+                      const uint16_t* k, const uint16_t* v, int64_t kv_layer_stride,
+                      int src_lo, int n_src, int ring_start, int old_len, int carry,
+                      void* stream);
+
+/*
+ * Query summaries for prefill routing.
+ *
+ * Replaces prefill_query_summaries (m12_runtime.py:53-67): out[l][s] =
+ * bf16 round-to-nearest-even of the mean of q[l][lo_s .. hi_s) (torch
+ * tensor_split bounds over T tokens, nseg = min(nsegments, T)).
+ * q: bf16 [num_layers][T][Hq][D]; out: bf16 [num_layers][nseg][Hq][D].
+ */
+int nkv_query_summaries(const uint16_t* q, int64_t q_layer_stride, int num_layers,
+                        int T, int num_heads, int head_dim, int nsegments,
+                        uint16_t* out, int64_t out_layer_stride, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANOKV_H */

@@ -1,0 +1,600 @@
+// Segmented GQA attention for few queries: sparse decode and speculative
+// verify (kernel 3 of the layer-step).
+//
+// One workgroup (4 wavefronts) handles one (layer, KV head, query group,
+// split).  The keys it attends are cut into 64-token segments: the selected
+// history blocks (read in place from the HBM history, bf16 or int8), the sink,
+// the recent ring (logical slots mapped to physical ones), and, for verify,
+// the causal chunk of new tokens.  Wavefront w of split s handles segments
+// w + 4*s, w + 4*s + 4*splits, ... and keeps an online-softmax state.
+//
+//  * Q.K^T runs on the matrix cores: v_mfma_f32_16x16x32_bf16 with A = 16
+//    keys x 32 dims (each lane loads 16 contiguous bytes of one key row) and
+//    B = 32 dims x 16 query rows (G heads per query, padded to 16).  int8
+//    keys are widened to bf16 exactly; the per-(head, dim) K scale is folded
+//    into the bf16 query operand of history segments.
+//  * softmax: fp32, exp2 with the scale folded in; masked keys get -inf.
+//  * P.V on the vector ALUs in fp32: lane (r, c) owns dims 8c..8c+7 of keys
+//    4j + r; p comes from LDS.  The int8 V scale (per block or per token) is
+//    folded into p.
+//  * the 4 wavefronts merge through LDS; with splits > 1 each workgroup
+//    writes a partial (m, l, acc[128]) per query row and the last workgroup
+//    of its (layer, head, group) - found with an atomic counter - merges them
+//    and resets the counter.
+//
+// Same result as the reference's gather + pack + fp32 einsum attention
+// (nanovllm/sparse/m12_runtime.py:1212-1320 and :845-896) up to fp32
+// summation order.
+#include "nkv_common.h"
+
+namespace nkv {
+namespace {
+
+constexpr int kAttendWaves = 4;
+constexpr int kAttendThreads = kAttendWaves * kWave;
+constexpr int kPRow = 20;        // floats per key row of the p tile in LDS (16 rows + pad)
+constexpr int kPartStride = 130; // floats per partial row: m, l, acc[128]
+constexpr int kMaxRows = 16;     // MFMA N: query rows per group
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+enum SegType { kSegHist = 0, kSegSink = 1, kSegRecent = 2, kSegChunk = 3 };
+
+struct AttendParams {
+  const void* hist_k;
+  const void* hist_v;
+  int64_t hist_ls;
+  const uint16_t* sink_k;
+  const uint16_t* sink_v;
+  int64_t sink_ls;
+  uint16_t* rec_k;
+  uint16_t* rec_v;
+  int64_t rec_ls;
+  const float* k_scale;     // [L][Hkv][D]
+  const float* v_scale;     // [L][Hkv][cap]
+  const uint16_t* k_tscale; // [L][Hkv][cap*64]
+  const uint16_t* v_tscale;
+  const uint16_t* q;
+  int64_t q_ls;
+  const uint16_t* k_new;
+  const uint16_t* v_new;
+  int64_t kv_ls;
+  const int32_t* ids;
+  int64_t ids_ls;
+  const uint8_t* allowed;
+  float* partial;
+  int32_t* counters;
+  uint16_t* out;
+  int hkv, G, cap, S, R;
+  int tq, qpg, nqg;
+  int n_chunk, new_slot, write_slot;
+  int n_hist, sink_len, ring_base, rec_lo, rec_len;
+  int n_sink_seg, n_rec_seg, nseg;
+  int splits;
+  float scale_log2;
+};
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// 8 signed bytes -> 8 bf16 (exact: |x| <= 127 has <= 7 significant bits).
+__device__ __forceinline__ uint4 i8x8_to_bf16x8(uint2 raw) {
+  uint32_t w[2] = {raw.x, raw.y};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t src = w[i >> 1] >> ((i & 1) * 16);
+    const float f0 = static_cast<float>(static_cast<int8_t>(src & 0xffu));
+    const float f1 = static_cast<float>(static_cast<int8_t>((src >> 8) & 0xffu));
+    o[i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+__device__ __forceinline__ void i8x8_to_f32(uint2 raw, float* f) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t w = (i < 4) ? raw.x : raw.y;
+    f[i] = static_cast<float>(static_cast<int8_t>((w >> ((i & 3) * 8)) & 0xffu));
+  }
+}
+
+struct Seg {
+  int type;
+  int len;   // valid tokens in this segment (1..64)
+  int off;   // first logical token (sink / recent / chunk)
+  int blk;   // history block id
+  int u;     // history segment index (column of `allowed`)
+};
+
+__device__ __forceinline__ Seg classify(const AttendParams& p, int layer, int s) {
+  Seg g;
+  g.blk = 0;
+  g.u = 0;
+  g.off = 0;
+  if (s < p.n_hist) {
+    g.type = kSegHist;
+    g.len = kBlock;
+    g.u = s;
+    g.blk = p.ids[static_cast<int64_t>(layer) * p.ids_ls + s];
+    if (g.blk < 0 || g.blk >= p.cap) {  // never read outside the history
+      g.blk = 0;
+      g.len = 0;
+    }
+    return g;
+  }
+  s -= p.n_hist;
+  if (s < p.n_sink_seg) {
+    g.type = kSegSink;
+    g.off = s * kBlock;
+    g.len = min(kBlock, p.sink_len - g.off);
+    return g;
+  }
+  s -= p.n_sink_seg;
+  if (s < p.n_rec_seg) {
+    g.type = kSegRecent;
+    g.off = p.rec_lo + s * kBlock;
+    g.len = min(kBlock, p.rec_lo + p.rec_len - g.off);
+    return g;
+  }
+  s -= p.n_rec_seg;
+  g.type = kSegChunk;
+  g.off = s * kBlock;
+  g.len = min(kBlock, p.n_chunk - g.off);
+  return g;
+}
+
+// Element offset of key/value row `tk` of segment `g` for bf16 sources, or the
+// byte offset into the int8 history for history segments of int8 formats.
+// `which` selects K (0) or V (1).
+template <int FMT>
+__device__ __forceinline__ const void* row_ptr(const AttendParams& p, int layer, int h,
+                                               const Seg& g, int tk, int which) {
+  if (g.type == kSegHist) {
+    const int64_t idx = p.hist_ls * layer +
+                        ((static_cast<int64_t>(h) * p.cap + g.blk) * kBlock + tk) * kHeadDim;
+    const void* base = which ? p.hist_v : p.hist_k;
+    if (FMT == NKV_KV_BF16) return static_cast<const uint16_t*>(base) + idx;
+    return static_cast<const int8_t*>(base) + idx;
+  }
+  if (g.type == kSegSink) {
+    const uint16_t* base = which ? p.sink_v : p.sink_k;
+    return base + p.sink_ls * layer + (static_cast<int64_t>(h) * p.S + g.off + tk) * kHeadDim;
+  }
+  if (g.type == kSegRecent) {
+    const int lp = g.off + tk;
+    if (lp == p.new_slot) {
+      const uint16_t* base = which ? p.v_new : p.k_new;
+      return base + p.kv_ls * layer + static_cast<int64_t>(h) * kHeadDim;
+    }
+    const int slot = (p.ring_base + lp) % p.R;
+    const uint16_t* base = which ? p.rec_v : p.rec_k;
+    return base + p.rec_ls * layer + (static_cast<int64_t>(h) * p.R + slot) * kHeadDim;
+  }
+  const uint16_t* base = which ? p.v_new : p.k_new;
+  return base + p.kv_ls * layer + (static_cast<int64_t>(g.off + tk) * p.hkv + h) * kHeadDim;
+}
+
+template <int FMT, int M>
+__global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendParams p) {
+  __shared__ __attribute__((aligned(16))) float s_p[kAttendWaves][kBlock * kPRow];
+  __shared__ float s_alpha[kAttendWaves][kMaxRows];
+  __shared__ int s_last;
+
+  const int split = blockIdx.x;
+  const int h = blockIdx.y;
+  const int layer = blockIdx.z / p.nqg;
+  const int qg = blockIdx.z % p.nqg;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int ln = lane & 15;   // MFMA column / PV dim group
+  const int lg = lane >> 4;   // MFMA row group / PV key residue
+  const int hq = p.hkv * p.G;
+  const int q0 = qg * p.qpg;
+  const int rows = min(p.qpg, p.tq - q0) * p.G;
+
+  // decode's shift+append: the new token goes into the freed ring slot.
+  if (p.write_slot >= 0 && split == 0 && qg == 0 && wave == 0 && lane < 32) {
+    const int which = lane >> 4;
+    const int c = lane & 15;
+    const uint4* src = reinterpret_cast<const uint4*>(
+        (which ? p.v_new : p.k_new) + p.kv_ls * layer + static_cast<int64_t>(h) * kHeadDim);
+    uint4* dst = reinterpret_cast<uint4*>(
+        (which ? p.rec_v : p.rec_k) + p.rec_ls * layer +
+        (static_cast<int64_t>(h) * p.R + p.write_slot) * kHeadDim);
+    dst[c] = src[c];
+  }
+
+  // ---- query operands (B of the MFMA): row n = lane & 15 -------------------
+  const int my_row = ln;
+  const bool row_ok = my_row < rows;
+  const int my_t = q0 + (row_ok ? my_row / p.G : 0);
+  const int my_hq = h * p.G + (my_row % p.G);
+  bf16x8 bq[4], bqs[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int d0 = s * 32 + lg * 8;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (row_ok) {
+      v = *reinterpret_cast<const uint4*>(
+          p.q + p.q_ls * layer + (static_cast<int64_t>(my_t) * hq + my_hq) * kHeadDim + d0);
+    }
+    bq[s] = as_bf16x8(v);
+    if (FMT == NKV_KV_INT8_CHANNEL) {
+      const float* ks = p.k_scale + static_cast<int64_t>(layer) * p.hkv * kHeadDim + h * kHeadDim + d0;
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a = bf16_lo(w[i]) * ks[2 * i];
+        const float b = bf16_hi(w[i]) * ks[2 * i + 1];
+        o[i] = static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+      }
+      bqs[s] = as_bf16x8(make_uint4(o[0], o[1], o[2], o[3]));
+    } else {
+      bqs[s] = bq[s];
+    }
+  }
+
+  float m_run = -INFINITY;   // per query row (lane & 15); equal across lane groups
+  float l_run = 0.0f;        // partial over this lane group's keys
+  float acc[M][8];
+#pragma unroll
+  for (int n = 0; n < M; ++n)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[n][e] = 0.0f;
+
+  float* my_p = s_p[wave];
+  const int nwaves = p.splits * kAttendWaves;
+  for (int sidx = split * kAttendWaves + wave; sidx < p.nseg; sidx += nwaves) {
+    const Seg g = classify(p, layer, sidx);
+    const bool int8_seg = (FMT != NKV_KV_BF16) && g.type == kSegHist;
+
+    // ---- S^T = K . Q^T on the matrix cores -------------------------------
+    f32x4 c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      c[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      const int tk = i * 16 + ln;
+      uint4 a[4];
+      if (tk < g.len) {
+        const void* rp = row_ptr<FMT>(p, layer, h, g, tk, 0);
+        if (int8_seg) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            a[s] = i8x8_to_bf16x8(*reinterpret_cast<const uint2*>(
+                static_cast<const int8_t*>(rp) + s * 32 + lg * 8));
+        } else {
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            a[s] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(rp) + s * 32 + lg * 8);
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) a[s] = make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        c[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[s]), int8_seg ? bqs[s] : bq[s],
+                                                        c[i], 0, 0, 0);
+    }
+
+    // ---- masking, scale, online softmax ------------------------------------
+    // c[i][e]: key tk = 16 i + 4 lg + e, query row ln.
+    float x[4][4];
+    float cmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int tk = i * 16 + lg * 4 + e;
+        float v = c[i][e];
+        bool ok = row_ok && tk < g.len;
+        if (FMT == NKV_KV_INT8_TOKEN && g.type == kSegHist && ok)
+          v *= f16_bits_to_f32(p.k_tscale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap * kBlock +
+                                          static_cast<int64_t>(g.blk) * kBlock + tk]);
+        if (g.type == kSegHist && p.allowed != nullptr && ok)
+          ok = p.allowed[static_cast<int64_t>(my_t) * p.n_hist + g.u] != 0;
+        if (g.type == kSegChunk && ok) ok = (g.off + tk) <= my_t;
+        v = ok ? v * p.scale_log2 : -INFINITY;
+        x[i][e] = v;
+        cmax = fmaxf(cmax, v);
+      }
+    }
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+    const float m_new = fmaxf(m_run, cmax);
+    const float alpha = (m_new == -INFINITY) ? 1.0f : exp2f(m_run - m_new);
+    float vs_blk = 1.0f;
+    if (FMT == NKV_KV_INT8_CHANNEL && g.type == kSegHist)
+      vs_blk = p.v_scale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap + g.blk];
+    float lsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int tk = i * 16 + lg * 4 + e;
+        const float pe = (x[i][e] == -INFINITY) ? 0.0f : exp2f(x[i][e] - m_new);
+        lsum += pe;
+        float pv = pe * vs_blk;
+        if (FMT == NKV_KV_INT8_TOKEN && g.type == kSegHist && tk < g.len)
+          pv *= f16_bits_to_f32(p.v_tscale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap * kBlock +
+                                           static_cast<int64_t>(g.blk) * kBlock + tk]);
+        my_p[tk * kPRow + ln] = pv;
+      }
+    }
+    l_run = l_run * alpha + lsum;
+    m_run = m_new;
+    if (lane < kMaxRows) s_alpha[wave][lane] = alpha;
+    wave_lds_sync();
+
+    // ---- O += P . V (fp32) --------------------------------------------------
+    float al[M];
+#pragma unroll
+    for (int n = 0; n < M; ++n) al[n] = s_alpha[wave][n];
+#pragma unroll
+    for (int n = 0; n < M; ++n)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[n][e] *= al[n];
+#pragma unroll 4
+    for (int j = 0; j < 16; ++j) {
+      const int tk = 4 * j + lg;
+      if (tk < g.len) {
+        float vf[8];
+        const void* rp = row_ptr<FMT>(p, layer, h, g, tk, 1);
+        if (int8_seg) {
+          i8x8_to_f32(*reinterpret_cast<const uint2*>(static_cast<const int8_t*>(rp) + ln * 8), vf);
+        } else {
+          const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(rp) + ln * 8);
+          vf[0] = bf16_lo(v.x); vf[1] = bf16_hi(v.x); vf[2] = bf16_lo(v.y); vf[3] = bf16_hi(v.y);
+          vf[4] = bf16_lo(v.z); vf[5] = bf16_hi(v.z); vf[6] = bf16_lo(v.w); vf[7] = bf16_hi(v.w);
+        }
+        const float* prow = my_p + tk * kPRow;
+#pragma unroll
+        for (int n4 = 0; n4 < M; n4 += 4) {
+          const float4 pp = *reinterpret_cast<const float4*>(prow + n4);
+          const float pn[4] = {pp.x, pp.y, pp.z, pp.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[n4 + u][e] = __builtin_fmaf(pn[u], vf[e], acc[n4 + u][e]);
+        }
+      }
+    }
+    wave_lds_sync();
+  }
+
+  // ---- reduce the wave's state across lane groups --------------------------
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
+#pragma unroll
+  for (int n = 0; n < M; ++n)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      acc[n][e] += __shfl_xor(acc[n][e], 16);
+      acc[n][e] += __shfl_xor(acc[n][e], 32);
+    }
+
+  // ---- merge the 4 wavefronts in LDS (reusing the p tiles) -----------------
+  __syncthreads();
+  float* s_m = &s_p[0][0];                         // [waves][16]
+  float* s_l = s_m + kAttendWaves * kMaxRows;      // [waves][16]
+  float* s_acc = s_l + kAttendWaves * kMaxRows;    // [waves][M][128]
+  if (lane < kMaxRows) {
+    s_m[wave * kMaxRows + lane] = m_run;
+    s_l[wave * kMaxRows + lane] = l_run;
+  }
+  if (lg == 0) {
+#pragma unroll
+    for (int n = 0; n < M; ++n)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_acc[(wave * M + n) * kHeadDim + ln * 8 + e] = acc[n][e];
+  }
+  __syncthreads();
+
+  const int64_t grp = (static_cast<int64_t>(layer) * p.hkv + h) * p.nqg + qg;
+  for (int idx = threadIdx.x; idx < M * kHeadDim; idx += kAttendThreads) {
+    const int n = idx / kHeadDim, d = idx % kHeadDim;
+    float mt = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kAttendWaves; ++w) mt = fmaxf(mt, s_m[w * kMaxRows + n]);
+    float L = 0.0f, A = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttendWaves; ++w) {
+      const float mw = s_m[w * kMaxRows + n];
+      const float sw = (mw == -INFINITY) ? 0.0f : exp2f(mw - mt);
+      L += s_l[w * kMaxRows + n] * sw;
+      A += s_acc[(w * M + n) * kHeadDim + d] * sw;
+    }
+    if (p.splits == 1) {
+      if (n < rows) {
+        const int t = q0 + n / p.G;
+        const int hh = h * p.G + n % p.G;
+        p.out[p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d] = f32_to_bf16(A / L);
+      }
+    } else {
+      float* part = p.partial + ((grp * p.splits + split) * kMaxRows + n) * kPartStride;
+      part[2 + d] = A;
+      if (d == 0) {
+        part[0] = mt;
+        part[1] = L;
+      }
+    }
+  }
+  if (p.splits == 1) return;
+
+  // ---- last workgroup of this (layer, head, group) merges the splits -------
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = atomicAdd(&p.counters[grp], 1);
+    s_last = (prev == p.splits - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  for (int idx = threadIdx.x; idx < M * kHeadDim; idx += kAttendThreads) {
+    const int n = idx / kHeadDim, d = idx % kHeadDim;
+    if (n >= rows) continue;
+    const float* base = p.partial + (grp * p.splits * kMaxRows + n) * kPartStride;
+    float mt = -INFINITY;
+    for (int s = 0; s < p.splits; ++s) mt = fmaxf(mt, __builtin_nontemporal_load(base + s * kMaxRows * kPartStride));
+    float L = 0.0f, A = 0.0f;
+    for (int s = 0; s < p.splits; ++s) {
+      const float* ps = base + s * kMaxRows * kPartStride;
+      const float ms = __builtin_nontemporal_load(ps);
+      const float sw = (ms == -INFINITY) ? 0.0f : exp2f(ms - mt);
+      L += __builtin_nontemporal_load(ps + 1) * sw;
+      A += __builtin_nontemporal_load(ps + 2 + d) * sw;
+    }
+    const int t = q0 + n / p.G;
+    const int hh = h * p.G + n % p.G;
+    p.out[p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d] = f32_to_bf16(A / L);
+  }
+  if (threadIdx.x == 0) atomicExch(&p.counters[grp], 0);
+}
+
+template <int FMT>
+int launch_fmt(int M, dim3 grid, hipStream_t s, const AttendParams& p) {
+  switch (M) {
+    case 4: hipLaunchKernelGGL((attend_kernel<FMT, 4>), grid, dim3(kAttendThreads), 0, s, p); return 0;
+    case 8: hipLaunchKernelGGL((attend_kernel<FMT, 8>), grid, dim3(kAttendThreads), 0, s, p); return 0;
+    case 16: hipLaunchKernelGGL((attend_kernel<FMT, 16>), grid, dim3(kAttendThreads), 0, s, p); return 0;
+    default: return -1;
+  }
+}
+
+// Query rows per group and the template row count for a given (tq, G).
+void group_shape(int tq, int G, int* qpg, int* M) {
+  int per = kMaxRows / G;          // queries that fit one MFMA tile
+  if (per > tq) per = tq;
+  *qpg = per;
+  const int rows = per * G;
+  *M = rows <= 4 ? 4 : (rows <= 8 ? 8 : 16);
+}
+
+}  // namespace
+}  // namespace nkv
+
+using namespace nkv;
+
+extern "C" int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads, int num_heads,
+                                               int tq, int splits) {
+  if (num_layers < 1 || num_kv_heads < 1 || num_heads < num_kv_heads || tq < 1 || splits < 1) return 0;
+  int qpg, M;
+  group_shape(tq, num_heads / num_kv_heads, &qpg, &M);
+  const int64_t nqg = (tq + qpg - 1) / qpg;
+  return static_cast<int64_t>(num_layers) * num_kv_heads * nqg * splits * kMaxRows * kPartStride;
+}
+
+extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
+                          int64_t q_layer_stride, int tq, const uint16_t* k_new,
+                          const uint16_t* v_new, int64_t kv_layer_stride, int n_chunk,
+                          int new_slot, int write_slot, const int32_t* ids,
+                          int64_t ids_layer_stride, int n_hist, const uint8_t* allowed,
+                          int sink_len, int ring_base, int rec_lo, int rec_len, float scale,
+                          int splits, float* partial_ws, int32_t* counters, uint16_t* out,
+                          void* stream) {
+  int rc = check_store(st, layer0, num_layers);
+  if (rc != NKV_OK) return rc;
+  const int G = st->num_heads / st->num_kv_heads;
+  const int R = st->recent_tokens;
+  NKV_CHECK_ARG(q != nullptr && out != nullptr, "nkv_attend: q and out must be non-NULL");
+  NKV_CHECK_ARG(tq >= 1 && tq <= 65536, "nkv_attend: tq must be in [1, 65536] (got %d)", tq);
+  NKV_CHECK_ARG(n_hist >= 0 && n_hist <= 4096, "nkv_attend: n_hist must be in [0, 4096] (got %d)", n_hist);
+  NKV_CHECK_ARG(n_hist == 0 || ids != nullptr, "nkv_attend: ids is NULL but n_hist=%d", n_hist);
+  NKV_CHECK_ARG(sink_len >= 0 && sink_len <= st->sink_tokens, "nkv_attend: sink_len %d outside [0, %d]",
+                sink_len, st->sink_tokens);
+  NKV_CHECK_ARG(rec_len >= 0 && rec_lo >= 0 && rec_lo + rec_len <= R,
+                "nkv_attend: recent range [%d, %d) outside [0, %d)", rec_lo, rec_lo + rec_len, R);
+  NKV_CHECK_ARG(ring_base >= 0 && ring_base < R, "nkv_attend: ring_base %d outside [0, %d)", ring_base, R);
+  NKV_CHECK_ARG(n_chunk >= 0 && (n_chunk == 0 || n_chunk == tq),
+                "nkv_attend: a causal chunk must have one token per query (n_chunk=%d, tq=%d)", n_chunk, tq);
+  NKV_CHECK_ARG(new_slot < 0 || (new_slot >= rec_lo && new_slot < rec_lo + rec_len),
+                "nkv_attend: new_slot %d outside the attended recent range", new_slot);
+  NKV_CHECK_ARG((new_slot < 0) == (write_slot < 0),
+                "nkv_attend: new_slot and write_slot must both be set or both be -1");
+  NKV_CHECK_ARG(write_slot < 0 || (write_slot < R && (ring_base + new_slot) % R == write_slot),
+                "nkv_attend: write_slot %d must be the physical slot of new_slot", write_slot);
+  NKV_CHECK_ARG((n_chunk == 0 && new_slot < 0) || (k_new != nullptr && v_new != nullptr),
+                "nkv_attend: k_new/v_new are NULL but new tokens are attended");
+  NKV_CHECK_ARG(!(n_chunk > 0 && new_slot >= 0), "nkv_attend: use either new_slot (decode) or a chunk (verify)");
+  NKV_CHECK_ARG(splits >= 1 && splits <= 64, "nkv_attend: splits must be in [1, 64] (got %d)", splits);
+  NKV_CHECK_ARG(splits == 1 || (partial_ws != nullptr && counters != nullptr),
+                "nkv_attend: splits > 1 needs partial_ws and counters");
+  const int n_sink_seg = (sink_len + kBlock - 1) / kBlock;
+  const int n_rec_seg = (rec_len + kBlock - 1) / kBlock;
+  const int n_chunk_seg = (n_chunk + kBlock - 1) / kBlock;
+  const int nseg = n_hist + n_sink_seg + n_rec_seg + n_chunk_seg;
+  NKV_CHECK_ARG(nseg >= 1, "nkv_attend: nothing to attend");
+
+  AttendParams p;
+  const int64_t hist_ls = static_cast<int64_t>(st->num_kv_heads) * st->cap_blocks * kBlock * kHeadDim;
+  const int64_t elem = st->kv_format == NKV_KV_BF16 ? 2 : 1;
+  p.hist_k = static_cast<const char*>(st->hist_k) + layer0 * hist_ls * elem;
+  p.hist_v = static_cast<const char*>(st->hist_v) + layer0 * hist_ls * elem;
+  p.hist_ls = hist_ls;
+  p.sink_ls = static_cast<int64_t>(st->num_kv_heads) * st->sink_tokens * kHeadDim;
+  p.sink_k = st->sink_k ? static_cast<const uint16_t*>(st->sink_k) + layer0 * p.sink_ls : nullptr;
+  p.sink_v = st->sink_v ? static_cast<const uint16_t*>(st->sink_v) + layer0 * p.sink_ls : nullptr;
+  p.rec_ls = static_cast<int64_t>(st->num_kv_heads) * R * kHeadDim;
+  p.rec_k = static_cast<uint16_t*>(st->recent_k) + layer0 * p.rec_ls;
+  p.rec_v = static_cast<uint16_t*>(st->recent_v) + layer0 * p.rec_ls;
+  p.k_scale = st->k_scale ? st->k_scale + static_cast<int64_t>(layer0) * st->num_kv_heads * kHeadDim : nullptr;
+  p.v_scale = st->v_scale ? st->v_scale + static_cast<int64_t>(layer0) * st->num_kv_heads * st->cap_blocks : nullptr;
+  const int64_t ts_ls = static_cast<int64_t>(st->num_kv_heads) * st->cap_blocks * kBlock;
+  p.k_tscale = st->k_tscale ? st->k_tscale + layer0 * ts_ls : nullptr;
+  p.v_tscale = st->v_tscale ? st->v_tscale + layer0 * ts_ls : nullptr;
+  p.q = q;
+  p.q_ls = q_layer_stride;
+  p.k_new = k_new;
+  p.v_new = v_new;
+  p.kv_ls = kv_layer_stride;
+  p.ids = ids;
+  p.ids_ls = ids_layer_stride;
+  p.allowed = allowed;
+  p.partial = partial_ws;
+  p.counters = counters;
+  p.out = out;
+  p.hkv = st->num_kv_heads;
+  p.G = G;
+  p.cap = st->cap_blocks;
+  p.S = st->sink_tokens;
+  p.R = R;
+  p.tq = tq;
+  int qpg, M;
+  group_shape(tq, G, &qpg, &M);
+  p.qpg = qpg;
+  p.nqg = (tq + qpg - 1) / qpg;
+  p.n_chunk = n_chunk;
+  p.new_slot = new_slot;
+  p.write_slot = write_slot;
+  p.n_hist = n_hist;
+  p.sink_len = sink_len;
+  p.ring_base = ring_base;
+  p.rec_lo = rec_lo;
+  p.rec_len = rec_len;
+  p.n_sink_seg = n_sink_seg;
+  p.n_rec_seg = n_rec_seg;
+  p.nseg = nseg;
+  p.splits = splits;
+  p.scale_log2 = scale * 1.4426950408889634f;
+
+  dim3 grid(splits, st->num_kv_heads, num_layers * p.nqg);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int bad = 0;
+  switch (st->kv_format) {
+    case NKV_KV_BF16: bad = launch_fmt<NKV_KV_BF16>(M, grid, s, p); break;
+    case NKV_KV_INT8_CHANNEL: bad = launch_fmt<NKV_KV_INT8_CHANNEL>(M, grid, s, p); break;
+    case NKV_KV_INT8_TOKEN: bad = launch_fmt<NKV_KV_INT8_TOKEN>(M, grid, s, p); break;
+    default: bad = -1;
+  }
+  NKV_CHECK_SUPPORTED(bad == 0, "nkv_attend: unsupported row count %d", M);
+  return launch_status("nkv_attend");
+}

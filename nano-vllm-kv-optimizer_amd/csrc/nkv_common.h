@@ -1,0 +1,80 @@
+// Shared helpers for the NanoKV gfx950 kernels: bf16 conversions, the
+// per-thread error message, and argument-check macros used by every entry
+// point of include/nanokv.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+#include "../../include/nanokv.h"
+
+namespace nkv {
+
+constexpr int kHeadDim = 128;   // D: fixed by the MFMA / lane tilings
+constexpr int kBlock = 64;      // B: tokens per history block
+constexpr int kWave = 64;       // CDNA wavefront width
+
+// ---------------------------------------------------------------- errors --
+void set_error(const char* fmt, ...);
+
+#define NKV_CHECK_ARG(cond, ...)                  \
+  do {                                            \
+    if (!(cond)) {                                \
+      ::nkv::set_error(__VA_ARGS__);              \
+      return NKV_ERR_ARG;                         \
+    }                                             \
+  } while (0)
+
+#define NKV_CHECK_SUPPORTED(cond, ...)            \
+  do {                                            \
+    if (!(cond)) {                                \
+      ::nkv::set_error(__VA_ARGS__);              \
+      return NKV_ERR_UNSUPPORTED;                 \
+    }                                             \
+  } while (0)
+
+// Launch-status check after a kernel enqueue.
+int launch_status(const char* what);
+
+// Validate the fields of a store descriptor that every entry point relies on.
+int check_store(const nkv_store* st, int layer0, int num_layers);
+
+// ------------------------------------------------------------ bf16 / fp16 --
+__device__ __forceinline__ float bf16_lo(uint32_t packed) {
+  return __uint_as_float(packed << 16);
+}
+__device__ __forceinline__ float bf16_hi(uint32_t packed) {
+  return __uint_as_float(packed & 0xffff0000u);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+// fp32 -> bf16, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// Monotone uint32 key of an fp32 score: larger score -> larger key.
+// -0.0 is folded onto +0.0; every NaN maps to the canonical quiet NaN, which
+// sorts above +inf (torch.topk's NaN convention).
+__device__ __forceinline__ uint32_t score_key(float s) {
+  s = s + 0.0f;
+  uint32_t u = __float_as_uint(s);
+  if ((u & 0x7fffffffu) > 0x7f800000u) u = 0x7fc00000u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_score(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+
+}  // namespace nkv

@@ -1,0 +1,820 @@
+"""MI355X-native M12 sparse layer runtime.
+
+Drop-in for ``nanovllm/sparse/m12_runtime.py`` of the reference: the same
+``M12Config`` fields and validation errors, and an ``M12LayerRuntime`` with
+the same call surface (``decode``, ``prefill_first``, ``prefill_chunk``,
+``verify_tokens``, ``commit_verified``, ``rollback_verified``, ``reset``,
+``reserve_blocks``, ``_gpu_select``, ``_gpu_select_per_query``,
+``_build_reps_gpu``) and state attributes (``nblocks_filled``,
+``valid_len``, ``prefill_len``, ``reps_gpu``, ``protected_blocks``,
+``last_block_ids``, ``timings`` ...), so ``Attention.forward``
+(nanovllm/layers/attention.py:64-99) and the engine wiring
+(nanovllm/engine/model_runner.py:134-184) can use it unchanged.
+
+What differs by design: the history stays in HBM (no host gather, no H2D
+pack); selected block ids stay on the device during decode and are copied to
+the host only when ``last_block_ids`` / ``ids_history`` is read; every
+operation is a hand-written gfx950 HIP kernel behind the C ABI of
+include/nanokv.h.  ``M12ModelRuntime`` runs the same kernels for all layers of
+a model in one launch per stage.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from time import perf_counter
+
+import torch
+
+from .. import _lib
+from ..store import SparseKVStore, query_summaries
+
+# ---------------------------------------------------------------------------
+# Host-side helpers (same contracts as the reference's module functions)
+# ---------------------------------------------------------------------------
+
+
+def prefill_recent_slice(valid_len: int, sink_tokens: int, recent_tokens: int):
+    """(buffer_start, buffer_offset, length) of the recent buffer not also sink.
+
+    Reference: m12_runtime.py:32-50.
+    """
+    assert valid_len >= 0
+    assert sink_tokens >= 0
+    assert recent_tokens >= 0
+    sink_len = min(sink_tokens, valid_len)
+    buffer_len = min(recent_tokens, valid_len)
+    buffer_start = valid_len - buffer_len
+    include_start = max(sink_len, buffer_start)
+    return buffer_start, include_start - buffer_start, valid_len - include_start
+
+
+def prefill_query_summaries(q: torch.Tensor, nsegments: int) -> torch.Tensor:
+    """Segment means of a prefill chunk's queries, [nseg, Hq, D] bf16, on device.
+
+    Reference: m12_runtime.py:53-67 (``q.mean(dim=0, keepdim=True)`` for one
+    segment, ``tensor_split`` means otherwise).  Each mean is the bf16
+    round-to-nearest-even of the exact mean.
+    """
+    assert q.ndim == 3, "q must be [T, Hq, D]"
+    assert nsegments > 0
+    return query_summaries(q.unsqueeze(0).contiguous(), nsegments)[0]
+
+
+def dynamic_top_k_from_scores(top_scores: torch.Tensor, max_k: int, target_mass: float) -> int:
+    """Decode budget from half, three quarters or all candidates.
+
+    Reference: m12_runtime.py:70-95 (host-side, CPU scores).
+    """
+    assert top_scores.ndim == 1 and top_scores.device.type == "cpu"
+    assert 0.0 < target_mass <= 1.0 and max_k > 0
+    count = top_scores.numel()
+    if count < max_k or count <= 1 or not bool(torch.isfinite(top_scores).all()):
+        return count
+    scale = top_scores.std(unbiased=False)
+    if float(scale) <= 1e-6:
+        return count
+    weights = torch.softmax((top_scores - top_scores[0]) / scale, dim=0)
+    cumulative = weights.cumsum(dim=0)
+    choices = sorted({max(1, (max_k + 1) // 2), max(1, (3 * max_k + 3) // 4), max_k})
+    for choice in choices:
+        if float(cumulative[choice - 1]) >= target_mass:
+            return choice
+    return max_k
+
+
+@dataclass
+class M12Config:
+    """Same fields, defaults and validation as the reference (m12_runtime.py:98-166).
+
+    Extra fields of this build: ``quant_scale_layout`` ("channel_block" = the
+    reference's K-per-channel / V-per-block fp32 scales, "token" = per-token
+    per-KV-head fp16 scales) and ``attend_splits`` (workgroups per KV head in
+    the attention kernel; None = automatic).  ``use_index_select``,
+    ``decode_kv_pipeline`` and ``gather_sort``'s gather-locality purpose
+    belong to the host-offload design and do not change the HBM path
+    (``gather_sort`` still orders ``last_block_ids`` ascending).
+    """
+    block_size: int = 64
+    r: int = 4
+    recent_tokens: int = 512
+    sink_tokens: int = 64
+    top_k_blocks: int = 32
+    prefill_top_k_blocks: int | None = None
+    decode_top_k_blocks: int | None = None
+    dynamic_top_k: bool = False
+    dynamic_top_k_mass: float = 0.90
+    decode_relative_a: float | None = None
+    decode_relative_max_blocks: int = 48
+    decode_relative_union: bool = False
+    decode_query_window: int = 1
+    fused_selector: bool = False
+    quant_history: bool = False
+    verify_union_blocks: int = 0
+    fused_dequant: bool = False
+    gather_sort: bool = False
+    max_model_len: int = 131072
+    num_heads: int = 32
+    num_kv_heads: int = 8
+    head_dim: int = 128
+    dtype: torch.dtype = torch.bfloat16
+    scale: float = 128.0 ** -0.5
+    use_index_select: bool = True
+    decode_kv_pipeline: bool = False
+    selector_cuda_graph: bool = False
+    selector_static_mask: bool = False
+    check_finite_outputs: bool = False
+    prefill_query_segments: int = 1
+    prefill_attention_backend: str = "torch"
+    prefill_adapter: object | None = None
+    quant_scale_layout: str = "channel_block"
+    attend_splits: int | None = None
+
+    def __post_init__(self):
+        if self.decode_kv_pipeline and not self.use_index_select:
+            raise ValueError("decode_kv_pipeline requires use_index_select")
+        for name, budget in (
+            ("prefill_top_k_blocks", self.prefill_top_k_blocks),
+            ("decode_top_k_blocks", self.decode_top_k_blocks),
+        ):
+            if budget is not None and not 1 <= budget <= self.top_k_blocks:
+                raise ValueError(f"{name} must be in [1, top_k_blocks]")
+        if self.decode_relative_a is not None:
+            if not 0.0 < self.decode_relative_a < 1.0:
+                raise ValueError("decode_relative_a must be in (0, 1)")
+            if self.decode_relative_max_blocks < 1:
+                raise ValueError("decode_relative_max_blocks must be >= 1")
+        if self.decode_query_window < 1:
+            raise ValueError("decode_query_window must be >= 1")
+        if self.fused_dequant and not self.quant_history:
+            raise ValueError("fused_dequant requires quant_history")
+        if self.quant_scale_layout not in ("channel_block", "token"):
+            raise ValueError("quant_scale_layout must be 'channel_block' or 'token'")
+        if self.attend_splits is not None and not 1 <= self.attend_splits <= 64:
+            raise ValueError("attend_splits must be in [1, 64]")
+
+    @property
+    def kv_format(self) -> str:
+        if not self.quant_history:
+            return "bf16"
+        return "int8" if self.quant_scale_layout == "channel_block" else "int8_token"
+
+
+def _check_hip_shapes(cfg: M12Config) -> None:
+    if cfg.dtype != torch.bfloat16:
+        raise ValueError("the HIP runtime computes on bfloat16 K/V/q (cfg.dtype must be torch.bfloat16)")
+    if cfg.head_dim != 128 or cfg.block_size != 64:
+        raise ValueError("the gfx950 kernels are built for head_dim=128 and block_size=64")
+    if cfg.num_heads % cfg.num_kv_heads or cfg.num_heads // cfg.num_kv_heads not in (1, 2, 4, 8, 16):
+        raise ValueError("num_heads / num_kv_heads must be 1, 2, 4, 8 or 16")
+    if cfg.r not in (1, 2, 4, 8):
+        raise ValueError("r must be 1, 2, 4 or 8")
+
+
+# ---------------------------------------------------------------------------
+# Sequence bookkeeping + kernel calls over a range of layers
+# ---------------------------------------------------------------------------
+
+
+class _SparseCore:
+    """One sequence's sparse-attention state over layers [layer0, layer0 + nl).
+
+    Bookkeeping follows M12LayerRuntime (m12_runtime.py:169-1346); the data
+    lives in a SparseKVStore.  All layers of the range share lengths,
+    protected set and ring position, which is what a model's layers see.
+    """
+
+    def __init__(self, cfg: M12Config, store: SparseKVStore, layer0: int, nl: int):
+        self.cfg = cfg
+        self.store = store
+        self.layer0 = layer0
+        self.nl = nl
+        self.device = store.device
+        self.max_blocks = store.cap_blocks
+        self.valid_len = 0
+        self.prefill_len = 0
+        self.nblocks_filled = 0
+        self.ring_start = 0
+        self.protected_blocks: set[int] = set()
+        self.k_scale_set = False
+        self.pending = None
+        self._prot_key = None
+        self._prot_dev = None
+        self._ws: dict[str, torch.Tensor] = {}
+        self._counters = torch.zeros(0, dtype=torch.int32, device=self.device)
+
+    # -- workspaces ---------------------------------------------------------
+    def _buf(self, name: str, numel: int, dtype) -> torch.Tensor:
+        t = self._ws.get(name)
+        if t is None or t.numel() < numel or t.dtype != dtype:
+            t = torch.empty(max(numel, 1), dtype=dtype, device=self.device)
+            self._ws[name] = t
+        return t[:numel]
+
+    def _counter_buf(self, n: int) -> torch.Tensor:
+        if self._counters.numel() < n:
+            self._counters = torch.zeros(n, dtype=torch.int32, device=self.device)
+        return self._counters
+
+    def reset(self) -> None:
+        self.valid_len = 0
+        self.prefill_len = 0
+        self.nblocks_filled = 0
+        self.protected_blocks.clear()
+        self.k_scale_set = False
+        self.pending = None
+        self._prot_key = None
+
+    # -- store (m12_runtime.py:420-513) --------------------------------------
+    def store_kv(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        """k, v: [nl, T, Hkv, D] bf16 device tensors."""
+        cfg = self.cfg
+        B, R = cfg.block_size, cfg.recent_tokens
+        T = k.shape[1]
+        assert T >= 2
+        k = k.contiguous()
+        v = v.contiguous()
+        nblk = (T + B - 1) // B
+        start = self.nblocks_filled
+        need = start + nblk
+        if need > self.max_blocks:
+            raise ValueError(f"history of {need} blocks exceeds max_model_len "
+                             f"({self.max_blocks} blocks)")
+        compute_k_scale = cfg.kv_format == "int8" and not self.k_scale_set
+        self.store.store_chunk(self.layer0, k, v, start, compute_k_scale, self.prefill_len == 0)
+        self.k_scale_set = self.k_scale_set or compute_k_scale
+        self.store.build_reps(self.layer0, k, start)
+        recent_len = min(R, self.valid_len + T)
+        if T >= recent_len:
+            self.store.recent_update(self.layer0, self.nl, k, v, T - recent_len, recent_len,
+                                     self.ring_start, 0, 0)
+        else:
+            carry = recent_len - T
+            old = min(R, self.valid_len)
+            self.store.recent_update(self.layer0, self.nl, k, v, 0, T, self.ring_start, old, carry)
+        self.valid_len += T
+        self.prefill_len += T
+        self.nblocks_filled = need
+        n_recent_blocks = R // B
+        self.protected_blocks = {0} | set(range(max(1, need - n_recent_blocks), need))
+
+    def commit(self, n: int) -> None:
+        """commit_verified (m12_runtime.py:777-803)."""
+        if n <= 0:
+            self.pending = None
+            return
+        k, v = self.pending
+        T = int(n)
+        R = self.cfg.recent_tokens
+        old = min(R, self.valid_len)
+        new = min(R, self.valid_len + T)
+        if T >= R:
+            self.store.recent_update(self.layer0, self.nl, k, v, T - R, R, self.ring_start, 0, 0)
+        else:
+            carry = new - T
+            self.store.recent_update(self.layer0, self.nl, k, v, 0, T, self.ring_start, old, carry)
+        self.valid_len += T
+        self.pending = None
+
+    # -- selection (m12_runtime.py:959-1087) ---------------------------------
+    def protected_dev(self):
+        nb = self.nblocks_filled
+        ids = tuple(sorted(p for p in self.protected_blocks if 0 <= p < nb))
+        if ids != self._prot_key:
+            self._prot_dev = torch.tensor(list(ids) or [0], dtype=torch.int32, device=self.device)
+            self._prot_key = ids
+        return self._prot_dev, len(ids)
+
+    def effective_k(self, requested: int) -> int:
+        nb = self.nblocks_filled
+        n_prot = len([p for p in self.protected_blocks if 0 <= p < nb])
+        return min(int(requested), max(1, nb - n_prot))
+
+    def select(self, q: torch.Tensor, requested: int, *, per_query: bool = False,
+               order: int = _lib.NKV_ORDER_SCORE_DESC):
+        """q: [nl, nq, Hq, D] bf16 -> (ids [nl, nq', requested] int32, vals, k_eff)."""
+        nb = self.nblocks_filled
+        if nb <= 0:
+            raise ValueError("selection needs at least one history block")
+        if requested < 1:
+            raise ValueError("the block budget must be >= 1")
+        q = q.contiguous()
+        nl, nq = q.shape[0], q.shape[1]
+        nqo = nq if per_query else 1
+        prot, n_prot = self.protected_dev()
+        scores = self._buf("scores", nl * nqo * nb, torch.float32)
+        ids = self._buf("ids", nl * nqo * requested, torch.int32).view(nl, nqo, requested)
+        vals = self._buf("vals", nl * nqo * requested, torch.float32).view(nl, nqo, requested)
+        self.store.select(self.layer0, q, nb, prot, n_prot, requested, order, per_query,
+                          scores, ids, vals)
+        self._last_scores = scores.view(nl, nqo, nb)
+        return ids, vals, self.effective_k(requested)
+
+    # -- attention ------------------------------------------------------------
+    def _splits(self, nseg: int, nqg: int) -> int:
+        if self.cfg.attend_splits is not None:
+            return self.cfg.attend_splits
+        want = -(-2048 // (self.store.num_kv_heads * self.nl * nqg))
+        return max(1, min(-(-nseg // 4), want, 64))
+
+    def attend(self, q, k_new, v_new, *, n_chunk, new_slot, write_slot, ids, ids_stride,
+               n_hist, allowed, sink_len, ring_base, rec_lo, rec_len):
+        cfg = self.cfg
+        nl, tq = q.shape[0], q.shape[1]
+        g = cfg.num_heads // cfg.num_kv_heads
+        qpg = min(tq, max(1, 16 // g))
+        nqg = -(-tq // qpg)
+        nseg = n_hist + -(-sink_len // 64) + -(-rec_len // 64) + -(-n_chunk // 64)
+        splits = self._splits(nseg, nqg)
+        out = torch.empty_like(q)
+        part = self._buf("partial", self.store.attend_workspace_floats(nl, tq, splits), torch.float32)
+        counters = self._counter_buf(nl * self.store.num_kv_heads * nqg)
+        self.store.attend(self.layer0, q, k_new, v_new, n_chunk, new_slot, write_slot, ids,
+                          ids_stride, n_hist, allowed, sink_len, ring_base, rec_lo, rec_len,
+                          cfg.scale, splits, part, counters, out)
+        return out
+
+    def decode_attend(self, q, k, v, ids, ids_stride, n_hist):
+        """Decode step 1 + 3-5 (m12_runtime.py:1164-1320): q [nl,1,Hq,D], k/v [nl,1,Hkv,D]."""
+        cfg = self.cfg
+        R = cfg.recent_tokens
+        sink_len = min(cfg.sink_tokens, self.valid_len)
+        rec_len = min(R, self.valid_len + 1)
+        out = self.attend(q.contiguous(), k.contiguous(), v.contiguous(), n_chunk=0,
+                          new_slot=R - 1, write_slot=self.ring_start, ids=ids,
+                          ids_stride=ids_stride, n_hist=n_hist, allowed=None,
+                          sink_len=sink_len, ring_base=(self.ring_start + 1) % R,
+                          rec_lo=R - rec_len, rec_len=rec_len)
+        self.ring_start = (self.ring_start + 1) % R
+        self.valid_len += 1
+        return out, sink_len, rec_len
+
+    def chunk_attend(self, q, k, v, ids, ids_stride, n_hist, allowed=None):
+        """[selected | sink | previous recent | chunk (causal)] (m12_runtime.py:592-639, :725-758)."""
+        cfg = self.cfg
+        sink_len = min(cfg.sink_tokens, self.valid_len)
+        _, off, ln = prefill_recent_slice(self.valid_len, cfg.sink_tokens, cfg.recent_tokens)
+        out = self.attend(q.contiguous(), k.contiguous(), v.contiguous(), n_chunk=q.shape[1],
+                          new_slot=-1, write_slot=-1, ids=ids, ids_stride=ids_stride,
+                          n_hist=n_hist, allowed=allowed, sink_len=sink_len,
+                          ring_base=self.ring_start, rec_lo=off, rec_len=ln)
+        return out, sink_len, ln
+
+
+# ---------------------------------------------------------------------------
+# Per-layer runtime (the reference's class surface)
+# ---------------------------------------------------------------------------
+
+
+class M12LayerRuntime:
+    """Per-layer sparse runtime on the HBM store (m12_runtime.py:169-1346)."""
+
+    def __init__(self, layer_id: int, cfg: M12Config, *, store: SparseKVStore | None = None,
+                 store_layer: int | None = None, device=None):
+        _check_hip_shapes(cfg)
+        self.layer_id = layer_id
+        self.cfg = cfg
+        self.enabled = True
+        B = cfg.block_size
+        self.max_blocks = (cfg.max_model_len + B - 1) // B
+        self.groups_per_kv = cfg.num_heads // cfg.num_kv_heads
+        if store is None:
+            store = SparseKVStore(
+                1, num_heads=cfg.num_heads, num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim,
+                block_size=B, r=cfg.r, cap_blocks=self.max_blocks, sink_tokens=cfg.sink_tokens,
+                recent_tokens=cfg.recent_tokens, kv_format=cfg.kv_format, device=device)
+            store_layer = 0
+        elif store_layer is None:
+            store_layer = layer_id
+        self.store = store
+        self.store_layer = store_layer
+        self._core = _SparseCore(cfg, store, store_layer, 1)
+        self.quant_history = cfg.quant_history
+        # [Hkv, max_blocks, r, D] view of this layer's representatives
+        self.reps_gpu = store.reps[store_layer]
+        self.timings: dict[str, float] = {}
+        self.last_prefill_query_summaries = 0
+        self.prefill_cpu_gather_ms = 0.0
+        self.record_ids = False
+        self.ids_history: list[list[int]] = []
+        self.record_q = False
+        self.q_history: list[torch.Tensor] = []
+        self.verify_mode = False
+        self.verify_lossless = False
+        self.last_verify_timings: dict = {}
+        self.selector_graph_setup_ms = 0.0
+        self.selector_graph_builds = 0
+        self.profile_cuda_stages = False
+        self.profile_torch_stages = False
+        self.profile_nsys_stages = False
+        self.cuda_stage_events: dict = {}
+        self._q_window: list[torch.Tensor] = []
+        self._last_ids_dev: torch.Tensor | None = None
+        self._last_ids_cpu: torch.Tensor | None = None
+        self._last_prefill_ids: torch.Tensor | None = None
+        self._last_verify_ids: torch.Tensor | None = None
+
+    # -- state attributes ------------------------------------------------------
+    @property
+    def nblocks_filled(self) -> int:
+        return self._core.nblocks_filled
+
+    @nblocks_filled.setter
+    def nblocks_filled(self, n: int) -> None:
+        self._core.nblocks_filled = int(n)
+
+    @property
+    def valid_len(self) -> int:
+        return self._core.valid_len
+
+    @valid_len.setter
+    def valid_len(self, n: int) -> None:
+        self._core.valid_len = int(n)
+
+    @property
+    def prefill_len(self) -> int:
+        return self._core.prefill_len
+
+    @prefill_len.setter
+    def prefill_len(self, n: int) -> None:
+        self._core.prefill_len = int(n)
+
+    @property
+    def protected_blocks(self) -> set:
+        return self._core.protected_blocks
+
+    @protected_blocks.setter
+    def protected_blocks(self, s) -> None:
+        self._core.protected_blocks = set(s)
+
+    def _ids_to_cpu(self, ids_dev):
+        return None if ids_dev is None else ids_dev.to("cpu", torch.int64)
+
+    @property
+    def last_block_ids(self) -> torch.Tensor | None:
+        """Selected ids of the last step as a CPU int64 tensor (copied on first read)."""
+        if self._last_ids_cpu is None and self._last_ids_dev is not None:
+            self._last_ids_cpu = self._ids_to_cpu(self._last_ids_dev)
+        return self._last_ids_cpu
+
+    @property
+    def last_prefill_block_ids(self) -> torch.Tensor | None:
+        return self._last_prefill_ids
+
+    @property
+    def last_verify_block_ids(self) -> torch.Tensor | None:
+        return self._last_verify_ids
+
+    def _set_last_ids(self, ids_dev: torch.Tensor) -> None:
+        self._last_ids_dev = ids_dev
+        self._last_ids_cpu = None
+
+    def reset(self) -> None:
+        """New sequence; buffers (and their contents) are kept (m12_runtime.py:322-349)."""
+        self._core.reset()
+        self._last_ids_dev = self._last_ids_cpu = None
+        self._last_prefill_ids = self._last_verify_ids = None
+        self.timings.clear()
+        self.last_prefill_query_summaries = 0
+        self.prefill_cpu_gather_ms = 0.0
+        self.cuda_stage_events.clear()
+        self.ids_history.clear()
+        self.q_history.clear()
+        self._q_window.clear()
+        self.selector_graph_setup_ms = 0.0
+        self.selector_graph_builds = 0
+
+    def reserve_blocks(self, nblocks: int) -> None:
+        """The HBM history is allocated up front for max_model_len; only validate."""
+        if nblocks > self.max_blocks:
+            raise ValueError(f"{nblocks} blocks exceed max_model_len ({self.max_blocks} blocks)")
+
+    # -- input checks ------------------------------------------------------------
+    def _as_bf16(self, t: torch.Tensor, name: str) -> torch.Tensor:
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be bfloat16 (got {t.dtype})")
+        return t.contiguous()
+
+    # -- representatives / store -------------------------------------------------
+    def _build_reps_gpu(self, k_blocks: torch.Tensor, start: int, nblocks: int) -> None:
+        """k_blocks [N, B, Hkv, D] -> reps_gpu[:, start:start+N] (m12_runtime.py:354-395)."""
+        kb = self._as_bf16(k_blocks[:nblocks], "k_blocks")
+        n, b, hkv, d = kb.shape
+        self.store.build_reps(self.store_layer, kb.reshape(1, n * b, hkv, d), start)
+
+    def _store_kv(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        self._core.store_kv(self._as_bf16(k, "k").unsqueeze(0), self._as_bf16(v, "v").unsqueeze(0))
+
+    def prefill_first(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> dict:
+        """Store the first chunk; its dense attention is the caller's (m12_runtime.py:518-523)."""
+        assert self.prefill_len == 0, "prefill_first called after history exists"
+        self._store_kv(k, v)
+        return {"nblocks": self.nblocks_filled, "valid_len": self.valid_len}
+
+    # -- selection -------------------------------------------------------------------
+    def _select_dev(self, q3: torch.Tensor, requested: int, order: int):
+        ids, vals, k = self._core.select(q3.unsqueeze(0), requested, order=order)
+        return ids, vals, k
+
+    def _gpu_select(self, q: torch.Tensor, *, dynamic: bool = False, budget: int | None = None,
+                    use_graph: bool = False, use_static_mask: bool = False,
+                    use_relative: bool = False):
+        """Block scores + Top-K; returns (block_ids_cpu [K] int64, info).
+
+        Reference: m12_runtime.py:959-1055.  The graph and static-mask options
+        select the same kernel (one score launch + one Top-K launch).
+        """
+        cfg = self.cfg
+        if q.ndim == 2:
+            q = q.unsqueeze(0)
+        assert q.ndim == 3 and q.shape[1:] == (cfg.num_heads, cfg.head_dim)
+        q = self._as_bf16(q, "q")
+        if use_relative and (use_graph and cfg.selector_cuda_graph):
+            raise ValueError("relative-threshold selection requires the flat GPU path")
+        requested_k = cfg.top_k_blocks if budget is None else budget
+        t_enq = perf_counter()
+        ids_cpu, vals_cpu, k = self._select_host(q, requested_k, use_relative)
+        t_d2h = perf_counter()
+        chosen = k
+        if dynamic and cfg.dynamic_top_k and k == requested_k:
+            chosen = dynamic_top_k_from_scores(vals_cpu, requested_k, cfg.dynamic_top_k_mass)
+        if chosen < k:
+            ids_cpu = ids_cpu[:chosen]
+        d2h_ms = (perf_counter() - t_d2h) * 1000.0
+        return ids_cpu, {
+            "d2h_ms": d2h_ms,
+            "enqueue_ms": (t_d2h - t_enq) * 1000.0,
+            "n_selected": chosen,
+            "n_candidates": k,
+            "n_query_summaries": q.shape[0],
+        }
+
+    def _select_host(self, q: torch.Tensor, requested_k: int, use_relative: bool):
+        """Selected ids and scores on the host (score-desc order)."""
+        cfg = self.cfg
+        if not use_relative:
+            ids, vals, k = self._select_dev(q, requested_k, _lib.NKV_ORDER_SCORE_DESC)
+            return ids[0, 0, :k].to("cpu", torch.int64), vals[0, 0, :k].cpu(), k
+        # relative threshold (m12_runtime.py:1015-1031): keep candidates within
+        # ln(a)/scale of the best among the top `cap`, or top-k in union mode.
+        a = cfg.decode_relative_a
+        assert a is not None and 0.0 < a < 1.0
+        nb = self.nblocks_filled
+        n_prot = len([p for p in self.protected_blocks if 0 <= p < nb])
+        avail = nb - n_prot
+        k = min(requested_k, max(1, avail))
+        cap = min(cfg.decode_relative_max_blocks, max(1, avail))
+        req = max(cap, k)
+        ids, vals, keff = self._select_dev(q, req, _lib.NKV_ORDER_SCORE_DESC)
+        order = ids[0, 0, :keff].to("cpu", torch.int64)
+        scores = vals[0, 0, :keff].cpu()
+        threshold = float(scores[0]) + math.log(a) / cfg.scale
+        cand, cs = order[:cap], scores[:cap]
+        above = cs >= threshold
+        if cfg.decode_relative_union:
+            pos = torch.arange(cand.numel()) < k
+            keep = above | pos
+        else:
+            keep = above
+        if not bool(keep.any()):
+            return order[:k], scores[:k], k
+        return cand[keep], cs[keep], int(keep.sum())
+
+    def _gpu_select_per_query(self, q: torch.Tensor, k: int):
+        """Per-query Top-K, union (sorted) and allowed mask (m12_runtime.py:1057-1087)."""
+        cfg = self.cfg
+        if q.ndim == 2:
+            q = q.unsqueeze(0)
+        q = self._as_bf16(q, "q")
+        tq = q.shape[0]
+        if tq > 16:
+            raise ValueError("per-query selection supports at most 16 queries")
+        ids, _, kk = self._core.select(q.unsqueeze(0), int(k), per_query=True)
+        top = ids[0, :, :kk].to("cpu", torch.int64)                 # [Tq, kk]
+        union = torch.unique(top.flatten())
+        pos = torch.searchsorted(union, top.flatten()).reshape(tq, kk)
+        allowed = torch.zeros(tq, union.numel(), dtype=torch.bool)
+        allowed.scatter_(1, pos, True)
+        return union, allowed.to(q.device)
+
+    def diagnose_target_margin(self, q: torch.Tensor, target_block: int) -> dict:
+        """Score margin of one block under the decode selector (m12_runtime.py:1089-1128)."""
+        cfg = self.cfg
+        if q.ndim == 2:
+            q = q.unsqueeze(0)
+        q = self._as_bf16(q, "q")
+        ids, _, k = self._select_dev(q, cfg.top_k_blocks, _lib.NKV_ORDER_SCORE_DESC)
+        scores = self._core._last_scores[0, 0].cpu().clone()
+        nb = self.nblocks_filled
+        prot = [p for p in self.protected_blocks if 0 <= p < nb]
+        if prot:
+            scores[torch.tensor(sorted(prot))] = float("-inf")
+        order = sorted(range(nb), key=lambda i: (-float(scores[i]), i))
+        rank = order.index(int(target_block))
+        return {
+            "target_score": float(scores[int(target_block)]),
+            "cutoff": float(scores[order[k - 1]]),
+            "rank": rank,
+            "nblocks": nb,
+            "in_topk": rank < k,
+        }
+
+    # -- decode (m12_runtime.py:1141-1346) ---------------------------------------------
+    def decode(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, device=None) -> torch.Tensor:
+        """One decode step.  q [1, Hq, D], k/v [1, Hkv, D] bf16 -> o [1, Hq, D] bf16."""
+        cfg = self.cfg
+        assert q.shape[0] == 1 and k.shape[0] == 1
+        q = self._as_bf16(q, "q")
+        k = self._as_bf16(k, "k")
+        v = self._as_bf16(v, "v")
+        if self.record_q:
+            self.q_history.append(q[0].detach().cpu().clone())
+        t0 = perf_counter()
+        if cfg.decode_query_window > 1:
+            self._q_window.append(q[0].detach().clone())
+            while len(self._q_window) > cfg.decode_query_window:
+                self._q_window.pop(0)
+            if len(self._q_window) == 1:
+                q_route = self._q_window[0].unsqueeze(0)
+            else:
+                q_route = prefill_query_summaries(torch.stack(self._q_window, dim=0), 1)
+        else:
+            q_route = q
+        requested = cfg.top_k_blocks if cfg.decode_top_k_blocks is None else cfg.decode_top_k_blocks
+        host_rule = cfg.decode_relative_a is not None or (cfg.dynamic_top_k)
+        if host_rule:
+            ids_cpu, info = self._gpu_select(q_route, dynamic=cfg.dynamic_top_k, budget=requested,
+                                             use_relative=cfg.decode_relative_a is not None)
+            if cfg.gather_sort and ids_cpu.numel() > 1:
+                ids_cpu = ids_cpu.sort().values
+            n_hist = ids_cpu.numel()
+            ids_dev = ids_cpu.to(torch.int32).to(self.store.device).view(1, 1, n_hist)
+            stride = n_hist
+        else:
+            order = _lib.NKV_ORDER_ID_ASC if cfg.gather_sort else _lib.NKV_ORDER_SCORE_DESC
+            ids_dev, _, n_hist = self._select_dev(q_route, requested, order)
+            stride = ids_dev.shape[-1]
+        selector_ms = (perf_counter() - t0) * 1000.0
+        t_a = perf_counter()
+        out, sink_len, rec_len = self._core.decode_attend(
+            q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), ids_dev, stride, n_hist)
+        attn_ms = (perf_counter() - t_a) * 1000.0
+        self._set_last_ids(ids_dev[0, 0, :n_hist])
+        if self.record_ids:
+            self.ids_history.append(self.last_block_ids.tolist())
+        sel_tokens = n_hist * cfg.block_size
+        self.timings = {
+            "selector_ms": selector_ms,
+            "selector_enqueue_ms": selector_ms,
+            "d2h_ms": 0.0,
+            "cpu_gather_ms": 0.0,
+            "h2d_pack_ms": 0.0,
+            "h2d_event_spans_cpu_gather": False,
+            "recent_ms": 0.0,
+            "packed_attn_ms": attn_ms,
+            "selected_tokens": sel_tokens,
+            "total_attend_tokens": sel_tokens + sink_len + rec_len,
+        }
+        o = out[0]
+        if cfg.check_finite_outputs and not bool(torch.isfinite(o).all()):
+            raise RuntimeError("M12 sparse decode output is non-finite")
+        return o
+
+    # -- chunked prefill (m12_runtime.py:528-651) ---------------------------------------
+    def prefill_chunk(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, device=None) -> torch.Tensor:
+        """Later prefill chunk: attention over [selected | sink | prev recent | chunk]."""
+        cfg = self.cfg
+        assert self.prefill_len > 0, "prefill_chunk requires prior history"
+        q = self._as_bf16(q, "q")
+        k = self._as_bf16(k, "k")
+        v = self._as_bf16(v, "v")
+        q_summary = prefill_query_summaries(q, cfg.prefill_query_segments)
+        self.last_prefill_query_summaries = q_summary.shape[0]
+        requested = cfg.top_k_blocks if cfg.prefill_top_k_blocks is None else cfg.prefill_top_k_blocks
+        order = _lib.NKV_ORDER_ID_ASC if cfg.gather_sort else _lib.NKV_ORDER_SCORE_DESC
+        ids_dev, _, n_hist = self._select_dev(q_summary, requested, order)
+        out, _, _ = self._core.chunk_attend(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0),
+                                            ids_dev, ids_dev.shape[-1], n_hist)
+        ids_cpu = ids_dev[0, 0, :n_hist].to("cpu", torch.int64)
+        self._store_kv(k, v)
+        self._last_prefill_ids = ids_cpu.clone()
+        self._last_ids_dev = None
+        self._last_ids_cpu = ids_cpu
+        return out[0]
+
+    # -- speculative verify (m12_runtime.py:656-807) -------------------------------------
+    def verify_tokens(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, device=None) -> torch.Tensor:
+        """One verification pass over Tq new tokens; commit or roll back afterwards."""
+        cfg = self.cfg
+        tq = k.shape[0]
+        assert tq >= 1, "verify needs at least one token"
+        assert self.prefill_len > 0, "verify requires a complete prefill"
+        q = self._as_bf16(q, "q")
+        k = self._as_bf16(k, "k")
+        v = self._as_bf16(v, "v")
+        t0 = perf_counter()
+        allowed_dev = None
+        if self.verify_lossless:
+            union, allowed = self._gpu_select_per_query(q, cfg.top_k_blocks)
+            ids_dev = union.to(torch.int32).to(self.store.device).view(1, 1, -1)
+            n_hist = union.numel()
+            allowed_dev = allowed.to(torch.uint8).contiguous()
+            ids_cpu = union
+        else:
+            ids_dev, _, n_hist = self._select_dev(q, cfg.top_k_blocks, _lib.NKV_ORDER_SCORE_DESC)
+            ids_cpu = None
+        t_sel = perf_counter()
+        out, _, _ = self._core.chunk_attend(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0),
+                                            ids_dev, ids_dev.shape[-1], n_hist, allowed_dev)
+        t_attn = perf_counter()
+        if ids_cpu is None:
+            ids_cpu = ids_dev[0, 0, :n_hist].to("cpu", torch.int64)
+        self.last_verify_timings = {
+            "selector_ms": (t_sel - t0) * 1000.0,
+            "gather_ms": 0.0,
+            "pack_ms": 0.0,
+            "attention_ms": (t_attn - t_sel) * 1000.0,
+            "tokens": int(tq),
+            "blocks": int(n_hist),
+        }
+        self._core.pending = (k.unsqueeze(0), v.unsqueeze(0))
+        self._last_verify_ids = ids_cpu.clone()
+        self._last_ids_dev = None
+        self._last_ids_cpu = ids_cpu
+        return out[0]
+
+    def commit_verified(self, n: int) -> None:
+        """Append the first n pending verified tokens to the recent window."""
+        self._core.commit(n)
+
+    def rollback_verified(self) -> None:
+        """Discard a verification pass without committing anything."""
+        self._core.pending = None
+
+    @property
+    def _pending_k(self):
+        return None if self._core.pending is None else self._core.pending[0][0]
+
+    @property
+    def _pending_v(self):
+        return None if self._core.pending is None else self._core.pending[1][0]
+
+
+# ---------------------------------------------------------------------------
+# All layers of a model at once
+# ---------------------------------------------------------------------------
+
+
+class M12ModelRuntime:
+    """The sparse layer-step for every attention layer of a model, batched.
+
+    One store holds all layers; each stage is one kernel launch over all
+    layers (grid dimension = layer).  Inputs carry a leading layer dimension:
+    q [L, T, Hq, D], k/v [L, T, Hkv, D].  Semantics per layer are exactly
+    those of M12LayerRuntime (all layers share the sequence bookkeeping).
+    """
+
+    def __init__(self, num_layers: int, cfg: M12Config, device=None):
+        _check_hip_shapes(cfg)
+        self.cfg = cfg
+        self.num_layers = num_layers
+        B = cfg.block_size
+        self.max_blocks = (cfg.max_model_len + B - 1) // B
+        self.store = SparseKVStore(
+            num_layers, num_heads=cfg.num_heads, num_kv_heads=cfg.num_kv_heads,
+            head_dim=cfg.head_dim, block_size=B, r=cfg.r, cap_blocks=self.max_blocks,
+            sink_tokens=cfg.sink_tokens, recent_tokens=cfg.recent_tokens,
+            kv_format=cfg.kv_format, device=device)
+        self.core = _SparseCore(cfg, self.store, 0, num_layers)
+        self.last_ids_dev: torch.Tensor | None = None
+        self.last_n_selected = 0
+
+    @property
+    def valid_len(self) -> int:
+        return self.core.valid_len
+
+    @property
+    def nblocks_filled(self) -> int:
+        return self.core.nblocks_filled
+
+    def reset(self) -> None:
+        self.core.reset()
+
+    def prefill(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Store a prefill chunk for every layer: k, v [L, T, Hkv, D] bf16."""
+        self.core.store_kv(k, v)
+
+    def select(self, q: torch.Tensor, budget: int | None = None):
+        """Decode selection for every layer: q [L, 1, Hq, D] -> (ids [L, 1, K], vals, k)."""
+        cfg = self.cfg
+        req = budget or (cfg.top_k_blocks if cfg.decode_top_k_blocks is None else cfg.decode_top_k_blocks)
+        return self.core.select(q, req)
+
+    def decode(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        """One decode step for every layer: q [L, 1, Hq, D], k/v [L, 1, Hkv, D] -> o [L, 1, Hq, D]."""
+        ids, _, n = self.select(q)
+        out, _, _ = self.core.decode_attend(q, k, v, ids, ids.shape[-1], n)
+        self.last_ids_dev = ids
+        self.last_n_selected = n
+        return out

@@ -1,0 +1,161 @@
+"""HBM-resident sparse KV store for a stack of attention layers.
+
+The reference keeps the post-RoPE history on the host and copies the selected
+blocks to the GPU every decode step (nanovllm/sparse/m12_runtime.py:185-246,
+:1212-1311).  Here the whole history lives in HBM, head-major so that one
+(KV head, block) is 16 KiB contiguous:
+
+    hist_k / hist_v : [L, Hkv, cap, 64, 128]  bf16, or int8 + scales
+    reps            : [L, Hkv, cap, r, 128]   bf16 (the reference's reps_gpu layout)
+    sink_k / sink_v : [L, Hkv, S, 128]        bf16
+    recent_k / _v   : [L, Hkv, R, 128]        bf16 ring (logical slot i at (ring_start + i) % R)
+
+Every method enqueues HIP kernels on the current torch stream through the C
+ABI of include/nanokv.h; none of them synchronises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+KV_FORMATS = {
+    "bf16": _lib.NKV_KV_BF16,
+    "int8": _lib.NKV_KV_INT8_CHANNEL,
+    "int8_token": _lib.NKV_KV_INT8_TOKEN,
+}
+
+HEAD_DIM = 128
+BLOCK_SIZE = 64
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+class SparseKVStore:
+    """Device buffers of one model's sparse attention history (all layers)."""
+
+    def __init__(self, num_layers: int, *, num_heads: int, num_kv_heads: int, head_dim: int,
+                 block_size: int, r: int, cap_blocks: int, sink_tokens: int, recent_tokens: int,
+                 kv_format: str = "bf16", device=None):
+        if head_dim != HEAD_DIM:
+            raise ValueError(f"head_dim must be {HEAD_DIM} for the gfx950 kernels (got {head_dim})")
+        if block_size != BLOCK_SIZE:
+            raise ValueError(f"block_size must be {BLOCK_SIZE} for the gfx950 kernels (got {block_size})")
+        if kv_format not in KV_FORMATS:
+            raise ValueError(f"unknown kv_format {kv_format!r}")
+        self.lib = _lib.load()
+        dev = torch.device(device if device is not None else "cuda")
+        L, H, S, R, B, D = num_layers, num_kv_heads, sink_tokens, recent_tokens, block_size, head_dim
+        self.num_layers, self.num_heads, self.num_kv_heads = L, num_heads, num_kv_heads
+        self.head_dim, self.block_size, self.r = D, B, r
+        self.cap_blocks, self.sink_tokens, self.recent_tokens = cap_blocks, S, R
+        self.kv_format = kv_format
+        self.device = dev
+        hdt = torch.bfloat16 if kv_format == "bf16" else torch.int8
+        self.hist_k = torch.zeros(L, H, cap_blocks, B, D, dtype=hdt, device=dev)
+        self.hist_v = torch.zeros_like(self.hist_k)
+        self.reps = torch.zeros(L, H, cap_blocks, r, D, dtype=torch.bfloat16, device=dev)
+        self.sink_k = torch.zeros(L, H, max(S, 1), D, dtype=torch.bfloat16, device=dev)
+        self.sink_v = torch.zeros_like(self.sink_k)
+        self.recent_k = torch.zeros(L, H, R, D, dtype=torch.bfloat16, device=dev)
+        self.recent_v = torch.zeros_like(self.recent_k)
+        self.k_scale = self.v_scale = self.k_tscale = self.v_tscale = None
+        if kv_format == "int8":
+            self.k_scale = torch.zeros(L, H, D, dtype=torch.float32, device=dev)
+            self.v_scale = torch.zeros(L, H, cap_blocks, dtype=torch.float32, device=dev)
+        elif kv_format == "int8_token":
+            self.k_tscale = torch.zeros(L, H, cap_blocks * B, dtype=torch.float16, device=dev)
+            self.v_tscale = torch.zeros_like(self.k_tscale)
+        self.desc = _lib.NkvStore(
+            _ptr(self.hist_k).value, _ptr(self.hist_v).value, _ptr(self.reps).value,
+            _ptr(self.sink_k).value, _ptr(self.sink_v).value,
+            _ptr(self.recent_k).value, _ptr(self.recent_v).value,
+            _ptr(self.k_scale).value, _ptr(self.v_scale).value,
+            _ptr(self.k_tscale).value, _ptr(self.v_tscale).value,
+            L, num_heads, num_kv_heads, D, B, r, cap_blocks, S, R, KV_FORMATS[kv_format])
+        self._desc_ref = ctypes.byref(self.desc)
+
+    # ------------------------------------------------------------------
+    @staticmethod
+    def _bf16(t, name):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be bfloat16 (got {t.dtype})")
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be a device tensor")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+        return t
+
+    def store_chunk(self, layer0: int, k, v, start_block: int, compute_k_scale: bool,
+                    write_sink: bool) -> None:
+        """History (+ int8 scales) and sink for a chunk k, v: [nl, T, Hkv, D]."""
+        self._bf16(k, "k")
+        self._bf16(v, "v")
+        nl, T = k.shape[0], k.shape[1]
+        _lib.check(self.lib.nkv_store_chunk(
+            self._desc_ref, layer0, nl, _ptr(k), _ptr(v), k.stride(0), T, start_block,
+            int(compute_k_scale), int(write_sink), _stream()), "store_chunk")
+
+    def build_reps(self, layer0: int, k, start_block: int) -> None:
+        self._bf16(k, "k")
+        _lib.check(self.lib.nkv_build_reps(
+            self._desc_ref, layer0, k.shape[0], _ptr(k), k.stride(0), k.shape[1], start_block,
+            _stream()), "build_reps")
+
+    def recent_update(self, layer0: int, nl: int, k, v, src_lo: int, n_src: int,
+                      ring_start: int, old_len: int, carry: int) -> None:
+        if n_src:
+            self._bf16(k, "k")
+            self._bf16(v, "v")
+        _lib.check(self.lib.nkv_recent_update(
+            self._desc_ref, layer0, nl, _ptr(k if n_src else None), _ptr(v if n_src else None),
+            k.stride(0) if n_src else 0, src_lo, n_src, ring_start, old_len, carry, _stream()),
+            "recent_update")
+
+    def select(self, layer0: int, q, nblocks: int, prot_dev, n_prot: int, k: int, order: int,
+               per_query: bool, scores_ws, out_ids, out_vals) -> None:
+        self._bf16(q, "q")
+        nl, nq = q.shape[0], q.shape[1]
+        _lib.check(self.lib.nkv_select(
+            self._desc_ref, layer0, nl, _ptr(q), q.stride(0), nq, int(per_query), nblocks,
+            _ptr(prot_dev), n_prot, k, order, _ptr(scores_ws), _ptr(out_ids), _ptr(out_vals),
+            _stream()), "select")
+
+    def attend(self, layer0: int, q, k_new, v_new, n_chunk: int, new_slot: int,
+               write_slot: int, ids, ids_layer_stride: int, n_hist: int, allowed,
+               sink_len: int, ring_base: int, rec_lo: int, rec_len: int, scale: float,
+               splits: int, partial_ws, counters, out) -> None:
+        self._bf16(q, "q")
+        self._bf16(out, "out")
+        nl, tq = q.shape[0], q.shape[1]
+        kv_stride = k_new.stride(0) if k_new is not None else 0
+        _lib.check(self.lib.nkv_attend(
+            self._desc_ref, layer0, nl, _ptr(q), q.stride(0), tq, _ptr(k_new), _ptr(v_new),
+            kv_stride, n_chunk, new_slot, write_slot, _ptr(ids), ids_layer_stride, n_hist,
+            _ptr(allowed), sink_len, ring_base, rec_lo, rec_len, float(scale), splits,
+            _ptr(partial_ws), _ptr(counters), _ptr(out), _stream()), "attend")
+
+    def attend_workspace_floats(self, nl: int, tq: int, splits: int) -> int:
+        return int(self.lib.nkv_attend_workspace_floats(nl, self.num_kv_heads, self.num_heads,
+                                                        tq, splits))
+
+
+def query_summaries(q, nsegments: int):
+    """prefill_query_summaries on device: q [nl, T, Hq, D] -> [nl, nseg, Hq, D] bf16."""
+    lib = _lib.load()
+    SparseKVStore._bf16(q, "q")
+    nl, T, hq, d = q.shape
+    nseg = min(nsegments, T)
+    out = torch.empty(nl, nseg, hq, d, dtype=torch.bfloat16, device=q.device)
+    _lib.check(lib.nkv_query_summaries(_ptr(q), q.stride(0), nl, T, hq, d, nsegments, _ptr(out),
+                                       out.stride(0), _stream()), "query_summaries")
+    return out

@@ -1,0 +1,173 @@
+"""Decode layer-step (select + in-place gather + segmented attention) vs the oracle.
+
+A runtime is prefilled, then stepped; after every step the selected ids must
+equal the oracle's (value and order) and the bf16 output must match the fp64
+oracle to about one bf16 ulp (and always within the 2e-3 max-abs bar).  The
+oracle replays the reference's semantics including the recent-window shift
+(m12_runtime.py:1164-1172), the frozen history / protected set, and the
+reference's int8 dequantisation into bf16 before attention
+(m12_runtime.py:1262-1267).
+
+The oracle is given the representatives the GPU built (the representative
+builder has its own test), so these tests isolate the decode path.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import nkv_oracle as O
+from tests._util import assert_close_bf16, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _make(T, steps, seed, *, quant=False, layout="channel_block", recent=512, sink=64,
+          top_k=32, planted=3, gather_sort=False, decode_budget=None):
+    from nanokv_amd import workload
+    from nanokv_amd.sparse import M12Config, M12LayerRuntime
+    cfg = M12Config(max_model_len=T + 64, quant_history=quant, quant_scale_layout=layout,
+                    recent_tokens=recent, sink_tokens=sink, top_k_blocks=top_k,
+                    gather_sort=gather_sort, decode_top_k_blocks=decode_budget)
+    rt = M12LayerRuntime(0, cfg)
+    k, v, q, planted_ids = workload.history(T, seed, num_planted=planted, recent_tokens=recent)
+    rt.prefill_first(None, k.cuda(), v.cuda())
+    ocfg = O.OracleConfig(recent_tokens=recent, sink_tokens=sink, top_k_blocks=top_k,
+                          quant_history=quant and layout == "channel_block",
+                          decode_top_k_blocks=decode_budget)
+    ob = O.M12Oracle(ocfg)
+    ob.store_kv(to_np(k), to_np(v), with_reps=False)
+    nb = rt.nblocks_filled
+    assert nb == ob.nblocks_filled
+    ob.reps[:, :nb] = to_np(rt.reps_gpu[:, :nb])
+    qs, ks, vs = workload.decode_inputs(steps, seed)
+    return rt, ob, q, planted_ids, (qs, ks, vs)
+
+
+def _dequant_token_layout(ob, rt):
+    """Give the oracle the per-token fp16-scale history the GPU stored."""
+    st = rt.store
+    nb = rt.nblocks_filled
+    kq = st.hist_k[0, :, :nb].cpu().numpy().astype(np.float32)          # [H, nb, 64, D]
+    vq = st.hist_v[0, :, :nb].cpu().numpy().astype(np.float32)
+    ks = st.k_tscale[0, :, :nb * 64].cpu().float().numpy().reshape(8, nb, 64, 1)
+    vsc = st.v_tscale[0, :, :nb * 64].cpu().float().numpy().reshape(8, nb, 64, 1)
+    ob.hist_k[:nb] = O.bf16_round(kq * ks).transpose(1, 2, 0, 3)
+    ob.hist_v[:nb] = O.bf16_round(vq * vsc).transpose(1, 2, 0, 3)
+
+
+def _run_steps(rt, ob, inputs, steps, *, rel=2.0 ** -7, abs_tol=2e-5, first_q=None):
+    qs, ks, vs = inputs
+    worst = 0.0
+    for s in range(steps):
+        q = qs[s, 0] if (s > 0 or first_q is None) else first_q.unsqueeze(0)
+        out = rt.decode(q.cuda(), ks[s, 0].cuda(), vs[s, 0].cuda())
+        ids_or, _, o_ref = ob.decode(to_np(q), to_np(ks[s, 0]), to_np(vs[s, 0]))
+        got = rt.last_block_ids.tolist()
+        if rt.cfg.gather_sort:
+            ids_or = np.sort(ids_or)
+        assert got == ids_or.tolist(), f"step {s}: ids differ"
+        worst = max(worst, assert_close_bf16(to_np(out), o_ref, rel=rel, abs_tol=abs_tol))
+        assert rt.valid_len == ob.valid_len
+    return worst
+
+
+def test_decode_8k_planted_blocks_selected():
+    # 8K history, 128 blocks, protected {0, 120..127}; the planted blocks win.
+    rt, ob, q, planted, inputs = _make(8192, 4, seed=1234)
+    assert rt.protected_blocks == ob.protected_blocks == ({0} | set(range(120, 128)))
+    out = rt.decode(q.unsqueeze(0).cuda(), inputs[1][0, 0].cuda(), inputs[2][0, 0].cuda())
+    ids_or, _, o_ref = ob.decode(to_np(q.unsqueeze(0)), to_np(inputs[1][0, 0]), to_np(inputs[2][0, 0]))
+    ids = rt.last_block_ids.tolist()
+    assert ids == ids_or.tolist()
+    assert set(planted) <= set(ids[:3])
+    assert_close_bf16(to_np(out), o_ref)
+
+
+@pytest.mark.parametrize("T,steps,seed", [
+    (32768, 6, 7),     # the 32K headline shape
+    (1000, 5, 8),      # partial last block, history shorter than sink+recent
+    (4096, 3, 9),
+    (131072, 2, 10),   # 2048 blocks
+])
+def test_decode_bf16_matches_oracle(T, steps, seed):
+    rt, ob, _, _, inputs = _make(T, steps, seed)
+    _run_steps(rt, ob, inputs, steps)
+
+
+def test_decode_short_history_and_small_windows():
+    # history shorter than the recent window: the reference's left-aligned
+    # buffer semantics (stale zero slots) are reproduced exactly.
+    rt, ob, _, _, inputs = _make(300, 6, 21, recent=256, sink=32, top_k=4, planted=0)
+    _run_steps(rt, ob, inputs, 6)
+
+
+def test_decode_gather_sort_and_budget():
+    rt, ob, _, _, inputs = _make(16384, 3, 22, gather_sort=True, decode_budget=24)
+    _run_steps(rt, ob, inputs, 3)
+
+
+def test_decode_many_steps_ring_wraps():
+    # 520 steps: the 512-slot ring wraps; prefill tokens scroll out of the window.
+    rt, ob, _, _, inputs = _make(2048, 520, 23, top_k=8, planted=0)
+    qs, ks, vs = inputs
+    for s in range(520):
+        out = rt.decode(qs[s, 0].cuda(), ks[s, 0].cuda(), vs[s, 0].cuda())
+        ids_or, _, o_ref = ob.decode(to_np(qs[s, 0]), to_np(ks[s, 0]), to_np(vs[s, 0]))
+        if s % 37 == 0 or s >= 510:
+            assert rt.last_block_ids.tolist() == ids_or.tolist()
+            assert_close_bf16(to_np(out), o_ref)
+
+
+def test_decode_int8_channel_block_matches_oracle():
+    rt, ob, _, _, inputs = _make(32768, 4, 31, quant=True)
+    # the GPU-stored int8 history and scales equal the oracle's bit for bit
+    nb = rt.nblocks_filled
+    st = rt.store
+    assert np.array_equal(st.k_scale[0].cpu().numpy(), ob.k_scale)
+    assert np.array_equal(st.v_scale[0, :, :nb].cpu().numpy(), ob.v_scale[:nb].T)
+    assert np.array_equal(st.hist_k[0, :, :nb].cpu().numpy().transpose(1, 2, 0, 3), ob.hist_kq[:nb])
+    assert np.array_equal(st.hist_v[0, :, :nb].cpu().numpy().transpose(1, 2, 0, 3), ob.hist_vq[:nb])
+    worst = _run_steps(rt, ob, inputs, 4, rel=2.0 ** -6, abs_tol=2e-4)
+    print(f"int8 channel/block decode max |err| = {worst:.3e}")
+
+
+def test_decode_int8_token_scales_matches_oracle():
+    rt, ob, _, _, inputs = _make(8192, 3, 41, quant=True, layout="token")
+    nb = rt.nblocks_filled
+    k, v = ob.hist_k[:nb].copy(), ob.hist_v[:nb].copy()
+    # per-token fp16 scale layout: scales and int8 codes bit-exact vs the closed form
+    ks_or = O.token_scale_fp16(k.transpose(2, 0, 1, 3))            # [H, nb, 64]
+    vs_or = O.token_scale_fp16(v.transpose(2, 0, 1, 3))
+    st = rt.store
+    assert np.array_equal(st.k_tscale[0, :, :nb * 64].cpu().numpy().reshape(8, nb, 64), ks_or)
+    assert np.array_equal(st.v_tscale[0, :, :nb * 64].cpu().numpy().reshape(8, nb, 64), vs_or)
+    kq_or = O.quantize(k.transpose(2, 0, 1, 3), ks_or.astype(np.float32)[..., None])
+    assert np.array_equal(st.hist_k[0, :, :nb].cpu().numpy(), kq_or)
+    _dequant_token_layout(ob, rt)
+    worst = _run_steps(rt, ob, inputs, 3, rel=2.0 ** -6, abs_tol=2e-4)
+    print(f"int8 per-token decode max |err| = {worst:.3e}")
+
+
+def test_model_runtime_batches_layers_like_per_layer_runtimes():
+    """M12ModelRuntime (one launch per stage for all layers) == per-layer runtimes."""
+    from nanokv_amd import workload
+    from nanokv_amd.sparse import M12Config, M12LayerRuntime, M12ModelRuntime
+    L, T, steps = 3, 4096, 3
+    cfg = M12Config(max_model_len=T + 64)
+    model = M12ModelRuntime(L, cfg)
+    layers = [M12LayerRuntime(i, cfg) for i in range(L)]
+    hist = [workload.history(T, 100 + i) for i in range(L)]
+    k = torch.stack([h[0] for h in hist]).cuda()
+    v = torch.stack([h[1] for h in hist]).cuda()
+    model.prefill(k, v)
+    for i, rt in enumerate(layers):
+        rt.prefill_first(None, k[i], v[i])
+    qs, ks, vs = workload.decode_inputs(steps, 5, layers=L)
+    for s in range(steps):
+        out = model.decode(qs[s].cuda(), ks[s].cuda(), vs[s].cuda())
+        for i, rt in enumerate(layers):
+            o_i = rt.decode(qs[s, i].cuda(), ks[s, i].cuda(), vs[s, i].cuda())
+            assert torch.equal(model.last_ids_dev[i, 0, :model.last_n_selected].cpu(),
+                               rt.last_block_ids.to(torch.int32))
+            assert torch.equal(out[i].cpu(), o_i.cpu())

@@ -1,0 +1,174 @@
+"""Kernels 1+2 (block scoring + Top-K) against the oracle, through the C ABI.
+
+Scores must be bit-identical to the oracle's fp32 sequential-fma definition,
+and the selected ids identical in value and order (score desc, id asc).
+Edge cases follow the reference's selector tests
+(tests/test_m19_selector_graph.py:47-87, test_m21_static_mask.py:36-101,
+test_m16_dynamic_topk.py:25-63): protected ids, budget caps, all-protected
+histories, exact ties, dynamic budgets.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import nkv_oracle as O
+from tests._util import f32_bits, to_np
+
+pytestmark = pytest.mark.gpu
+
+HQ, HKV, D = 32, 8, 128
+
+
+def _runtime(nblocks, *, r=4, top_k=32, max_blocks=None, **kw):
+    from nanokv_amd.sparse import M12Config, M12LayerRuntime
+    cfg = M12Config(top_k_blocks=top_k, r=r, max_model_len=64 * (max_blocks or nblocks), **kw)
+    rt = M12LayerRuntime(0, cfg)
+    rt.nblocks_filled = nblocks
+    return rt
+
+
+def _rand_reps(nb, r, seed):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(HKV, nb, r, D, generator=g) / D ** 0.5).to(torch.bfloat16)
+
+
+def _rand_q(nq, seed):
+    g = torch.Generator().manual_seed(seed + 1)
+    return torch.randn(nq, HQ, D, generator=g).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("nb,r,nq,prot,budget,seed", [
+    (512, 4, 1, "std", 32, 0),       # 32K decode shape
+    (128, 4, 1, "std", 32, 1),       # 8K
+    (2048, 4, 1, "std", 32, 2),      # 128K
+    (256, 4, 6, "std", 32, 3),       # verify: 6 queries max-reduced
+    (37, 4, 1, "std", 32, 4),        # ragged tile
+    (1, 4, 1, "none", 32, 5),        # one block
+    (300, 2, 3, {0, 3, 299, 1000}, 24, 6),
+    (64, 8, 1, "none", 16, 7),
+    (100, 1, 2, "std", 48, 8),
+])
+def test_scores_and_ids_bit_exact(nb, r, nq, prot, budget, seed):
+    rt = _runtime(nb, r=r, top_k=max(budget, 32))
+    reps = _rand_reps(nb, r, seed)
+    rt.reps_gpu[:, :nb].copy_(reps.cuda())
+    if prot == "std":
+        rt.protected_blocks = O.protected_blocks_after_store(nb, 512, 64)
+    elif prot == "none":
+        rt.protected_blocks = set()
+    else:
+        rt.protected_blocks = set(prot)
+    q = _rand_q(nq, seed)
+    ids, info = rt._gpu_select(q.cuda(), budget=budget)
+    scores_gpu = rt._core._last_scores[0, 0].cpu().numpy()
+
+    s_or = O.block_scores(to_np(q), to_np(reps), nb, HKV)
+    ids_or, vals_or = O.topk_blocks(s_or, rt.protected_blocks, budget)
+    assert np.array_equal(f32_bits(scores_gpu), f32_bits(s_or)), "scores differ from the oracle"
+    assert ids.tolist() == ids_or.tolist()
+    assert info["n_selected"] == info["n_candidates"] == len(ids_or)
+
+
+def test_per_query_topk_matches_oracle():
+    nb, tq = 256, 6
+    rt = _runtime(nb)
+    reps = _rand_reps(nb, 4, 11)
+    rt.reps_gpu[:, :nb].copy_(reps.cuda())
+    rt.protected_blocks = O.protected_blocks_after_store(nb, 512, 64)
+    q = _rand_q(tq, 11)
+    union, allowed = rt._gpu_select_per_query(q.cuda(), 32)
+    u_or, a_or, _ = O.select_per_query(to_np(q), to_np(reps), nb, HKV, rt.protected_blocks, 32)
+    assert union.tolist() == u_or.tolist()
+    assert np.array_equal(allowed.cpu().numpy(), a_or)
+
+
+@pytest.mark.parametrize("budget", [1, 3, 6])
+def test_protected_ids_and_small_budgets(budget):
+    # test_m19_selector_graph.py:47-56: protected ids (and ids beyond history) never selected
+    nb = 8
+    rt = _runtime(nb, top_k=6, max_blocks=32)
+    rt.reps_gpu[:, :nb].copy_(_rand_reps(nb, 4, 19).cuda())
+    rt.protected_blocks = {0, 3, 100}
+    ids, _ = rt._gpu_select(_rand_q(1, 19)[0].cuda(), budget=budget)
+    assert ids.numel() == budget
+    assert not ({0, 3} & set(ids.tolist()))
+
+
+def test_budget_capped_by_history_after_protection():
+    # test_m19_selector_graph.py:68-76
+    rt = _runtime(3, top_k=6, max_blocks=32)
+    rt.reps_gpu[:, :3].copy_(_rand_reps(3, 4, 23).cuda())
+    rt.protected_blocks = {0, 20}
+    ids, info = rt._gpu_select(_rand_q(1, 23)[0].cuda(), budget=6)
+    assert ids.numel() == 2 and 0 not in ids.tolist()
+    assert info["n_candidates"] == 2
+
+
+def test_all_protected_returns_one_block_lowest_id():
+    # test_m19_selector_graph.py:79-87 / test_m21_static_mask.py:80-90: k collapses to 1;
+    # every score is -inf, the id-ascending tie rule picks block 0.
+    rt = _runtime(4, top_k=6, max_blocks=32)
+    rt.reps_gpu[:, :4].copy_(_rand_reps(4, 4, 29).cuda())
+    rt.protected_blocks = {0, 1, 2, 3, 20}
+    ids, info = rt._gpu_select(_rand_q(1, 29)[0].cuda(), budget=6)
+    assert ids.tolist() == [0]
+    assert info["n_candidates"] == 1
+
+
+def test_exact_ties_take_lowest_ids():
+    # test_m21_static_mask.py:28-45: all-zero reps and query -> every score is 0
+    nb = 8
+    rt = _runtime(nb, top_k=6, max_blocks=32)
+    rt.reps_gpu[:, :nb].zero_()
+    rt.protected_blocks = {0, 4, 100}
+    ids, info = rt._gpu_select(torch.zeros(HQ, D, dtype=torch.bfloat16, device="cuda"), budget=6)
+    assert ids.tolist() == [1, 2, 3, 5, 6, 7]
+    assert info["n_selected"] == 6
+
+
+def test_dynamic_budget_changes_decode_only():
+    # test_m16_dynamic_topk.py:25-43: one dominant block -> dynamic budget 16 of 32
+    rt = _runtime(40, top_k=32, max_blocks=128, dynamic_top_k=True)
+    rt.reps_gpu.zero_()
+    rt.reps_gpu[0, 0, 0, 0] = 10.0
+    query = torch.zeros(1, HQ, D, dtype=torch.bfloat16, device="cuda")
+    query[0, 0, 0] = 1.0
+    prefill_ids, _ = rt._gpu_select(query)
+    decode_ids, info = rt._gpu_select(query, dynamic=True)
+    assert prefill_ids.numel() == 32
+    assert decode_ids.numel() == info["n_selected"] == 16
+    assert torch.equal(decode_ids, prefill_ids[:16])
+    assert prefill_ids.tolist() == list(range(32))
+
+
+def test_fixed_decode_override_keeps_prefill_budget():
+    # test_m16_dynamic_topk.py:46-63
+    rt = _runtime(40, top_k=32, max_blocks=128, decode_top_k_blocks=24)
+    rt.reps_gpu.zero_()
+    query = torch.zeros(1, HQ, D, dtype=torch.bfloat16, device="cuda")
+    prefill_ids, _ = rt._gpu_select(query)
+    decode_ids, info = rt._gpu_select(query, budget=rt.cfg.decode_top_k_blocks)
+    assert prefill_ids.numel() == 32
+    assert decode_ids.numel() == info["n_selected"] == 24
+
+
+def test_gather_sort_orders_ids_ascending_on_device():
+    from nanokv_amd import _lib
+    nb = 512
+    rt = _runtime(nb)
+    reps = _rand_reps(nb, 4, 31)
+    rt.reps_gpu[:, :nb].copy_(reps.cuda())
+    rt.protected_blocks = O.protected_blocks_after_store(nb, 512, 64)
+    q = _rand_q(1, 31)
+    ids, _, k = rt._select_dev(q.cuda(), 32, _lib.NKV_ORDER_ID_ASC)
+    got = ids[0, 0, :k].cpu().tolist()
+    s_or = O.block_scores(to_np(q), to_np(reps), nb, HKV)
+    ids_or, _ = O.topk_blocks(s_or, rt.protected_blocks, 32)
+    assert got == sorted(ids_or.tolist())
+
+
+def test_select_rejects_empty_history():
+    rt = _runtime(0, max_blocks=8)
+    with pytest.raises(ValueError, match="history block"):
+        rt._gpu_select(_rand_q(1, 0)[0].cuda())

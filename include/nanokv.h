@@ -91,20 +91,26 @@ const char* nkv_last_error(void);
  *
  * q        : bf16 [num_layers][nq][Hq][D], layer stride q_layer_stride elements.
  * score[b] = max over (n<nq, h, g, j<r) of the fp32 dot q[n][h*G+g] . reps[h][b][j],
- *            accumulated in ascending d with fma, per_query=0;
- *            per (n) when per_query=1.
+ *            each dot accumulated in ascending d with fma from +0
+ *            (per_query=0); per n when per_query=1.
  * Protected ids (device int32 list, shared by all layers; ids outside
  * [0, nblocks) are ignored) are scored -inf.  k_eff = min(k, max(1, nblocks
- * - |protected in range|)) ids are returned per (layer[, n]), in `order`.
- * scores_ws: fp32 workspace [num_layers][nq'][nblocks] (nq' = per_query ? nq : 1).
- * out_ids  : int32 [num_layers][nq'][k] (entries >= k_eff untouched).
- * out_vals : fp32  [num_layers][nq'][k] selected scores (may be NULL).
- * Constraints: 1 <= nblocks <= cap_blocks, nblocks <= 12288, 1 <= k <= 1024.
+ * - |protected in range|)) ids are returned per (layer[, n]), ordered by
+ * `order`; exact ties go to the lower block id.
+ * score_keys : uint32 workspace [num_layers][nq'][nblocks] (nq' = per_query ?
+ *              nq : 1) that must be zero before the first call; every call
+ *              leaves it zero.
+ * out_scores : fp32 [num_layers][nq'][nblocks] raw scores (before the
+ *              protected mask), or NULL.
+ * out_ids    : int32 [num_layers][nq'][k] (entries >= k_eff untouched).
+ * out_vals   : fp32  [num_layers][nq'][k] selected scores, or NULL.
+ * Constraints: 1 <= nblocks <= cap_blocks, nblocks <= 12288, 1 <= k <= 1024,
+ *              nq <= 64.
  */
 int nkv_select(const nkv_store* st, int layer0, int num_layers,
                const uint16_t* q, int64_t q_layer_stride, int nq, int per_query,
                int nblocks, const int32_t* protected_ids, int n_protected,
-               int k, int order, float* scores_ws,
+               int k, int order, uint32_t* score_keys, float* out_scores,
                int32_t* out_ids, float* out_vals, void* stream);
 
 /*
@@ -116,37 +122,40 @@ int nkv_select(const nkv_store* st, int layer0, int num_layers,
  * verify_tokens steps 2-3 (m12_runtime.py:686-758) with the masked
  * _fused_attention path (:875-896) and the lossless per-query mask (:753-758).
  *
- * Keys/values attended by query t of layer l, KV head h, in this order:
- *   n_hist selected history blocks  ids[l][i] (64 tokens each; with
+ * Keys/values attended by query t of layer l, KV head h (as one softmax):
+ *   n_hist selected history blocks ids[l][i] (64 tokens each; with
  *            `allowed` != NULL only blocks with allowed[t][i] != 0),
  *   sink   : sink[l][h][0 .. sink_len),
- *   recent : logical slots [rec_lo, rec_lo + rec_len) of the ring, physical
- *            slot (ring_base + i) % R; logical slot `new_slot` (>= 0) is read
- *            from k_new/v_new instead, which this call also writes into
- *            physical slot `write_slot` (decode's shift+append),
- *   chunk  : k_new/v_new tokens 0 .. n_chunk-1, causal (query t sees c <= t).
+ *   recent : ring slots whose logical position (slot - ring_base) mod R lies
+ *            in [rec_lo, rec_lo + rec_len),
+ *   chunk  : new tokens k_new/v_new[l][c], c < n_chunk, causal (query t sees
+ *            c <= t).  Decode passes its new token as a one-token chunk.
+ * If write_slot >= 0 the call also stores chunk token 0 into ring slot
+ * write_slot (decode's shift + append); that slot must lie outside the
+ * attended recent window.
  * q      : bf16 [num_layers][tq][Hq][D] (layer stride q_layer_stride).
- * k_new, v_new : bf16 [num_layers][max(n_chunk,1)][Hkv][D] (layer stride kv_layer_stride).
- * ids    : int32 [num_layers][ids_layer_stride]; allowed: uint8 [tq][n_hist] (shared by layers).
+ * k_new, v_new : bf16 [num_layers][n_chunk][Hkv][D] (layer stride kv_layer_stride).
+ * ids    : int32 [num_layers][ids_layer_stride]; ids outside [0, cap) attend nothing.
+ * allowed: uint8 [tq][n_hist] (shared by layers) or NULL.
  * out    : bf16 [num_layers][tq][Hq][D] (layer stride q_layer_stride).
- * partial_ws : fp32 workspace, >= nkv_attend_workspace_floats(...) floats.
- * counters   : int32 workspace of num_layers*Hkv*ceil(tq/qpw) entries, zero
- *              before first use; every call leaves them zero.
- * splits : workgroups per (layer, KV head, query group), 1..64.  Queries are
- *          processed in groups of 16/G per workgroup (grid z = layers x groups).
+ * partial_ws : fp32 workspace, >= nkv_attend_workspace_floats(...) floats
+ *              (unused when splits == 1).
+ * splits : workgroups per (layer, KV head, query group), 1..64; with
+ *          splits > 1 a second kernel on the same stream merges the partial
+ *          softmax states.  Queries are processed in groups of 16/G per
+ *          workgroup (grid z = layers x groups).
  * Constraints: 1 <= tq <= 65536, n_hist <= 4096, n_chunk in {0, tq};
  *          fp32 softmax and accumulation.
  */
 int nkv_attend(const nkv_store* st, int layer0, int num_layers,
                const uint16_t* q, int64_t q_layer_stride, int tq,
                const uint16_t* k_new, const uint16_t* v_new, int64_t kv_layer_stride,
-               int n_chunk, int new_slot, int write_slot,
+               int n_chunk, int write_slot,
                const int32_t* ids, int64_t ids_layer_stride, int n_hist,
                const uint8_t* allowed, int sink_len,
                int ring_base, int rec_lo, int rec_len,
                float scale, int splits,
-               float* partial_ws, int32_t* counters,
-               uint16_t* out, void* stream);
+               float* partial_ws, uint16_t* out, void* stream);
 
 /* Floats of partial_ws needed by nkv_attend for these sizes. */
 int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads, int num_heads,

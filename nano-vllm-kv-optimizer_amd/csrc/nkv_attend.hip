@@ -2,25 +2,33 @@
 // verify (kernel 3 of the layer-step).
 //
 // One workgroup (4 wavefronts) handles one (layer, KV head, query group,
-// split).  The keys it attends are cut into 64-token segments: the selected
-// history blocks (read in place from the HBM history, bf16 or int8), the sink,
-// the recent ring (logical slots mapped to physical ones), and, for verify,
-// the causal chunk of new tokens.  Wavefront w of split s handles segments
-// w + 4*s, w + 4*s + 4*splits, ... and keeps an online-softmax state.
+// split).  The keys it attends are cut into segments of up to 64 rows that
+// are contiguous in memory with a uniform row stride:
+//   * the selected history blocks, read in place from the HBM history
+//     (bf16 or int8),
+//   * the sink,
+//   * the recent ring, walked in physical 64-slot pieces; a slot takes part
+//     when its logical position lies in the requested window,
+//   * the chunk of new tokens (verify's Tq tokens, or decode's new token),
+//     causal: query t sees chunk token c iff c <= t.
+// Row indices are clamped into each segment, so every load stays inside its
+// buffer; validity is applied as a -inf mask on the logits.  Wavefront w of
+// split s handles segments w + 4 s, w + 4 s + 4 splits, ... with an online
+// softmax.
 //
 //  * Q.K^T runs on the matrix cores: v_mfma_f32_16x16x32_bf16 with A = 16
 //    keys x 32 dims (each lane loads 16 contiguous bytes of one key row) and
 //    B = 32 dims x 16 query rows (G heads per query, padded to 16).  int8
 //    keys are widened to bf16 exactly; the per-(head, dim) K scale is folded
 //    into the bf16 query operand of history segments.
-//  * softmax: fp32, exp2 with the scale folded in; masked keys get -inf.
+//  * softmax: fp32, exp2 with the scale folded in.
 //  * P.V on the vector ALUs in fp32: lane (r, c) owns dims 8c..8c+7 of keys
 //    4j + r; p comes from LDS.  The int8 V scale (per block or per token) is
-//    folded into p.
+//    folded into p.  V loads are issued right after the MFMAs so they overlap
+//    the softmax.
 //  * the 4 wavefronts merge through LDS; with splits > 1 each workgroup
-//    writes a partial (m, l, acc[128]) per query row and the last workgroup
-//    of its (layer, head, group) - found with an atomic counter - merges them
-//    and resets the counter.
+//    writes a partial (m, l, acc[128]) per query row and a second kernel
+//    merges them (stream order makes the partials visible).
 //
 // Same result as the reference's gather + pack + fp32 einsum attention
 // (nanovllm/sparse/m12_runtime.py:1212-1320 and :845-896) up to fp32
@@ -64,11 +72,10 @@ struct AttendParams {
   int64_t ids_ls;
   const uint8_t* allowed;
   float* partial;
-  int32_t* counters;
   uint16_t* out;
   int hkv, G, cap, S, R;
   int tq, qpg, nqg;
-  int n_chunk, new_slot, write_slot;
+  int n_chunk, write_slot;
   int n_hist, sink_len, ring_base, rec_lo, rec_len;
   int n_sink_seg, n_rec_seg, nseg;
   int splits;
@@ -84,12 +91,11 @@ __device__ __forceinline__ void wave_lds_sync() {
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // 8 signed bytes -> 8 bf16 (exact: |x| <= 127 has <= 7 significant bits).
-__device__ __forceinline__ uint4 i8x8_to_bf16x8(uint2 raw) {
-  uint32_t w[2] = {raw.x, raw.y};
+__device__ __forceinline__ uint4 i8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
   uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t src = w[i >> 1] >> ((i & 1) * 16);
+    const uint32_t src = ((i < 2) ? lo : hi) >> ((i & 1) * 16);
     const float f0 = static_cast<float>(static_cast<int8_t>(src & 0xffu));
     const float f1 = static_cast<float>(static_cast<int8_t>((src >> 8) & 0xffu));
     o[i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
@@ -97,95 +103,84 @@ __device__ __forceinline__ uint4 i8x8_to_bf16x8(uint2 raw) {
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
-__device__ __forceinline__ void i8x8_to_f32(uint2 raw, float* f) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t w = (i < 4) ? raw.x : raw.y;
-    f[i] = static_cast<float>(static_cast<int8_t>((w >> ((i & 3) * 8)) & 0xffu));
-  }
-}
-
+// A segment: `len` rows starting at kbase / vbase, row stride `rowb` bytes;
+// rows >= len are never loaded (indices are clamped).  `vlen` = rows that may
+// be valid (a history block with an out-of-range id has vlen 0).
 struct Seg {
   int type;
-  int len;   // valid tokens in this segment (1..64)
-  int off;   // first logical token (sink / recent / chunk)
+  int len;
+  int vlen;
+  int off;   // sink / chunk: first token; recent: first physical slot
   int blk;   // history block id
   int u;     // history segment index (column of `allowed`)
+  int rowb;
+  const char* kbase;
+  const char* vbase;
 };
 
-__device__ __forceinline__ Seg classify(const AttendParams& p, int layer, int s) {
+template <int FMT>
+__device__ __forceinline__ Seg make_seg(const AttendParams& p, int layer, int h, int s) {
   Seg g;
   g.blk = 0;
   g.u = 0;
   g.off = 0;
   if (s < p.n_hist) {
+    constexpr int64_t elem = (FMT == NKV_KV_BF16) ? 2 : 1;
     g.type = kSegHist;
     g.len = kBlock;
+    g.vlen = kBlock;
     g.u = s;
-    g.blk = p.ids[static_cast<int64_t>(layer) * p.ids_ls + s];
-    if (g.blk < 0 || g.blk >= p.cap) {  // never read outside the history
-      g.blk = 0;
-      g.len = 0;
+    int blk = p.ids[static_cast<int64_t>(layer) * p.ids_ls + s];
+    if (blk < 0 || blk >= p.cap) {  // never read outside the history
+      blk = 0;
+      g.vlen = 0;
     }
+    g.blk = blk;
+    const int64_t off = (p.hist_ls * layer + (static_cast<int64_t>(h) * p.cap + blk) * kBlock * kHeadDim) * elem;
+    g.kbase = static_cast<const char*>(p.hist_k) + off;
+    g.vbase = static_cast<const char*>(p.hist_v) + off;
+    g.rowb = kHeadDim * static_cast<int>(elem);
     return g;
   }
   s -= p.n_hist;
+  g.rowb = kHeadDim * 2;
   if (s < p.n_sink_seg) {
     g.type = kSegSink;
     g.off = s * kBlock;
     g.len = min(kBlock, p.sink_len - g.off);
+    g.vlen = g.len;
+    const int64_t off = p.sink_ls * layer + (static_cast<int64_t>(h) * p.S + g.off) * kHeadDim;
+    g.kbase = reinterpret_cast<const char*>(p.sink_k + off);
+    g.vbase = reinterpret_cast<const char*>(p.sink_v + off);
     return g;
   }
   s -= p.n_sink_seg;
   if (s < p.n_rec_seg) {
     g.type = kSegRecent;
-    g.off = p.rec_lo + s * kBlock;
-    g.len = min(kBlock, p.rec_lo + p.rec_len - g.off);
+    g.off = s * kBlock;
+    g.len = min(kBlock, p.R - g.off);
+    g.vlen = g.len;
+    const int64_t off = p.rec_ls * layer + (static_cast<int64_t>(h) * p.R + g.off) * kHeadDim;
+    g.kbase = reinterpret_cast<const char*>(p.rec_k + off);
+    g.vbase = reinterpret_cast<const char*>(p.rec_v + off);
     return g;
   }
   s -= p.n_rec_seg;
   g.type = kSegChunk;
   g.off = s * kBlock;
   g.len = min(kBlock, p.n_chunk - g.off);
+  g.vlen = g.len;
+  g.rowb = p.hkv * kHeadDim * 2;
+  const int64_t off = p.kv_ls * layer + (static_cast<int64_t>(g.off) * p.hkv + h) * kHeadDim;
+  g.kbase = reinterpret_cast<const char*>(p.k_new + off);
+  g.vbase = reinterpret_cast<const char*>(p.v_new + off);
   return g;
-}
-
-// Element offset of key/value row `tk` of segment `g` for bf16 sources, or the
-// byte offset into the int8 history for history segments of int8 formats.
-// `which` selects K (0) or V (1).
-template <int FMT>
-__device__ __forceinline__ const void* row_ptr(const AttendParams& p, int layer, int h,
-                                               const Seg& g, int tk, int which) {
-  if (g.type == kSegHist) {
-    const int64_t idx = p.hist_ls * layer +
-                        ((static_cast<int64_t>(h) * p.cap + g.blk) * kBlock + tk) * kHeadDim;
-    const void* base = which ? p.hist_v : p.hist_k;
-    if (FMT == NKV_KV_BF16) return static_cast<const uint16_t*>(base) + idx;
-    return static_cast<const int8_t*>(base) + idx;
-  }
-  if (g.type == kSegSink) {
-    const uint16_t* base = which ? p.sink_v : p.sink_k;
-    return base + p.sink_ls * layer + (static_cast<int64_t>(h) * p.S + g.off + tk) * kHeadDim;
-  }
-  if (g.type == kSegRecent) {
-    const int lp = g.off + tk;
-    if (lp == p.new_slot) {
-      const uint16_t* base = which ? p.v_new : p.k_new;
-      return base + p.kv_ls * layer + static_cast<int64_t>(h) * kHeadDim;
-    }
-    const int slot = (p.ring_base + lp) % p.R;
-    const uint16_t* base = which ? p.rec_v : p.rec_k;
-    return base + p.rec_ls * layer + (static_cast<int64_t>(h) * p.R + slot) * kHeadDim;
-  }
-  const uint16_t* base = which ? p.v_new : p.k_new;
-  return base + p.kv_ls * layer + (static_cast<int64_t>(g.off + tk) * p.hkv + h) * kHeadDim;
 }
 
 template <int FMT, int M>
 __global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendParams p) {
   __shared__ __attribute__((aligned(16))) float s_p[kAttendWaves][kBlock * kPRow];
   __shared__ float s_alpha[kAttendWaves][kMaxRows];
-  __shared__ int s_last;
 
   const int split = blockIdx.x;
   const int h = blockIdx.y;
@@ -199,7 +194,8 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendPara
   const int q0 = qg * p.qpg;
   const int rows = min(p.qpg, p.tq - q0) * p.G;
 
-  // decode's shift+append: the new token goes into the freed ring slot.
+  // decode's shift+append: the new token (chunk token 0) also goes into the
+  // freed ring slot, which no workgroup of this launch reads.
   if (p.write_slot >= 0 && split == 0 && qg == 0 && wave == 0 && lane < 32) {
     const int which = lane >> 4;
     const int c = lane & 15;
@@ -253,40 +249,66 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendPara
   float* my_p = s_p[wave];
   const int nwaves = p.splits * kAttendWaves;
   for (int sidx = split * kAttendWaves + wave; sidx < p.nseg; sidx += nwaves) {
-    const Seg g = classify(p, layer, sidx);
+    const Seg g = make_seg<FMT>(p, layer, h, sidx);
     const bool int8_seg = (FMT != NKV_KV_BF16) && g.type == kSegHist;
+    const int last = g.len - 1;
 
     // ---- S^T = K . Q^T on the matrix cores -------------------------------
+    // lane (lg, ln) loads dims [32 s + 8 lg, +8) of key 16 i + ln.
     f32x4 c[4];
+    if (int8_seg) {
+      uint2 ka[4][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      c[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      const int tk = i * 16 + ln;
-      uint4 a[4];
-      if (tk < g.len) {
-        const void* rp = row_ptr<FMT>(p, layer, h, g, tk, 0);
-        if (int8_seg) {
+      for (int i = 0; i < 4; ++i) {
+        const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 8;
 #pragma unroll
-          for (int s = 0; s < 4; ++s)
-            a[s] = i8x8_to_bf16x8(*reinterpret_cast<const uint2*>(
-                static_cast<const int8_t*>(rp) + s * 32 + lg * 8));
-        } else {
-#pragma unroll
-          for (int s = 0; s < 4; ++s)
-            a[s] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(rp) + s * 32 + lg * 8);
-        }
-      } else {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) a[s] = make_uint4(0u, 0u, 0u, 0u);
+        for (int s = 0; s < 4; ++s) ka[i][s] = *reinterpret_cast<const uint2*>(rp + s * 32);
       }
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        c[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[s]), int8_seg ? bqs[s] : bq[s],
-                                                        c[i], 0, 0, 0);
+      for (int i = 0; i < 4; ++i) {
+        c[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          c[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(i8x8_to_bf16x8(ka[i][s].x, ka[i][s].y)),
+                                                          bqs[s], c[i], 0, 0, 0);
+      }
+    } else {
+      uint4 ka[4][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 16;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) ka[i][s] = *reinterpret_cast<const uint4*>(rp + s * 64);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          c[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[i][s]), bq[s], c[i], 0, 0, 0);
+      }
+    }
+
+    // ---- V loads go out now and overlap the softmax below -----------------
+    // lane (lg, ln) loads dims [8 ln, +8) of key 4 j + lg.
+    uint4 va[16];
+    if (int8_seg) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint2 r = *reinterpret_cast<const uint2*>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 8);
+        va[j] = make_uint4(r.x, r.y, 0u, 0u);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        va[j] = *reinterpret_cast<const uint4*>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 16);
     }
 
     // ---- masking, scale, online softmax ------------------------------------
     // c[i][e]: key tk = 16 i + 4 lg + e, query row ln.
+    const uint8_t* allow_row =
+        (g.type == kSegHist && p.allowed != nullptr) ? p.allowed + static_cast<int64_t>(my_t) * p.n_hist : nullptr;
+    const bool seg_allowed = allow_row == nullptr || allow_row[g.u] != 0;
     float x[4][4];
     float cmax = -INFINITY;
 #pragma unroll
@@ -295,13 +317,17 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendPara
       for (int e = 0; e < 4; ++e) {
         const int tk = i * 16 + lg * 4 + e;
         float v = c[i][e];
-        bool ok = row_ok && tk < g.len;
-        if (FMT == NKV_KV_INT8_TOKEN && g.type == kSegHist && ok)
+        bool ok = row_ok && tk < g.vlen && seg_allowed;
+        if (g.type == kSegRecent) {
+          int lp = g.off + tk - p.ring_base;
+          if (lp < 0) lp += p.R;
+          ok = ok && static_cast<unsigned>(lp - p.rec_lo) < static_cast<unsigned>(p.rec_len);
+        } else if (g.type == kSegChunk) {
+          ok = ok && (g.off + tk) <= my_t;
+        }
+        if (FMT == NKV_KV_INT8_TOKEN && g.type == kSegHist)
           v *= f16_bits_to_f32(p.k_tscale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap * kBlock +
                                           static_cast<int64_t>(g.blk) * kBlock + tk]);
-        if (g.type == kSegHist && p.allowed != nullptr && ok)
-          ok = p.allowed[static_cast<int64_t>(my_t) * p.n_hist + g.u] != 0;
-        if (g.type == kSegChunk && ok) ok = (g.off + tk) <= my_t;
         v = ok ? v * p.scale_log2 : -INFINITY;
         x[i][e] = v;
         cmax = fmaxf(cmax, v);
@@ -310,7 +336,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendPara
     cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
     cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
     const float m_new = fmaxf(m_run, cmax);
-    const float alpha = (m_new == -INFINITY) ? 1.0f : exp2f(m_run - m_new);
+    const float alpha = (m_new == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
     float vs_blk = 1.0f;
     if (FMT == NKV_KV_INT8_CHANNEL && g.type == kSegHist)
       vs_blk = p.v_scale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap + g.blk];
@@ -320,10 +346,10 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendPara
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int tk = i * 16 + lg * 4 + e;
-        const float pe = (x[i][e] == -INFINITY) ? 0.0f : exp2f(x[i][e] - m_new);
+        const float pe = (x[i][e] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(x[i][e] - m_new);
         lsum += pe;
         float pv = pe * vs_blk;
-        if (FMT == NKV_KV_INT8_TOKEN && g.type == kSegHist && tk < g.len)
+        if (FMT == NKV_KV_INT8_TOKEN && g.type == kSegHist)
           pv *= f16_bits_to_f32(p.v_tscale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap * kBlock +
                                            static_cast<int64_t>(g.blk) * kBlock + tk]);
         my_p[tk * kPRow + ln] = pv;
@@ -335,36 +361,35 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendPara
     wave_lds_sync();
 
     // ---- O += P . V (fp32) --------------------------------------------------
-    float al[M];
 #pragma unroll
-    for (int n = 0; n < M; ++n) al[n] = s_alpha[wave][n];
+    for (int n = 0; n < M; ++n) {
+      const float al = s_alpha[wave][n];
 #pragma unroll
-    for (int n = 0; n < M; ++n)
+      for (int e = 0; e < 8; ++e) acc[n][e] *= al;
+    }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[n][e] *= al[n];
-#pragma unroll 4
     for (int j = 0; j < 16; ++j) {
       const int tk = 4 * j + lg;
-      if (tk < g.len) {
-        float vf[8];
-        const void* rp = row_ptr<FMT>(p, layer, h, g, tk, 1);
-        if (int8_seg) {
-          i8x8_to_f32(*reinterpret_cast<const uint2*>(static_cast<const int8_t*>(rp) + ln * 8), vf);
-        } else {
-          const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(rp) + ln * 8);
-          vf[0] = bf16_lo(v.x); vf[1] = bf16_hi(v.x); vf[2] = bf16_lo(v.y); vf[3] = bf16_hi(v.y);
-          vf[4] = bf16_lo(v.z); vf[5] = bf16_hi(v.z); vf[6] = bf16_lo(v.w); vf[7] = bf16_hi(v.w);
+      float vf[8];
+      if (int8_seg) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t w = (e < 4) ? va[j].x : va[j].y;
+          vf[e] = static_cast<float>(static_cast<int8_t>((w >> ((e & 3) * 8)) & 0xffu));
         }
-        const float* prow = my_p + tk * kPRow;
+      } else {
+        vf[0] = bf16_lo(va[j].x); vf[1] = bf16_hi(va[j].x); vf[2] = bf16_lo(va[j].y); vf[3] = bf16_hi(va[j].y);
+        vf[4] = bf16_lo(va[j].z); vf[5] = bf16_hi(va[j].z); vf[6] = bf16_lo(va[j].w); vf[7] = bf16_hi(va[j].w);
+      }
+      const float* prow = my_p + tk * kPRow;
 #pragma unroll
-        for (int n4 = 0; n4 < M; n4 += 4) {
-          const float4 pp = *reinterpret_cast<const float4*>(prow + n4);
-          const float pn[4] = {pp.x, pp.y, pp.z, pp.w};
+      for (int n4 = 0; n4 < M; n4 += 4) {
+        const float4 pp = *reinterpret_cast<const float4*>(prow + n4);
+        const float pn[4] = {pp.x, pp.y, pp.z, pp.w};
 #pragma unroll
-          for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < 4; ++u)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[n4 + u][e] = __builtin_fmaf(pn[u], vf[e], acc[n4 + u][e]);
-        }
+          for (int e = 0; e < 8; ++e) acc[n4 + u][e] = __builtin_fmaf(pn[u], vf[e], acc[n4 + u][e]);
       }
     }
     wave_lds_sync();
@@ -401,6 +426,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendPara
   const int64_t grp = (static_cast<int64_t>(layer) * p.hkv + h) * p.nqg + qg;
   for (int idx = threadIdx.x; idx < M * kHeadDim; idx += kAttendThreads) {
     const int n = idx / kHeadDim, d = idx % kHeadDim;
+    if (n >= rows) continue;
     float mt = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kAttendWaves; ++w) mt = fmaxf(mt, s_m[w * kMaxRows + n]);
@@ -408,16 +434,14 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendPara
 #pragma unroll
     for (int w = 0; w < kAttendWaves; ++w) {
       const float mw = s_m[w * kMaxRows + n];
-      const float sw = (mw == -INFINITY) ? 0.0f : exp2f(mw - mt);
+      const float sw = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - mt);
       L += s_l[w * kMaxRows + n] * sw;
       A += s_acc[(w * M + n) * kHeadDim + d] * sw;
     }
     if (p.splits == 1) {
-      if (n < rows) {
-        const int t = q0 + n / p.G;
-        const int hh = h * p.G + n % p.G;
-        p.out[p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d] = f32_to_bf16(A / L);
-      }
+      const int t = q0 + n / p.G;
+      const int hh = h * p.G + n % p.G;
+      p.out[p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d] = f32_to_bf16(A / L);
     } else {
       float* part = p.partial + ((grp * p.splits + split) * kMaxRows + n) * kPartStride;
       part[2 + d] = A;
@@ -427,37 +451,39 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendPara
       }
     }
   }
-  if (p.splits == 1) return;
+}
 
-  // ---- last workgroup of this (layer, head, group) merges the splits -------
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = atomicAdd(&p.counters[grp], 1);
-    s_last = (prev == p.splits - 1);
+// Merge the split partials: one workgroup per (KV head, layer x group, row),
+// one thread per output dim.  Runs after attend_kernel on the same stream, so
+// the partials are visible without device-scope fences.
+__global__ __launch_bounds__(kHeadDim) void attend_merge_kernel(const AttendParams p) {
+  const int h = blockIdx.x;
+  const int layer = blockIdx.y / p.nqg;
+  const int qg = blockIdx.y % p.nqg;
+  const int n = blockIdx.z;
+  const int d = threadIdx.x;
+  const int hq = p.hkv * p.G;
+  const int q0 = qg * p.qpg;
+  const int rows = min(p.qpg, p.tq - q0) * p.G;
+  if (n >= rows) return;
+  const int64_t grp = (static_cast<int64_t>(layer) * p.hkv + h) * p.nqg + qg;
+  const float* base = p.partial + (grp * p.splits * kMaxRows + n) * kPartStride;
+  const int64_t sstride = static_cast<int64_t>(kMaxRows) * kPartStride;
+  float mt = -INFINITY;
+#pragma unroll 8
+  for (int s = 0; s < p.splits; ++s) mt = fmaxf(mt, base[s * sstride]);
+  float L = 0.0f, A = 0.0f;
+#pragma unroll 8
+  for (int s = 0; s < p.splits; ++s) {
+    const float* ps = base + s * sstride;
+    const float ms = ps[0];
+    const float sw = (ms == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ms - mt);
+    L += ps[1] * sw;
+    A += ps[2 + d] * sw;
   }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  for (int idx = threadIdx.x; idx < M * kHeadDim; idx += kAttendThreads) {
-    const int n = idx / kHeadDim, d = idx % kHeadDim;
-    if (n >= rows) continue;
-    const float* base = p.partial + (grp * p.splits * kMaxRows + n) * kPartStride;
-    float mt = -INFINITY;
-    for (int s = 0; s < p.splits; ++s) mt = fmaxf(mt, __builtin_nontemporal_load(base + s * kMaxRows * kPartStride));
-    float L = 0.0f, A = 0.0f;
-    for (int s = 0; s < p.splits; ++s) {
-      const float* ps = base + s * kMaxRows * kPartStride;
-      const float ms = __builtin_nontemporal_load(ps);
-      const float sw = (ms == -INFINITY) ? 0.0f : exp2f(ms - mt);
-      L += __builtin_nontemporal_load(ps + 1) * sw;
-      A += __builtin_nontemporal_load(ps + 2 + d) * sw;
-    }
-    const int t = q0 + n / p.G;
-    const int hh = h * p.G + n % p.G;
-    p.out[p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d] = f32_to_bf16(A / L);
-  }
-  if (threadIdx.x == 0) atomicExch(&p.counters[grp], 0);
+  const int t = q0 + n / p.G;
+  const int hh = h * p.G + n % p.G;
+  p.out[p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d] = f32_to_bf16(A / L);
 }
 
 template <int FMT>
@@ -496,11 +522,10 @@ extern "C" int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads,
 extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
                           int64_t q_layer_stride, int tq, const uint16_t* k_new,
                           const uint16_t* v_new, int64_t kv_layer_stride, int n_chunk,
-                          int new_slot, int write_slot, const int32_t* ids,
-                          int64_t ids_layer_stride, int n_hist, const uint8_t* allowed,
-                          int sink_len, int ring_base, int rec_lo, int rec_len, float scale,
-                          int splits, float* partial_ws, int32_t* counters, uint16_t* out,
-                          void* stream) {
+                          int write_slot, const int32_t* ids, int64_t ids_layer_stride,
+                          int n_hist, const uint8_t* allowed, int sink_len, int ring_base,
+                          int rec_lo, int rec_len, float scale, int splits, float* partial_ws,
+                          uint16_t* out, void* stream) {
   int rc = check_store(st, layer0, num_layers);
   if (rc != NKV_OK) return rc;
   const int G = st->num_heads / st->num_kv_heads;
@@ -514,22 +539,22 @@ extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const
   NKV_CHECK_ARG(rec_len >= 0 && rec_lo >= 0 && rec_lo + rec_len <= R,
                 "nkv_attend: recent range [%d, %d) outside [0, %d)", rec_lo, rec_lo + rec_len, R);
   NKV_CHECK_ARG(ring_base >= 0 && ring_base < R, "nkv_attend: ring_base %d outside [0, %d)", ring_base, R);
-  NKV_CHECK_ARG(n_chunk >= 0 && (n_chunk == 0 || n_chunk == tq),
-                "nkv_attend: a causal chunk must have one token per query (n_chunk=%d, tq=%d)", n_chunk, tq);
-  NKV_CHECK_ARG(new_slot < 0 || (new_slot >= rec_lo && new_slot < rec_lo + rec_len),
-                "nkv_attend: new_slot %d outside the attended recent range", new_slot);
-  NKV_CHECK_ARG((new_slot < 0) == (write_slot < 0),
-                "nkv_attend: new_slot and write_slot must both be set or both be -1");
-  NKV_CHECK_ARG(write_slot < 0 || (write_slot < R && (ring_base + new_slot) % R == write_slot),
-                "nkv_attend: write_slot %d must be the physical slot of new_slot", write_slot);
-  NKV_CHECK_ARG((n_chunk == 0 && new_slot < 0) || (k_new != nullptr && v_new != nullptr),
-                "nkv_attend: k_new/v_new are NULL but new tokens are attended");
-  NKV_CHECK_ARG(!(n_chunk > 0 && new_slot >= 0), "nkv_attend: use either new_slot (decode) or a chunk (verify)");
+  NKV_CHECK_ARG(n_chunk == 0 || n_chunk == tq,
+                "nkv_attend: the causal chunk must have one token per query (n_chunk=%d, tq=%d)", n_chunk, tq);
+  NKV_CHECK_ARG(n_chunk == 0 || (k_new != nullptr && v_new != nullptr),
+                "nkv_attend: k_new/v_new are NULL but n_chunk=%d", n_chunk);
+  NKV_CHECK_ARG(write_slot < R, "nkv_attend: write_slot %d outside the ring", write_slot);
+  NKV_CHECK_ARG(write_slot < 0 || n_chunk >= 1, "nkv_attend: write_slot needs a new token (n_chunk >= 1)");
+  if (write_slot >= 0 && rec_len > 0) {
+    // the slot being written must not be one the call reads
+    const int lp = ((write_slot - ring_base) % R + R) % R;
+    NKV_CHECK_ARG(lp < rec_lo || lp >= rec_lo + rec_len,
+                  "nkv_attend: write_slot %d lies inside the attended recent window", write_slot);
+  }
   NKV_CHECK_ARG(splits >= 1 && splits <= 64, "nkv_attend: splits must be in [1, 64] (got %d)", splits);
-  NKV_CHECK_ARG(splits == 1 || (partial_ws != nullptr && counters != nullptr),
-                "nkv_attend: splits > 1 needs partial_ws and counters");
+  NKV_CHECK_ARG(splits == 1 || partial_ws != nullptr, "nkv_attend: splits > 1 needs partial_ws");
   const int n_sink_seg = (sink_len + kBlock - 1) / kBlock;
-  const int n_rec_seg = (rec_len + kBlock - 1) / kBlock;
+  const int n_rec_seg = rec_len > 0 ? (R + kBlock - 1) / kBlock : 0;
   const int n_chunk_seg = (n_chunk + kBlock - 1) / kBlock;
   const int nseg = n_hist + n_sink_seg + n_rec_seg + n_chunk_seg;
   NKV_CHECK_ARG(nseg >= 1, "nkv_attend: nothing to attend");
@@ -560,7 +585,6 @@ extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const
   p.ids_ls = ids_layer_stride;
   p.allowed = allowed;
   p.partial = partial_ws;
-  p.counters = counters;
   p.out = out;
   p.hkv = st->num_kv_heads;
   p.G = G;
@@ -573,7 +597,6 @@ extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const
   p.qpg = qpg;
   p.nqg = (tq + qpg - 1) / qpg;
   p.n_chunk = n_chunk;
-  p.new_slot = new_slot;
   p.write_slot = write_slot;
   p.n_hist = n_hist;
   p.sink_len = sink_len;
@@ -596,5 +619,7 @@ extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const
     default: bad = -1;
   }
   NKV_CHECK_SUPPORTED(bad == 0, "nkv_attend: unsupported row count %d", M);
+  if (splits > 1)
+    hipLaunchKernelGGL(attend_merge_kernel, dim3(st->num_kv_heads, num_layers * p.nqg, qpg * G), dim3(kHeadDim), 0, s, p);
   return launch_status("nkv_attend");
 }

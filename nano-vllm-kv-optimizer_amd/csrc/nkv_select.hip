@@ -9,14 +9,15 @@
 // (nanovllm/sparse/fused_select.py:23-54) and its eager einsum chain
 // (nanovllm/sparse/m12_runtime.py:999-1003).
 //
-// Mapping: a wavefront owns 64 representative rows = 64/r blocks of one KV
-// head.  The wave first streams that 16 KiB tile with fully coalesced 16-byte
+// Mapping: a wavefront owns one (16-block tile, KV head) unit = 64 rows of
+// r representatives.  It streams that 16 KiB tile with fully coalesced 16-byte
 // loads (lane i reads bytes [1024*c + 16*i, +16)), transposes it through LDS
 // with an XOR swizzle (conflict-free ds_read_b128), and then every lane dots
 // its own row with the G query rows of that head; the query values are
 // wave-uniform, so they are read with scalar loads.  Block maxima across the
-// r rows use lane shuffles; across heads a running max per lane; across the
-// two waves of a workgroup LDS.
+// r rows use lane shuffles; the maximum across KV heads is an atomicMax on
+// the order-preserving uint32 key of the score, which kernel 2 consumes and
+// resets to zero.
 //
 // Kernel 2 (topk_kernel) selects, per (layer[, query]), the k largest scores
 // with protected blocks forced to -inf: an LDS radix select over the 32-bit
@@ -29,7 +30,7 @@
 namespace nkv {
 namespace {
 
-constexpr int kScoreWaves = 2;
+constexpr int kScoreWaves = 4;
 constexpr int kScoreThreads = kScoreWaves * kWave;
 constexpr int kTopkThreads = 256;
 constexpr int kMaxTopk = 1024;
@@ -46,101 +47,92 @@ template <int R, int G>
 __global__ __launch_bounds__(kScoreThreads) void score_kernel(
     const uint16_t* __restrict__ q, int64_t q_ls, int nq, int per_query,
     const uint16_t* __restrict__ reps, int64_t reps_ls, int hkv, int cap,
-    int nblocks, float* __restrict__ scores) {
+    int nblocks, int units, uint32_t* __restrict__ keys) {
   constexpr int TB = kWave / R;  // blocks per tile
-  extern __shared__ uint4 smem[];
-  uint4* stage = smem;  // [kScoreWaves][64 rows][16 chunks], swizzled
-  float* red = reinterpret_cast<float*>(smem + kScoreWaves * 64 * 16);  // [waves][nq'][TB]
+  __shared__ uint4 stage[kScoreWaves][64 * 8];  // per wave: 64 rows x 8 chunks (one half), swizzled
 
   const int nqo = per_query ? nq : 1;
   const int layer = blockIdx.y;
-  const int b0 = blockIdx.x * TB;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int unit = blockIdx.x * kScoreWaves + wave;  // (tile, head) pair
+  if (unit >= units) return;
+  const int h = unit % hkv;
+  const int b0 = (unit / hkv) * TB;
   const int lane = threadIdx.x & 63;
-  const int bl = lane / R;
+  const int b = b0 + lane / R;
   const int hq = hkv * G;
   const uint16_t* qL = q + static_cast<int64_t>(layer) * q_ls;
   const uint16_t* rL = reps + static_cast<int64_t>(layer) * reps_ls;
 
-  for (int i = threadIdx.x; i < kScoreWaves * nqo * TB; i += kScoreThreads) red[i] = -INFINITY;
-  __syncthreads();
+  // The tile is 64 rows x 256 B.  All 16 loads are issued up front; the rows
+  // are then staged and consumed in two halves (dims 0-63, then 64-127), so
+  // each wave needs only 8 KiB of LDS.  Half c8 of chunk c: row = (64c+lane)/16.
+  const uint4* src = reinterpret_cast<const uint4*>(rL + (static_cast<int64_t>(h) * cap + b0) * R * kHeadDim);
+  uint4 v[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    // half hf = c / 8 holds row chunks 8 hf .. 8 hf + 7; chunk index within
+    // the tile: row * 16 + 8 hf + (i & 7) with i = (c % 8) * 64 + lane
+    const int i = (c & 7) * 64 + lane;
+    const int row = i >> 3;
+    const int col = (c >> 3) * 8 + (i & 7);
+    v[c] = (b0 + row / R < nblocks) ? src[row * 16 + col] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  uint4* my = stage[wave];
 
-  uint4* my = stage + wave * 64 * 16;
+  // per query n: dot over both halves in ascending d (half 0 then half 1);
+  // each half is re-staged from registers, so only 8 KiB of LDS per wave.
   float best = -INFINITY;
-  const int n_iter = (hkv + kScoreWaves - 1) / kScoreWaves;
-  for (int it = 0; it < n_iter; ++it) {
-    const int h = wave + kScoreWaves * it;
-    if (h >= hkv) break;  // wave-uniform
-    const uint4* src = reinterpret_cast<const uint4*>(
-        rL + (static_cast<int64_t>(h) * cap + b0) * R * kHeadDim);
-    uint4 v[16];
+  for (int n = 0; n < nq; ++n) {
+    const uint4* qh = reinterpret_cast<const uint4*>(qL + (static_cast<int64_t>(n) * hq + h * G) * kHeadDim);
+    float acc[G];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      const int idx = c * 64 + lane;  // 16-byte chunk index inside the tile
-      const int row = idx >> 4;
-      v[c] = (b0 + row / R < nblocks) ? src[idx] : make_uint4(0u, 0u, 0u, 0u);
-    }
-    wave_lds_sync();  // previous head's reads of `my` are complete
+    for (int g = 0; g < G; ++g) acc[g] = 0.0f;
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      const int idx = c * 64 + lane;
-      const int row = idx >> 4, col = idx & 15;
-      my[row * 16 + (col ^ (row & 15))] = v[c];
-    }
-    wave_lds_sync();
-
-    for (int n = 0; n < nq; ++n) {
-      const uint4* qh = reinterpret_cast<const uint4*>(
-          qL + (static_cast<int64_t>(n) * hq + h * G) * kHeadDim);
-      float acc[G];
+    for (int hf = 0; hf < 2; ++hf) {
+      wave_lds_sync();  // previous half fully consumed
 #pragma unroll
-      for (int g = 0; g < G; ++g) acc[g] = 0.0f;
+      for (int c = 0; c < 8; ++c) {
+        const int i = c * 64 + lane;
+        const int row = i >> 3, col = i & 7;
+        my[row * 8 + (col ^ (row & 7))] = v[hf * 8 + c];
+      }
+      wave_lds_sync();
 #pragma unroll 2
-      for (int c = 0; c < 16; ++c) {
-        const uint4 rv = my[lane * 16 + (c ^ (lane & 15))];
+      for (int c = 0; c < 8; ++c) {
+        const uint4 rv = my[lane * 8 + (c ^ (lane & 7))];
         const float rf[8] = {bf16_lo(rv.x), bf16_hi(rv.x), bf16_lo(rv.y), bf16_hi(rv.y),
                              bf16_lo(rv.z), bf16_hi(rv.z), bf16_lo(rv.w), bf16_hi(rv.w)};
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          const uint4 qv = qh[g * 16 + c];
+          const uint4 qv = qh[g * 16 + hf * 8 + c];
           const float qf[8] = {bf16_lo(qv.x), bf16_hi(qv.x), bf16_lo(qv.y), bf16_hi(qv.y),
                                bf16_lo(qv.z), bf16_hi(qv.z), bf16_lo(qv.w), bf16_hi(qv.w)};
 #pragma unroll
           for (int e = 0; e < 8; ++e) acc[g] = __builtin_fmaf(qf[e], rf[e], acc[g]);
         }
       }
-      float m = acc[0];
+    }
+    float m = acc[0];
 #pragma unroll
-      for (int g = 1; g < G; ++g) m = fmaxf(m, acc[g]);
+    for (int g = 1; g < G; ++g) m = fmaxf(m, acc[g]);
 #pragma unroll
-      for (int o = 1; o < R; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
-      if (per_query) {
-        if ((lane % R) == 0) {
-          float* slot = &red[(wave * nqo + n) * TB + bl];
-          *slot = fmaxf(*slot, m);
-        }
-      } else {
-        best = fmaxf(best, m);
-      }
+    for (int o = 1; o < R; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if (per_query) {
+      if ((lane % R) == 0 && b < nblocks)
+        atomicMax(&keys[(static_cast<int64_t>(layer) * nqo + n) * nblocks + b], score_key(m));
+    } else {
+      best = fmaxf(best, m);
     }
   }
-  if (!per_query && (lane % R) == 0) red[wave * TB + bl] = best;
-  __syncthreads();
-  for (int i = threadIdx.x; i < nqo * TB; i += kScoreThreads) {
-    const int n = i / TB, b = i % TB;
-    if (b0 + b < nblocks) {
-      float m = red[n * TB + b];
-#pragma unroll
-      for (int w = 1; w < kScoreWaves; ++w) m = fmaxf(m, red[(w * nqo + n) * TB + b]);
-      scores[(static_cast<int64_t>(layer) * nqo + n) * nblocks + b0 + b] = m;
-    }
-  }
+  if (!per_query && (lane % R) == 0 && b < nblocks)
+    atomicMax(&keys[static_cast<int64_t>(layer) * nblocks + b], score_key(best));
 }
 
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
-    const float* __restrict__ scores, int nblocks, const int32_t* __restrict__ prot,
+    uint32_t* __restrict__ score_keys, int nblocks, const int32_t* __restrict__ prot,
     int nprot, int k_req, int order, int32_t* __restrict__ out_ids,
-    float* __restrict__ out_vals, int k_stride) {
+    float* __restrict__ out_vals, int k_stride, float* __restrict__ out_scores) {
   extern __shared__ uint32_t sm[];
   uint32_t* keys = sm;                 // [nblocks]
   uint32_t* pmask = keys + nblocks;    // [ceil(nblocks / 32)]
@@ -151,7 +143,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const float* sc = scores + static_cast<int64_t>(row) * nblocks;
+  uint32_t* sk = score_keys + static_cast<int64_t>(row) * nblocks;
   const int nwords = (nblocks + 31) >> 5;
 
   if (tid == 0) {
@@ -159,7 +151,12 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
     s_above = 0u;
   }
   for (int i = tid; i < nwords; i += kTopkThreads) pmask[i] = 0u;
-  for (int i = tid; i < nblocks; i += kTopkThreads) keys[i] = score_key(sc[i]);
+  for (int i = tid; i < nblocks; i += kTopkThreads) {
+    const uint32_t key = sk[i];
+    keys[i] = key;
+    sk[i] = 0u;  // leave the key buffer zeroed for the next scoring pass
+    if (out_scores) out_scores[static_cast<int64_t>(row) * nblocks + i] = key_score(key);
+  }
   __syncthreads();
   for (int i = tid; i < nprot; i += kTopkThreads) {
     const int p = prot[i];
@@ -280,23 +277,23 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
 }
 
 template <int R, int G>
-void launch_score(dim3 grid, size_t smem, hipStream_t s, const uint16_t* q, int64_t q_ls, int nq,
+void launch_score(dim3 grid, hipStream_t s, const uint16_t* q, int64_t q_ls, int nq,
                   int per_query, const uint16_t* reps, int64_t reps_ls, int hkv, int cap,
-                  int nblocks, float* scores) {
-  hipLaunchKernelGGL((score_kernel<R, G>), grid, dim3(kScoreThreads), smem, s, q, q_ls, nq,
-                     per_query, reps, reps_ls, hkv, cap, nblocks, scores);
+                  int nblocks, int units, uint32_t* keys) {
+  hipLaunchKernelGGL((score_kernel<R, G>), grid, dim3(kScoreThreads), 0, s, q, q_ls, nq,
+                     per_query, reps, reps_ls, hkv, cap, nblocks, units, keys);
 }
 
 template <int R>
-int dispatch_g(int g, dim3 grid, size_t smem, hipStream_t s, const uint16_t* q, int64_t q_ls,
-               int nq, int per_query, const uint16_t* reps, int64_t reps_ls, int hkv, int cap,
-               int nblocks, float* scores) {
+int dispatch_g(int g, dim3 grid, hipStream_t s, const uint16_t* q, int64_t q_ls, int nq,
+               int per_query, const uint16_t* reps, int64_t reps_ls, int hkv, int cap,
+               int nblocks, int units, uint32_t* keys) {
   switch (g) {
-    case 1: launch_score<R, 1>(grid, smem, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, scores); return 0;
-    case 2: launch_score<R, 2>(grid, smem, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, scores); return 0;
-    case 4: launch_score<R, 4>(grid, smem, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, scores); return 0;
-    case 8: launch_score<R, 8>(grid, smem, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, scores); return 0;
-    case 16: launch_score<R, 16>(grid, smem, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, scores); return 0;
+    case 1: launch_score<R, 1>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
+    case 2: launch_score<R, 2>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
+    case 4: launch_score<R, 4>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
+    case 8: launch_score<R, 8>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
+    case 16: launch_score<R, 16>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
     default: return -1;
   }
 }
@@ -309,13 +306,13 @@ using namespace nkv;
 extern "C" int nkv_select(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
                           int64_t q_layer_stride, int nq, int per_query, int nblocks,
                           const int32_t* protected_ids, int n_protected, int k, int order,
-                          float* scores_ws, int32_t* out_ids, float* out_vals, void* stream) {
+                          uint32_t* score_keys, float* out_scores, int32_t* out_ids,
+                          float* out_vals, void* stream) {
   int rc = check_store(st, layer0, num_layers);
   if (rc != NKV_OK) return rc;
-  NKV_CHECK_ARG(q != nullptr && scores_ws != nullptr && out_ids != nullptr,
-                "nkv_select: q, scores_ws and out_ids must be non-NULL");
+  NKV_CHECK_ARG(q != nullptr && score_keys != nullptr && out_ids != nullptr,
+                "nkv_select: q, score_keys and out_ids must be non-NULL");
   NKV_CHECK_ARG(nq >= 1 && nq <= 64, "nkv_select: nq must be in [1, 64] (got %d)", nq);
-  NKV_CHECK_ARG(!per_query || nq <= 16, "nkv_select: per-query selection supports nq <= 16 (got %d)", nq);
   NKV_CHECK_ARG(nblocks >= 1, "nkv_select: selection needs at least one history block (nblocks=%d)", nblocks);
   NKV_CHECK_ARG(nblocks <= st->cap_blocks, "nkv_select: nblocks %d exceeds cap_blocks %d", nblocks, st->cap_blocks);
   NKV_CHECK_SUPPORTED(nblocks <= kMaxSelectBlocks, "nkv_select: nblocks %d exceeds %d", nblocks, kMaxSelectBlocks);
@@ -333,14 +330,14 @@ extern "C" int nkv_select(const nkv_store* st, int layer0, int num_layers, const
   const int nqo = per_query ? nq : 1;
   const int64_t reps_ls = static_cast<int64_t>(st->num_kv_heads) * st->cap_blocks * R * kHeadDim;
   const uint16_t* reps = static_cast<const uint16_t*>(st->reps) + layer0 * reps_ls;
-  dim3 grid((nblocks + TB - 1) / TB, num_layers);
-  const size_t smem = kScoreWaves * 64 * 16 * sizeof(uint4) + kScoreWaves * nqo * TB * sizeof(float);
+  const int units = ((nblocks + TB - 1) / TB) * st->num_kv_heads;
+  dim3 grid((units + kScoreWaves - 1) / kScoreWaves, num_layers);
   int bad = 0;
   switch (R) {
-    case 1: bad = dispatch_g<1>(g, grid, smem, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, scores_ws); break;
-    case 2: bad = dispatch_g<2>(g, grid, smem, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, scores_ws); break;
-    case 4: bad = dispatch_g<4>(g, grid, smem, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, scores_ws); break;
-    case 8: bad = dispatch_g<8>(g, grid, smem, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, scores_ws); break;
+    case 1: bad = dispatch_g<1>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
+    case 2: bad = dispatch_g<2>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
+    case 4: bad = dispatch_g<4>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
+    case 8: bad = dispatch_g<8>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
     default: bad = -1;
   }
   NKV_CHECK_SUPPORTED(bad == 0, "nkv_select: unsupported (r=%d, G=%d)", R, g);
@@ -349,7 +346,7 @@ extern "C" int nkv_select(const nkv_store* st, int layer0, int num_layers, const
 
   const int nwords = (nblocks + 31) >> 5;
   const size_t tsmem = static_cast<size_t>(nblocks + nwords) * sizeof(uint32_t);
-  hipLaunchKernelGGL(topk_kernel, dim3(num_layers * nqo), dim3(kTopkThreads), tsmem, s, scores_ws,
-                     nblocks, protected_ids, n_protected, k, order, out_ids, out_vals, k);
+  hipLaunchKernelGGL(topk_kernel, dim3(num_layers * nqo), dim3(kTopkThreads), tsmem, s, score_keys,
+                     nblocks, protected_ids, n_protected, k, order, out_ids, out_vals, k, out_scores);
   return launch_status("nkv_select/topk");
 }

@@ -202,7 +202,6 @@ class _SparseCore:
         self._prot_key = None
         self._prot_dev = None
         self._ws: dict[str, torch.Tensor] = {}
-        self._counters = torch.zeros(0, dtype=torch.int32, device=self.device)
 
     # -- workspaces ---------------------------------------------------------
     def _buf(self, name: str, numel: int, dtype) -> torch.Tensor:
@@ -212,10 +211,13 @@ class _SparseCore:
             self._ws[name] = t
         return t[:numel]
 
-    def _counter_buf(self, n: int) -> torch.Tensor:
-        if self._counters.numel() < n:
-            self._counters = torch.zeros(n, dtype=torch.int32, device=self.device)
-        return self._counters
+    def _zeroed_keys(self, numel: int) -> torch.Tensor:
+        """Score-key workspace: zero before first use, left zero by every select."""
+        t = self._ws.get("keys")
+        if t is None or t.numel() < numel:
+            t = torch.zeros(max(numel, 1), dtype=torch.int32, device=self.device)
+            self._ws["keys"] = t
+        return t[:numel]
 
     def reset(self) -> None:
         self.valid_len = 0
@@ -303,11 +305,12 @@ class _SparseCore:
         nl, nq = q.shape[0], q.shape[1]
         nqo = nq if per_query else 1
         prot, n_prot = self.protected_dev()
+        keys = self._zeroed_keys(nl * nqo * nb)
         scores = self._buf("scores", nl * nqo * nb, torch.float32)
         ids = self._buf("ids", nl * nqo * requested, torch.int32).view(nl, nqo, requested)
         vals = self._buf("vals", nl * nqo * requested, torch.float32).view(nl, nqo, requested)
         self.store.select(self.layer0, q, nb, prot, n_prot, requested, order, per_query,
-                          scores, ids, vals)
+                          keys, scores, ids, vals)
         self._last_scores = scores.view(nl, nqo, nb)
         return ids, vals, self.effective_k(requested)
 
@@ -315,24 +318,27 @@ class _SparseCore:
     def _splits(self, nseg: int, nqg: int) -> int:
         if self.cfg.attend_splits is not None:
             return self.cfg.attend_splits
-        want = -(-2048 // (self.store.num_kv_heads * self.nl * nqg))
+        # ~900 workgroups per launch (about 3.5 per CU on 256 CUs) measured
+        # best for the 36-layer 32K decode step; never more than one segment
+        # per wavefront.
+        want = max(1, round(900 / (self.store.num_kv_heads * self.nl * nqg)))
         return max(1, min(-(-nseg // 4), want, 64))
 
-    def attend(self, q, k_new, v_new, *, n_chunk, new_slot, write_slot, ids, ids_stride,
+    def attend(self, q, k_new, v_new, *, n_chunk, write_slot, ids, ids_stride,
                n_hist, allowed, sink_len, ring_base, rec_lo, rec_len):
         cfg = self.cfg
         nl, tq = q.shape[0], q.shape[1]
         g = cfg.num_heads // cfg.num_kv_heads
         qpg = min(tq, max(1, 16 // g))
         nqg = -(-tq // qpg)
-        nseg = n_hist + -(-sink_len // 64) + -(-rec_len // 64) + -(-n_chunk // 64)
+        R = cfg.recent_tokens
+        nseg = n_hist + -(-sink_len // 64) + (-(-R // 64) if rec_len else 0) + -(-n_chunk // 64)
         splits = self._splits(nseg, nqg)
         out = torch.empty_like(q)
         part = self._buf("partial", self.store.attend_workspace_floats(nl, tq, splits), torch.float32)
-        counters = self._counter_buf(nl * self.store.num_kv_heads * nqg)
-        self.store.attend(self.layer0, q, k_new, v_new, n_chunk, new_slot, write_slot, ids,
+        self.store.attend(self.layer0, q, k_new, v_new, n_chunk, write_slot, ids,
                           ids_stride, n_hist, allowed, sink_len, ring_base, rec_lo, rec_len,
-                          cfg.scale, splits, part, counters, out)
+                          cfg.scale, splits, part, out)
         return out
 
     def decode_attend(self, q, k, v, ids, ids_stride, n_hist):
@@ -341,11 +347,14 @@ class _SparseCore:
         R = cfg.recent_tokens
         sink_len = min(cfg.sink_tokens, self.valid_len)
         rec_len = min(R, self.valid_len + 1)
-        out = self.attend(q.contiguous(), k.contiguous(), v.contiguous(), n_chunk=0,
-                          new_slot=R - 1, write_slot=self.ring_start, ids=ids,
+        # logical window after the shift = [R - rec_len, R); its last slot is
+        # the new token, attended as a one-token chunk and stored into the
+        # freed physical slot (the old logical slot 0).
+        out = self.attend(q.contiguous(), k.contiguous(), v.contiguous(), n_chunk=1,
+                          write_slot=self.ring_start, ids=ids,
                           ids_stride=ids_stride, n_hist=n_hist, allowed=None,
                           sink_len=sink_len, ring_base=(self.ring_start + 1) % R,
-                          rec_lo=R - rec_len, rec_len=rec_len)
+                          rec_lo=R - rec_len, rec_len=rec_len - 1)
         self.ring_start = (self.ring_start + 1) % R
         self.valid_len += 1
         return out, sink_len, rec_len
@@ -356,7 +365,7 @@ class _SparseCore:
         sink_len = min(cfg.sink_tokens, self.valid_len)
         _, off, ln = prefill_recent_slice(self.valid_len, cfg.sink_tokens, cfg.recent_tokens)
         out = self.attend(q.contiguous(), k.contiguous(), v.contiguous(), n_chunk=q.shape[1],
-                          new_slot=-1, write_slot=-1, ids=ids, ids_stride=ids_stride,
+                          write_slot=-1, ids=ids, ids_stride=ids_stride,
                           n_hist=n_hist, allowed=allowed, sink_len=sink_len,
                           ring_base=self.ring_start, rec_lo=off, rec_len=ln)
         return out, sink_len, ln

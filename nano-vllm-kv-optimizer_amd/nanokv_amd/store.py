@@ -122,27 +122,28 @@ class SparseKVStore:
             "recent_update")
 
     def select(self, layer0: int, q, nblocks: int, prot_dev, n_prot: int, k: int, order: int,
-               per_query: bool, scores_ws, out_ids, out_vals) -> None:
+               per_query: bool, score_keys, out_scores, out_ids, out_vals) -> None:
+        """score_keys: zeroed uint32 workspace (left zeroed); out_scores may be None."""
         self._bf16(q, "q")
         nl, nq = q.shape[0], q.shape[1]
         _lib.check(self.lib.nkv_select(
             self._desc_ref, layer0, nl, _ptr(q), q.stride(0), nq, int(per_query), nblocks,
-            _ptr(prot_dev), n_prot, k, order, _ptr(scores_ws), _ptr(out_ids), _ptr(out_vals),
-            _stream()), "select")
+            _ptr(prot_dev), n_prot, k, order, _ptr(score_keys), _ptr(out_scores), _ptr(out_ids),
+            _ptr(out_vals), _stream()), "select")
 
-    def attend(self, layer0: int, q, k_new, v_new, n_chunk: int, new_slot: int,
+    def attend(self, layer0: int, q, k_new, v_new, n_chunk: int,
                write_slot: int, ids, ids_layer_stride: int, n_hist: int, allowed,
                sink_len: int, ring_base: int, rec_lo: int, rec_len: int, scale: float,
-               splits: int, partial_ws, counters, out) -> None:
+               splits: int, partial_ws, out) -> None:
         self._bf16(q, "q")
         self._bf16(out, "out")
         nl, tq = q.shape[0], q.shape[1]
         kv_stride = k_new.stride(0) if k_new is not None else 0
         _lib.check(self.lib.nkv_attend(
             self._desc_ref, layer0, nl, _ptr(q), q.stride(0), tq, _ptr(k_new), _ptr(v_new),
-            kv_stride, n_chunk, new_slot, write_slot, _ptr(ids), ids_layer_stride, n_hist,
+            kv_stride, n_chunk, write_slot, _ptr(ids), ids_layer_stride, n_hist,
             _ptr(allowed), sink_len, ring_base, rec_lo, rec_len, float(scale), splits,
-            _ptr(partial_ws), _ptr(counters), _ptr(out), _stream()), "attend")
+            _ptr(partial_ws), _ptr(out), _stream()), "attend")
 
     def attend_workspace_floats(self, nl: int, tq: int, splits: int) -> int:
         return int(self.lib.nkv_attend_workspace_floats(nl, self.num_kv_heads, self.num_heads,

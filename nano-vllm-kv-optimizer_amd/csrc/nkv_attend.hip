@@ -177,9 +177,18 @@ __device__ __forceinline__ Seg make_seg(const AttendParams& p, int layer, int h,
   return g;
 }
 
+// LDS floats of one workgroup: the per-wave p tiles during the segment loop,
+// reused afterwards for the cross-wave merge (m, l and acc of every wave).
+template <int M>
+constexpr int attend_lds_floats() {
+  return kAttendWaves * kBlock * kPRow > 2 * kAttendWaves * kMaxRows + kAttendWaves * M * kHeadDim
+             ? kAttendWaves * kBlock * kPRow
+             : 2 * kAttendWaves * kMaxRows + kAttendWaves * M * kHeadDim;
+}
+
 template <int FMT, int M>
 __global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendParams p) {
-  __shared__ __attribute__((aligned(16))) float s_p[kAttendWaves][kBlock * kPRow];
+  __shared__ __attribute__((aligned(16))) float s_lds[attend_lds_floats<M>()];
   __shared__ float s_alpha[kAttendWaves][kMaxRows];
 
   const int split = blockIdx.x;
@@ -246,7 +255,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendPara
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[n][e] = 0.0f;
 
-  float* my_p = s_p[wave];
+  float* my_p = s_lds + wave * kBlock * kPRow;
   const int nwaves = p.splits * kAttendWaves;
   for (int sidx = split * kAttendWaves + wave; sidx < p.nseg; sidx += nwaves) {
     const Seg g = make_seg<FMT>(p, layer, h, sidx);
@@ -408,7 +417,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendPara
 
   // ---- merge the 4 wavefronts in LDS (reusing the p tiles) -----------------
   __syncthreads();
-  float* s_m = &s_p[0][0];                         // [waves][16]
+  float* s_m = s_lds;                              // [waves][16]
   float* s_l = s_m + kAttendWaves * kMaxRows;      // [waves][16]
   float* s_acc = s_l + kAttendWaves * kMaxRows;    // [waves][M][128]
   if (lane < kMaxRows) {

@@ -1,0 +1,56 @@
+"""The C ABI library: loads on a machine without a GPU, exports every entry
+point include/nanokv.h declares, and rejects bad arguments before touching
+the device (no compute calls here)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from nanokv_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nanokv.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"\b(?:int|int64_t|const char\s*\*)\s+(nkv_\w+)\s*\(([^)]*)\)\s*;", text):
+        args = [a.strip() for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
+        decls[m.group(1)] = len(args)
+    return decls
+
+
+def test_library_loads_and_reports_abi_version():
+    lib = _lib.load()
+    assert lib.nkv_abi_version() == _lib.ABI_VERSION
+
+
+def test_every_declared_entry_point_is_exported_with_matching_arity():
+    lib = _lib.load()
+    decls = _declared()
+    assert {"nkv_select", "nkv_attend", "nkv_store_chunk", "nkv_build_reps",
+            "nkv_recent_update", "nkv_query_summaries"} <= set(decls)
+    for name, nargs in decls.items():
+        assert hasattr(lib, name), f"{name} not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+        assert len(_lib.SIGNATURES[name][1]) == nargs, f"{name}: {nargs} args declared"
+
+
+def test_bad_arguments_are_rejected_before_any_device_work():
+    lib = _lib.load()
+    rc = lib.nkv_select(None, 0, 1, None, 0, 1, 0, 1, None, 0, 32, 0, None, None, None, None, None)
+    assert rc == _lib.NKV_ERR_ARG
+    assert b"store descriptor is NULL" in lib.nkv_last_error()
+    st = _lib.NkvStore()
+    st.head_dim, st.block_size = 64, 64
+    rc = lib.nkv_attend(ctypes.byref(st), 0, 1, None, 0, 1, None, None, 0, 0, -1, None, 0, 0,
+                        None, 0, 0, 0, 0, 1.0, 1, None, None, None)
+    assert rc == _lib.NKV_ERR_UNSUPPORTED
+    with pytest.raises(ValueError, match="head_dim"):
+        _lib.check(rc, "attend")
+    rc = lib.nkv_query_summaries(None, 0, 1, 8, 32, 128, 1, None, 0, None)
+    assert rc == _lib.NKV_ERR_ARG

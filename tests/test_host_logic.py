@@ -1,0 +1,77 @@
+"""Host-side logic of the runtime mirror (no GPU): config validation and the
+reference's module-level helpers, with the reference tests' known answers."""
+
+import pytest
+import torch
+
+from nanokv_amd.sparse import m12_runtime as rt
+from oracle import nkv_oracle as O
+
+
+@pytest.mark.parametrize("budget", [0, 33])
+def test_prefill_budget_cannot_exceed_allocated_maximum(budget):
+    # reference tests/test_m17_prefill_budget.py:9-12
+    with pytest.raises(ValueError, match="prefill_top_k_blocks"):
+        rt.M12Config(top_k_blocks=32, prefill_top_k_blocks=budget)
+
+
+@pytest.mark.parametrize("budget", [0, 33])
+def test_decode_budget_cannot_exceed_allocated_maximum(budget):
+    # reference tests/test_m17_prefill_budget.py:66-69
+    with pytest.raises(ValueError, match="decode_top_k_blocks"):
+        rt.M12Config(top_k_blocks=32, decode_top_k_blocks=budget)
+
+
+def test_pipeline_requires_direct_pinned_gather():
+    # reference tests/test_m20_kv_pipeline.py:9-11
+    with pytest.raises(ValueError, match="requires use_index_select"):
+        rt.M12Config(use_index_select=False, decode_kv_pipeline=True)
+
+
+@pytest.mark.parametrize("kw,msg", [
+    ({"decode_relative_a": 1.5}, "decode_relative_a"),
+    ({"decode_relative_a": 0.5, "decode_relative_max_blocks": 0}, "decode_relative_max_blocks"),
+    ({"decode_query_window": 0}, "decode_query_window"),
+    ({"fused_dequant": True}, "fused_dequant requires quant_history"),
+    ({"quant_scale_layout": "row"}, "quant_scale_layout"),
+    ({"attend_splits": 0}, "attend_splits"),
+])
+def test_config_validation_errors(kw, msg):
+    with pytest.raises(ValueError, match=msg):
+        rt.M12Config(**kw)
+
+
+def test_kv_format_mapping():
+    assert rt.M12Config().kv_format == "bf16"
+    assert rt.M12Config(quant_history=True).kv_format == "int8"
+    assert rt.M12Config(quant_history=True, quant_scale_layout="token").kv_format == "int8_token"
+
+
+@pytest.mark.parametrize("bad", [
+    {"dtype": torch.float32}, {"head_dim": 64}, {"block_size": 32}, {"num_heads": 24}, {"r": 3},
+])
+def test_hip_runtime_rejects_shapes_the_kernels_do_not_cover(bad):
+    with pytest.raises(ValueError):
+        rt._check_hip_shapes(rt.M12Config(**bad))
+
+
+def test_prefill_recent_slice_known_answers():
+    # reference tests/test_m14_prefill_layout.py:34-44
+    assert rt.prefill_recent_slice(4096, 64, 512) == (3584, 0, 512)
+    assert rt.prefill_recent_slice(128, 64, 512) == (0, 64, 64)
+    assert rt.prefill_recent_slice(64, 64, 512) == (0, 64, 0)
+    for v in range(0, 1300, 37):
+        assert rt.prefill_recent_slice(v, 64, 512) == O.prefill_recent_slice(v, 64, 512)
+
+
+def test_dynamic_top_k_known_answers():
+    # reference tests/test_m16_dynamic_topk.py:13-22
+    f = rt.dynamic_top_k_from_scores
+    assert f(torch.ones(32), 32, 0.90) == 32
+    assert f(torch.arange(10, 0, -1).float(), 32, 0.90) == 10
+    assert f(torch.tensor([float("inf")] + [0.0] * 31), 32, 0.90) == 32
+    assert f(torch.tensor([10.0] + [0.0] * 31), 32, 0.90) == 16
+    g = torch.Generator().manual_seed(3)
+    for _ in range(50):
+        s = torch.sort(torch.randn(32, generator=g) * 3, descending=True).values
+        assert f(s, 32, 0.9) == O.dynamic_top_k_from_scores(s.numpy(), 32, 0.9)

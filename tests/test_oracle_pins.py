@@ -1,0 +1,325 @@
+"""Pins of the CPU oracle (oracle/nkv_oracle.py) -- no GPU needed.
+
+Each oracle function is checked against (a) the known answers the
+reference's own tests hold, (b) an independent formulation that mathematics
+fixes (exact rational arithmetic, brute force, textbook softmax), chosen so
+that a dropped term, a swapped operand or a wrong index fails.
+"""
+
+import math
+import random
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import nkv_oracle as O
+
+
+# ---------------------------------------------------------------- rounding --
+
+def test_bf16_round_matches_torch_and_ties_to_even():
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal(10000) * np.exp(rng.uniform(-20, 20, 10000))).astype(np.float32)
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(O.bf16_round(x), ref)
+    # exact halfway cases: 1 + 2^-8 lies between 1 and 1 + 2^-7 -> even (1.0)
+    half = np.array([1 + 2 ** -8, 1 + 3 * 2 ** -8, -(1 + 2 ** -8)], dtype=np.float32)
+    assert O.bf16_round(half).tolist() == [1.0, 1 + 2 ** -6, -1.0]
+
+
+def test_f64_to_bf16_is_one_correct_rounding():
+    rng = random.Random(1)
+    for _ in range(3000):
+        v = rng.uniform(-1, 1) * 2.0 ** rng.randint(-140, 100)
+        got = float(O.f64_to_bf16(np.array([v]))[0])
+        # exact: the bf16 grid around v, nearest, ties to even (Fraction arithmetic)
+        fv = Fraction(v)
+        m, e = math.frexp(v)
+        q = Fraction(2) ** max(e - 8, -133)          # bf16 quantum at this binade
+        lo = (fv / q).__floor__()
+        cands = [lo * q, (lo + 1) * q]
+        d0, d1 = abs(fv - cands[0]), abs(fv - cands[1])
+        if d0 < d1 or (d0 == d1 and lo % 2 == 0):
+            want = cands[0]
+        else:
+            want = cands[1]
+        assert Fraction(got) == want, v
+
+
+# ----------------------------------------------------------------- scores --
+
+def _rand_bf16(rng, shape, scale=1.0):
+    return O.bf16_round((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+def test_block_scores_equal_a_pure_python_sequential_loop():
+    rng = np.random.default_rng(2)
+    q = _rand_bf16(rng, (2, 8, 128))          # Nq=2, Hq=8
+    reps = _rand_bf16(rng, (2, 5, 3, 128), 128 ** -0.5)   # Hkv=2, nb=5, r=3
+    got = O.block_scores(q, reps, 5, 2)
+    for b in range(5):
+        best = None
+        for n in range(2):
+            for hq in range(8):
+                h = hq // 4
+                for j in range(3):
+                    acc = np.float32(0.0)
+                    for d in range(128):
+                        acc = np.float32(acc + np.float32(q[n, hq, d]) * np.float32(reps[h, b, j, d]))
+                    best = acc if best is None else max(best, acc)
+        assert np.float32(got[b]) == best
+
+
+def test_block_scores_are_the_exact_dot_within_fp32_bound():
+    rng = np.random.default_rng(3)
+    q = _rand_bf16(rng, (1, 32, 128))
+    reps = _rand_bf16(rng, (8, 6, 4, 128), 128 ** -0.5)
+    got = O.block_scores(q, reps, 6, 8)
+    u = 2.0 ** -24
+    for b in range(6):
+        exact_best, bound = None, 0.0
+        for hq in range(32):
+            h = hq // 4
+            for j in range(4):
+                terms = [Fraction(float(q[0, hq, d])) * Fraction(float(reps[h, b, j, d])) for d in range(128)]
+                ex = sum(terms, Fraction(0))
+                if exact_best is None or ex > exact_best:
+                    exact_best = ex
+                bound = max(bound, 128 * u * float(sum(abs(t) for t in terms)))
+        assert abs(Fraction(float(got[b])) - exact_best) <= Fraction(bound)
+
+
+def test_gqa_map_routes_each_query_head_to_its_kv_head():
+    # block_sparse.py:33-41 / test_block_sparse.py:192-207: heads 0..3 -> kv 0, 4..7 -> kv 1
+    assert O.kv_head_for_query(4, 2).tolist() == [0, 0, 1, 1]
+    reps = np.zeros((2, 2, 1, 128), np.float32)
+    reps[1, 1, 0, 0] = 1.0            # only KV head 1, block 1 has signal
+    q = np.zeros((1, 8, 128), np.float32)
+    q[0, 5, 0] = 2.0                  # query head 5 -> KV head 1: sees it
+    assert O.block_scores(q, reps, 2, 2).tolist() == [0.0, 2.0]
+    q[0, 5, 0] = 0.0
+    q[0, 2, 0] = 2.0                  # query head 2 -> KV head 0: does not
+    assert O.block_scores(q, reps, 2, 2).tolist() == [0.0, 0.0]
+
+
+# ------------------------------------------------------------------ top-k --
+
+def test_topk_known_answers_from_reference_tests():
+    # test_block_sparse.py:156-161
+    ids, vals = O.topk_blocks(np.array([0.0, 5.0, 1.0, 4.0, 2.0], np.float32), set(), 2)
+    assert ids.tolist() == [1, 3] and vals.tolist() == [5.0, 4.0]
+    # test_m19_selector_graph.py:68-87: budget capped after protection; all protected -> one id
+    s = np.array([0.3, 0.1, 0.2], np.float32)
+    ids, _ = O.topk_blocks(s, {0, 20}, 6)
+    assert ids.tolist() == [2, 1]
+    ids, _ = O.topk_blocks(s, {0, 1, 2, 20}, 6)
+    assert ids.tolist() == [0]
+    # test_m21_static_mask.py:28-45: exact ties, protected {0, 4}
+    ids, _ = O.topk_blocks(np.zeros(8, np.float32), {0, 4, 100}, 6)
+    assert ids.tolist() == [1, 2, 3, 5, 6, 7]
+
+
+def test_topk_against_brute_force_sort():
+    rng = random.Random(4)
+    for _ in range(300):
+        nb = rng.randint(1, 40)
+        s = np.array([rng.choice([rng.uniform(-3, 3), 0.5, -0.0, float("-inf")]) for _ in range(nb)], np.float32)
+        prot = {rng.randint(-2, nb + 2) for _ in range(rng.randint(0, 5))}
+        k = rng.randint(1, 45)
+        ids, vals = O.topk_blocks(s, prot, k)
+        masked = [(-math.inf if b in prot else float(s[b])) for b in range(nb)]
+        n_prot = len([p for p in prot if 0 <= p < nb])
+        kk = min(k, max(1, nb - n_prot))
+        want = sorted(range(nb), key=lambda b: (-masked[b], b))[:kk]
+        assert ids.tolist() == want
+
+
+def test_per_query_union_and_allowed_mask():
+    rng = np.random.default_rng(5)
+    q = _rand_bf16(rng, (3, 8, 128))
+    reps = _rand_bf16(rng, (2, 20, 2, 128), 128 ** -0.5)
+    prot = {0, 19}
+    union, allowed, tops = O.select_per_query(q, reps, 20, 2, prot, 4)
+    for t in range(3):
+        own = O.topk_blocks(O.block_scores(q[t:t + 1], reps, 20, 2), prot, 4)[0]
+        assert tops[t].tolist() == own.tolist()
+        assert set(union[allowed[t]].tolist()) == set(own.tolist())
+    assert union.tolist() == sorted(set(tops.reshape(-1).tolist()))
+
+
+def test_dynamic_top_k_known_answers():
+    # test_m16_dynamic_topk.py:13-22
+    f = O.dynamic_top_k_from_scores
+    assert f(np.ones(32, np.float32), 32, 0.90) == 32
+    assert f(np.arange(10, 0, -1).astype(np.float32), 32, 0.90) == 10
+    assert f(np.array([np.inf] + [0.0] * 31, np.float32), 32, 0.90) == 32
+    assert f(np.array([10.0] + [0.0] * 31, np.float32), 32, 0.90) == 16
+
+
+# ------------------------------------------------------------ bookkeeping --
+
+def test_prefill_recent_slice_known_answers():
+    # test_m14_prefill_layout.py:34-44
+    assert O.prefill_recent_slice(4096, 64, 512) == (3584, 0, 512)
+    assert O.prefill_recent_slice(128, 64, 512) == (0, 64, 64)
+    assert O.prefill_recent_slice(64, 64, 512) == (0, 64, 0)
+
+
+def test_prefill_layout_covers_every_prior_token_once():
+    # test_m14_prefill_layout.py:12-37: selected (all non-protected) + sink + recent
+    valid_len, B, S, R = 4096, 64, 64, 512
+    nb = valid_len // B
+    prot = O.protected_blocks_after_store(nb, R, B)
+    selected = {t for b in range(nb) if b not in prot for t in range(b * B, (b + 1) * B)}
+    sink = set(range(min(S, valid_len)))
+    start, off, ln = O.prefill_recent_slice(valid_len, S, R)
+    recent = set(range(start + off, start + off + ln))
+    assert not (selected & sink) and not (selected & recent) and not (sink & recent)
+    assert selected | sink | recent == set(range(valid_len))
+
+
+def test_protected_set_after_store():
+    # m12_runtime.py:509-513: {0} U last 8 blocks
+    assert O.protected_blocks_after_store(128, 512, 64) == {0} | set(range(120, 128))
+    assert O.protected_blocks_after_store(5, 512, 64) == {0, 1, 2, 3, 4}
+
+
+def test_query_summaries_are_segment_means():
+    # test_m14_prefill_layout.py:47-58 (values exact in bf16)
+    q = np.arange(8 * 2 * 3, dtype=np.float32).reshape(8, 2, 3)
+    assert np.array_equal(O.query_summaries(q, 1)[0], q.mean(axis=0))
+    want = np.stack([q[0:2].mean(0), q[2:4].mean(0), q[4:6].mean(0), q[6:8].mean(0)])
+    assert np.array_equal(O.query_summaries(q, 4), want)
+    # tensor_split bounds with a remainder: 10 tokens in 4 parts -> 3, 3, 2, 2
+    assert O.tensor_split_bounds(10, 4) == [(0, 3), (3, 6), (6, 8), (8, 10)]
+    assert [t.shape[0] for t in torch.tensor_split(torch.zeros(10), 4)] == [3, 3, 2, 2]
+
+
+# -------------------------------------------------------------- attention --
+
+def test_attention_matches_manual_softmax():
+    # test_block_sparse.py:36-49: per-head manual softmax(q k^T / sqrt(d)) v
+    rng = np.random.default_rng(6)
+    q = rng.standard_normal((1, 4, 8))
+    k = rng.standard_normal((10, 2, 8))
+    v = rng.standard_normal((10, 2, 8))
+    out = O.attention_fp64(q, k, v, 8 ** -0.5)
+    for hq in range(4):
+        h = hq // 2
+        logits = [sum(q[0, hq, d] * k[s, h, d] for d in range(8)) * 8 ** -0.5 for s in range(10)]
+        mx = max(logits)
+        w = [math.exp(x - mx) for x in logits]
+        tot = sum(w)
+        for d in range(8):
+            want = sum(w[s] / tot * v[s, h, d] for s in range(10))
+            assert abs(out[0, hq, d] - want) < 1e-12
+
+
+def test_causal_mask_and_select_all_equals_dense():
+    # m12_runtime.py:877-883: query t sees history and chunk keys <= t
+    m = O.causal_mask(3, 6, 3)
+    assert m.tolist() == [[False, False, False, False, True, True],
+                          [False, False, False, False, False, True],
+                          [False, False, False, False, False, False]]
+    # test_block_sparse.py:236-242: attending every token == dense
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((1, 4, 8))
+    k = rng.standard_normal((48, 2, 8))
+    v = rng.standard_normal((48, 2, 8))
+    perm = rng.permutation(48)
+    a = O.attention_fp64(q, k, v, 0.3)
+    b = O.attention_fp64(q, k[perm], v[perm], 0.3)
+    assert np.allclose(a, b, atol=1e-12, rtol=0)
+
+
+# ------------------------------------------------------------------- int8 --
+
+def test_int8_scheme_matches_torch_round_half_even_and_clamp():
+    # quant_kv.py:27-49: round(x / scale).clamp(-127, 127), torch.round = half-to-even
+    x = np.array([0.5, 1.5, 2.5, -0.5, -2.5, 300.0, -300.0, 126.5], np.float32)
+    assert O.quantize(x, np.float32(1.0)).tolist() == [0, 2, 2, 0, -2, 127, -127, 126]
+    rng = np.random.default_rng(8)
+    kb = _rand_bf16(rng, (3, 64, 2, 128), 128 ** -0.5)
+    ks = O.k_scale_from_chunk(kb)
+    t = torch.from_numpy(kb)
+    ks_t = t.float().abs().amax(dim=(0, 1)).clamp_min(1e-8) / 127
+    assert np.array_equal(ks, ks_t.numpy())
+    kq_t = torch.round(t.float() / ks_t).clamp(-127, 127).to(torch.int8)
+    assert np.array_equal(O.quantize(kb, ks), kq_t.numpy())
+    vs = O.v_scale_per_block(kb)
+    vs_t = t.float().abs().amax(dim=(1, 3)).clamp_min(1e-8) / 127
+    assert np.array_equal(vs, vs_t.numpy())
+    vq_t = torch.round(t.float() / vs_t[:, None, :, None]).clamp(-127, 127).to(torch.int8)
+    assert np.array_equal(O.quantize(kb, vs[:, None, :, None]), vq_t.numpy())
+    # dequantisation as packed by the reference: bf16(int8 * scale)
+    deq_t = (kq_t.float() * ks_t).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(O.dequant_to_bf16(O.quantize(kb, ks), ks), deq_t)
+
+
+def test_token_scale_fp16_closed_form():
+    x = np.zeros((2, 128), np.float32)
+    x[0, 7] = -254.0                      # amax 254 -> 254/127 = 2.0 exactly
+    sc = O.token_scale_fp16(x)
+    assert sc.dtype == np.float16
+    assert float(sc[0]) == 2.0
+    assert float(sc[1]) == 2.0 ** -24     # all-zero row: smallest fp16 subnormal
+
+
+# -------------------------------------------------------- representatives --
+
+def _reps_loop(kb, r):
+    """Direct loop restatement of m12_runtime.py:354-395 for one (block, head)."""
+    B, D = kb.shape
+    dirs = []
+    for t in range(B):
+        n = math.sqrt(sum(float(x) ** 2 for x in kb[t]))
+        dirs.append([float(x) / max(n, 1e-12) for x in kb[t]])
+    mean = [sum(dirs[t][d] for t in range(B)) / B for d in range(D)]
+    mn = math.sqrt(sum(m * m for m in mean))
+    md = [m / max(mn, 1e-12) for m in mean]
+    cos0 = [sum(dirs[t][d] * md[d] for d in range(D)) for t in range(B)]
+    chosen = [max(range(B), key=lambda t: (cos0[t], -t))]
+    for _ in range(1, r):
+        def score(t):
+            mx = max(sum(dirs[t][d] * dirs[c][d] for d in range(D)) for c in chosen)
+            return 2.0 if t in chosen else mx
+        chosen.append(min(range(B), key=lambda t: (score(t), t)))
+    return chosen
+
+
+def test_build_reps_matches_loop_restatement_and_invariants():
+    rng = np.random.default_rng(9)
+    kb = _rand_bf16(rng, (3, 12, 2, 6))           # N=3 blocks, B=12 tokens, Hkv=2, D=6
+    kb[2, 5:] = 0.0                               # zero-padded tail of a partial block
+    sel, reps, margins = O.build_reps(kb, 4)
+    for n in range(3):
+        for h in range(2):
+            if np.all(margins[n, h] > 1e-9):
+                assert sel[n, h].tolist() == _reps_loop(kb[n, :, h], 4)
+            assert len(set(sel[n, h].tolist())) == 4          # distinct tokens
+            for j in range(4):                                # reps are raw rows of K
+                assert np.array_equal(reps[h, n, j], kb[n, sel[n, h, j], h])
+
+
+# -------------------------------------------------- runtime state machine --
+
+def test_oracle_recent_window_follows_reference_buffer_ops():
+    """Decode shift-left + append keeps the last R tokens (m12_runtime.py:1164-1172)."""
+    cfg = O.OracleConfig(recent_tokens=128, sink_tokens=64, top_k_blocks=2)
+    ob = O.M12Oracle(cfg)
+    rng = np.random.default_rng(10)
+    T = 640
+    k = _rand_bf16(rng, (T, 8, 128), 0.1)
+    ob.store_kv(k, k, with_reps=False)
+    ob.reps[:] = _rand_bf16(rng, ob.reps.shape, 0.1)
+    assert np.array_equal(ob.recent_k, k[T - 128:])
+    assert np.array_equal(ob.sink_k, k[:64])
+    news = []
+    for s in range(5):
+        kn = _rand_bf16(rng, (1, 8, 128), 0.1)
+        news.append(kn[0])
+        ob.decode(_rand_bf16(rng, (1, 32, 128)), kn, kn)
+    assert np.array_equal(ob.recent_k, np.concatenate([k[T - 128 + 5:], np.stack(news)]))
+    assert ob.valid_len == T + 5

@@ -111,6 +111,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-layers", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -128,6 +130,15 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(8):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "launches": 8}), flush=True)
+        return
     L, T = args.layers, args.context
     quant = args.kv_format != "bf16"
     cfg = M12Config(max_model_len=T, top_k_blocks=args.top_k, quant_history=quant,
@@ -174,6 +185,11 @@ def main():
 
     nb = model.nblocks_filled
     by = step_bytes(nb, args.top_k, cfg.sink_tokens, cfg.recent_tokens, args.kv_format)
+    traffic = None
+    prof = os.path.join(ROOT, "profiles", "decode32k_bf16_traffic.json")
+    if (args.kv_format, L, T, args.top_k) == ("bf16", 36, 32768, 32) and os.path.exists(prof):
+        with open(prof) as f:
+            traffic = json.load(f)["attend_op_traffic_bytes"]
     us_layer = ms_step * 1e3 / L
     step_gbps = by["total"] * L / (ms_step * 1e-3) / 1e9
     attend_gbps = by["attend"] * L / (attend_us * 1e-6) / 1e9
@@ -203,12 +219,13 @@ def main():
         "attend_splits": model.core._splits(args.top_k + 9, 1) if args.splits is None else args.splits,
         "roofline": {
             "bound": "hbm",
-            "kernel": "attend_kernel (in-place gather + segmented attention, all layers)",
+            "kernel": "attend_kernel + attend_merge_kernel (in-place gather + segmented attention, all layers)",
             "achieved": round(attend_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(attend_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": "profiles/decode32k_bf16_traffic.json (calibrated FETCH_SIZE+WRITE_SIZE)" if traffic else None,
             "bytes_per_launch": by["attend"] * L,
             "avg_launch_us": round(attend_us, 2),
         },

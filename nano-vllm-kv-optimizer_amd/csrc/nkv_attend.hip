@@ -38,6 +38,9 @@
 namespace nkv {
 namespace {
 
+#ifndef NKV_ATTEND_DECODE_WAVES
+#define NKV_ATTEND_DECODE_WAVES 2  // waves per SIMD the bf16 decode variant is built for (3 spills and measured slower)
+#endif
 constexpr int kAttendWaves = 4;
 constexpr int kAttendThreads = kAttendWaves * kWave;
 constexpr int kPRow = 20;        // floats per key row of the p tile in LDS (16 rows + pad)
@@ -187,7 +190,7 @@ constexpr int attend_lds_floats() {
 }
 
 template <int FMT, int M>
-__global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendParams p) {
+__global__ __launch_bounds__(kAttendThreads, (FMT == NKV_KV_BF16 && M == 4) ? NKV_ATTEND_DECODE_WAVES : 1) void attend_kernel(const AttendParams p) {
   __shared__ __attribute__((aligned(16))) float s_lds[attend_lds_floats<M>()];
   __shared__ float s_alpha[kAttendWaves][kMaxRows];
 
@@ -299,7 +302,10 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(const AttendPara
     }
 
     // ---- V loads go out now and overlap the softmax below -----------------
-    // lane (lg, ln) loads dims [8 ln, +8) of key 4 j + lg.
+    // lane (lg, ln) loads dims [8 ln, +8) of key 4 j + lg.  The scheduling
+    // barrier keeps them after the MFMAs so K and V registers are not live
+    // together (occupancy).
+    __builtin_amdgcn_sched_barrier(0);
     uint4 va[16];
     if (int8_seg) {
 #pragma unroll

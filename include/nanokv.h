@@ -162,6 +162,31 @@ int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads, int num_he
                                     int tq, int splits);
 
 /*
+ * Segmented causal GQA attention for a chunk of many queries, on the matrix
+ * cores (bf16 MFMA for Q.K^T and P.V, fp32 softmax and accumulation).
+ *
+ * Replaces the attention of M12LayerRuntime.prefill_chunk: the pack of
+ * [selected | sink | previous recent | chunk] (m12_runtime.py:560-636) and
+ * _prefill_attention's bottom-right causal flash attention over it
+ * (:809-839; same function as the masked _fused_attention path :875-896).
+ * int8 history blocks are dequantised to bf16(code * scale) as the
+ * reference's pack does (m12_runtime.py:1262-1267, fused_dequant.py:34-44).
+ *
+ * Same key set and argument meaning as nkv_attend with n_chunk = tq (query t
+ * is chunk token t and sees chunk tokens c <= t), write_slot = -1 and
+ * splits = 1.  Queries are tiled 128/G tokens x G heads per workgroup
+ * (G = Hq / Hkv must divide 128).  No workspace.
+ * Constraints: 1 <= tq <= 65536, n_hist <= 4096.
+ */
+int nkv_prefill_attend(const nkv_store* st, int layer0, int num_layers,
+                       const uint16_t* q, int64_t q_layer_stride, int tq,
+                       const uint16_t* k_new, const uint16_t* v_new, int64_t kv_layer_stride,
+                       const int32_t* ids, int64_t ids_layer_stride, int n_hist,
+                       const uint8_t* allowed, int sink_len,
+                       int ring_base, int rec_lo, int rec_len,
+                       float scale, uint16_t* out, void* stream);
+
+/*
  * Append one prefill chunk to the history of `num_layers` layers.
  *
  * Replaces the history / quantisation / sink part of M12LayerRuntime._store_kv

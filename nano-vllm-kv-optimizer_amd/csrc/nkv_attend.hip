@@ -33,152 +33,11 @@
 // Same result as the reference's gather + pack + fp32 einsum attention
 // (nanovllm/sparse/m12_runtime.py:1212-1320 and :845-896) up to fp32
 // summation order.
-#include "nkv_common.h"
+#include "nkv_attend_common.h"
 
 namespace nkv {
 namespace {
-
-#ifndef NKV_ATTEND_DECODE_WAVES
-#define NKV_ATTEND_DECODE_WAVES 2  // waves per SIMD the bf16 decode variant is built for (3 spills and measured slower)
-#endif
-constexpr int kAttendWaves = 4;
-constexpr int kAttendThreads = kAttendWaves * kWave;
-constexpr int kPRow = 20;        // floats per key row of the p tile in LDS (16 rows + pad)
-constexpr int kPartStride = 130; // floats per partial row: m, l, acc[128]
-constexpr int kMaxRows = 16;     // MFMA N: query rows per group
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-enum SegType { kSegHist = 0, kSegSink = 1, kSegRecent = 2, kSegChunk = 3 };
-
-struct AttendParams {
-  const void* hist_k;
-  const void* hist_v;
-  int64_t hist_ls;
-  const uint16_t* sink_k;
-  const uint16_t* sink_v;
-  int64_t sink_ls;
-  uint16_t* rec_k;
-  uint16_t* rec_v;
-  int64_t rec_ls;
-  const float* k_scale;     // [L][Hkv][D]
-  const float* v_scale;     // [L][Hkv][cap]
-  const uint16_t* k_tscale; // [L][Hkv][cap*64]
-  const uint16_t* v_tscale;
-  const uint16_t* q;
-  int64_t q_ls;
-  const uint16_t* k_new;
-  const uint16_t* v_new;
-  int64_t kv_ls;
-  const int32_t* ids;
-  int64_t ids_ls;
-  const uint8_t* allowed;
-  float* partial;
-  uint16_t* out;
-  int hkv, G, cap, S, R;
-  int tq, qpg, nqg;
-  int n_chunk, write_slot;
-  int n_hist, sink_len, ring_base, rec_lo, rec_len;
-  int n_sink_seg, n_rec_seg, nseg;
-  int splits;
-  float scale_log2;
-};
-
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
-
-__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
-
-// 8 signed bytes -> 8 bf16 (exact: |x| <= 127 has <= 7 significant bits).
-__device__ __forceinline__ uint4 i8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t src = ((i < 2) ? lo : hi) >> ((i & 1) * 16);
-    const float f0 = static_cast<float>(static_cast<int8_t>(src & 0xffu));
-    const float f1 = static_cast<float>(static_cast<int8_t>((src >> 8) & 0xffu));
-    o[i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
-  }
-  return make_uint4(o[0], o[1], o[2], o[3]);
-}
-
-// A segment: `len` rows starting at kbase / vbase, row stride `rowb` bytes;
-// rows >= len are never loaded (indices are clamped).  `vlen` = rows that may
-// be valid (a history block with an out-of-range id has vlen 0).
-struct Seg {
-  int type;
-  int len;
-  int vlen;
-  int off;   // sink / chunk: first token; recent: first physical slot
-  int blk;   // history block id
-  int u;     // history segment index (column of `allowed`)
-  int rowb;
-  const char* kbase;
-  const char* vbase;
-};
-
-template <int FMT>
-__device__ __forceinline__ Seg make_seg(const AttendParams& p, int layer, int h, int s) {
-  Seg g;
-  g.blk = 0;
-  g.u = 0;
-  g.off = 0;
-  if (s < p.n_hist) {
-    constexpr int64_t elem = (FMT == NKV_KV_BF16) ? 2 : 1;
-    g.type = kSegHist;
-    g.len = kBlock;
-    g.vlen = kBlock;
-    g.u = s;
-    int blk = p.ids[static_cast<int64_t>(layer) * p.ids_ls + s];
-    if (blk < 0 || blk >= p.cap) {  // never read outside the history
-      blk = 0;
-      g.vlen = 0;
-    }
-    g.blk = blk;
-    const int64_t off = (p.hist_ls * layer + (static_cast<int64_t>(h) * p.cap + blk) * kBlock * kHeadDim) * elem;
-    g.kbase = static_cast<const char*>(p.hist_k) + off;
-    g.vbase = static_cast<const char*>(p.hist_v) + off;
-    g.rowb = kHeadDim * static_cast<int>(elem);
-    return g;
-  }
-  s -= p.n_hist;
-  g.rowb = kHeadDim * 2;
-  if (s < p.n_sink_seg) {
-    g.type = kSegSink;
-    g.off = s * kBlock;
-    g.len = min(kBlock, p.sink_len - g.off);
-    g.vlen = g.len;
-    const int64_t off = p.sink_ls * layer + (static_cast<int64_t>(h) * p.S + g.off) * kHeadDim;
-    g.kbase = reinterpret_cast<const char*>(p.sink_k + off);
-    g.vbase = reinterpret_cast<const char*>(p.sink_v + off);
-    return g;
-  }
-  s -= p.n_sink_seg;
-  if (s < p.n_rec_seg) {
-    g.type = kSegRecent;
-    g.off = s * kBlock;
-    g.len = min(kBlock, p.R - g.off);
-    g.vlen = g.len;
-    const int64_t off = p.rec_ls * layer + (static_cast<int64_t>(h) * p.R + g.off) * kHeadDim;
-    g.kbase = reinterpret_cast<const char*>(p.rec_k + off);
-    g.vbase = reinterpret_cast<const char*>(p.rec_v + off);
-    return g;
-  }
-  s -= p.n_rec_seg;
-  g.type = kSegChunk;
-  g.off = s * kBlock;
-  g.len = min(kBlock, p.n_chunk - g.off);
-  g.vlen = g.len;
-  g.rowb = p.hkv * kHeadDim * 2;
-  const int64_t off = p.kv_ls * layer + (static_cast<int64_t>(g.off) * p.hkv + h) * kHeadDim;
-  g.kbase = reinterpret_cast<const char*>(p.k_new + off);
-  g.vbase = reinterpret_cast<const char*>(p.v_new + off);
-  return g;
-}
+using namespace attend_detail;
 
 // LDS floats of one workgroup: the per-wave p tiles during the segment loop,
 // reused afterwards for the cross-wave merge (m, l and acc of every wave).
@@ -534,47 +393,49 @@ extern "C" int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads,
   return static_cast<int64_t>(num_layers) * num_kv_heads * nqg * splits * kMaxRows * kPartStride;
 }
 
-extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
-                          int64_t q_layer_stride, int tq, const uint16_t* k_new,
-                          const uint16_t* v_new, int64_t kv_layer_stride, int n_chunk,
-                          int write_slot, const int32_t* ids, int64_t ids_layer_stride,
-                          int n_hist, const uint8_t* allowed, int sink_len, int ring_base,
-                          int rec_lo, int rec_len, float scale, int splits, float* partial_ws,
-                          uint16_t* out, void* stream) {
+namespace nkv {
+
+int fill_attend_params(const char* who, const nkv_store* st, int layer0, int num_layers,
+                       const uint16_t* q, int64_t q_layer_stride, int tq, const uint16_t* k_new,
+                       const uint16_t* v_new, int64_t kv_layer_stride, int n_chunk, int write_slot,
+                       const int32_t* ids, int64_t ids_layer_stride, int n_hist,
+                       const uint8_t* allowed, int sink_len, int ring_base, int rec_lo, int rec_len,
+                       float scale, int splits, float* partial_ws, uint16_t* out,
+                       AttendParams* pp) {
   int rc = check_store(st, layer0, num_layers);
   if (rc != NKV_OK) return rc;
   const int G = st->num_heads / st->num_kv_heads;
   const int R = st->recent_tokens;
-  NKV_CHECK_ARG(q != nullptr && out != nullptr, "nkv_attend: q and out must be non-NULL");
-  NKV_CHECK_ARG(tq >= 1 && tq <= 65536, "nkv_attend: tq must be in [1, 65536] (got %d)", tq);
-  NKV_CHECK_ARG(n_hist >= 0 && n_hist <= 4096, "nkv_attend: n_hist must be in [0, 4096] (got %d)", n_hist);
-  NKV_CHECK_ARG(n_hist == 0 || ids != nullptr, "nkv_attend: ids is NULL but n_hist=%d", n_hist);
-  NKV_CHECK_ARG(sink_len >= 0 && sink_len <= st->sink_tokens, "nkv_attend: sink_len %d outside [0, %d]",
-                sink_len, st->sink_tokens);
+  NKV_CHECK_ARG(q != nullptr && out != nullptr, "%s: q and out must be non-NULL", who);
+  NKV_CHECK_ARG(tq >= 1 && tq <= 65536, "%s: tq must be in [1, 65536] (got %d)", who, tq);
+  NKV_CHECK_ARG(n_hist >= 0 && n_hist <= 4096, "%s: n_hist must be in [0, 4096] (got %d)", who, n_hist);
+  NKV_CHECK_ARG(n_hist == 0 || ids != nullptr, "%s: ids is NULL but n_hist=%d", who, n_hist);
+  NKV_CHECK_ARG(sink_len >= 0 && sink_len <= st->sink_tokens, "%s: sink_len %d outside [0, %d]",
+                who, sink_len, st->sink_tokens);
   NKV_CHECK_ARG(rec_len >= 0 && rec_lo >= 0 && rec_lo + rec_len <= R,
-                "nkv_attend: recent range [%d, %d) outside [0, %d)", rec_lo, rec_lo + rec_len, R);
-  NKV_CHECK_ARG(ring_base >= 0 && ring_base < R, "nkv_attend: ring_base %d outside [0, %d)", ring_base, R);
+                "%s: recent range [%d, %d) outside [0, %d)", who, rec_lo, rec_lo + rec_len, R);
+  NKV_CHECK_ARG(ring_base >= 0 && ring_base < R, "%s: ring_base %d outside [0, %d)", who, ring_base, R);
   NKV_CHECK_ARG(n_chunk == 0 || n_chunk == tq,
-                "nkv_attend: the causal chunk must have one token per query (n_chunk=%d, tq=%d)", n_chunk, tq);
+                "%s: the causal chunk must have one token per query (n_chunk=%d, tq=%d)", who, n_chunk, tq);
   NKV_CHECK_ARG(n_chunk == 0 || (k_new != nullptr && v_new != nullptr),
-                "nkv_attend: k_new/v_new are NULL but n_chunk=%d", n_chunk);
-  NKV_CHECK_ARG(write_slot < R, "nkv_attend: write_slot %d outside the ring", write_slot);
-  NKV_CHECK_ARG(write_slot < 0 || n_chunk >= 1, "nkv_attend: write_slot needs a new token (n_chunk >= 1)");
+                "%s: k_new/v_new are NULL but n_chunk=%d", who, n_chunk);
+  NKV_CHECK_ARG(write_slot < R, "%s: write_slot %d outside the ring", who, write_slot);
+  NKV_CHECK_ARG(write_slot < 0 || n_chunk >= 1, "%s: write_slot needs a new token (n_chunk >= 1)", who);
   if (write_slot >= 0 && rec_len > 0) {
     // the slot being written must not be one the call reads
     const int lp = ((write_slot - ring_base) % R + R) % R;
     NKV_CHECK_ARG(lp < rec_lo || lp >= rec_lo + rec_len,
-                  "nkv_attend: write_slot %d lies inside the attended recent window", write_slot);
+                  "%s: write_slot %d lies inside the attended recent window", who, write_slot);
   }
-  NKV_CHECK_ARG(splits >= 1 && splits <= 64, "nkv_attend: splits must be in [1, 64] (got %d)", splits);
-  NKV_CHECK_ARG(splits == 1 || partial_ws != nullptr, "nkv_attend: splits > 1 needs partial_ws");
+  NKV_CHECK_ARG(splits >= 1 && splits <= 64, "%s: splits must be in [1, 64] (got %d)", who, splits);
+  NKV_CHECK_ARG(splits == 1 || partial_ws != nullptr, "%s: splits > 1 needs partial_ws", who);
   const int n_sink_seg = (sink_len + kBlock - 1) / kBlock;
   const int n_rec_seg = rec_len > 0 ? (R + kBlock - 1) / kBlock : 0;
   const int n_chunk_seg = (n_chunk + kBlock - 1) / kBlock;
   const int nseg = n_hist + n_sink_seg + n_rec_seg + n_chunk_seg;
-  NKV_CHECK_ARG(nseg >= 1, "nkv_attend: nothing to attend");
+  NKV_CHECK_ARG(nseg >= 1, "%s: nothing to attend", who);
 
-  AttendParams p;
+  AttendParams& p = *pp;
   const int64_t hist_ls = static_cast<int64_t>(st->num_kv_heads) * st->cap_blocks * kBlock * kHeadDim;
   const int64_t elem = st->kv_format == NKV_KV_BF16 ? 2 : 1;
   p.hist_k = static_cast<const char*>(st->hist_k) + layer0 * hist_ls * elem;
@@ -607,10 +468,8 @@ extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const
   p.S = st->sink_tokens;
   p.R = R;
   p.tq = tq;
-  int qpg, M;
-  group_shape(tq, G, &qpg, &M);
-  p.qpg = qpg;
-  p.nqg = (tq + qpg - 1) / qpg;
+  p.qpg = 1;
+  p.nqg = tq;
   p.n_chunk = n_chunk;
   p.write_slot = write_slot;
   p.n_hist = n_hist;
@@ -623,6 +482,28 @@ extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const
   p.nseg = nseg;
   p.splits = splits;
   p.scale_log2 = scale * 1.4426950408889634f;
+  return NKV_OK;
+}
+
+}  // namespace nkv
+
+extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
+                          int64_t q_layer_stride, int tq, const uint16_t* k_new,
+                          const uint16_t* v_new, int64_t kv_layer_stride, int n_chunk,
+                          int write_slot, const int32_t* ids, int64_t ids_layer_stride,
+                          int n_hist, const uint8_t* allowed, int sink_len, int ring_base,
+                          int rec_lo, int rec_len, float scale, int splits, float* partial_ws,
+                          uint16_t* out, void* stream) {
+  AttendParams p;
+  const int rc = fill_attend_params("nkv_attend", st, layer0, num_layers, q, q_layer_stride, tq, k_new,
+                                    v_new, kv_layer_stride, n_chunk, write_slot, ids, ids_layer_stride,
+                                    n_hist, allowed, sink_len, ring_base, rec_lo, rec_len, scale, splits,
+                                    partial_ws, out, &p);
+  if (rc != NKV_OK) return rc;
+  int qpg, M;
+  group_shape(tq, p.G, &qpg, &M);
+  p.qpg = qpg;
+  p.nqg = (tq + qpg - 1) / qpg;
 
   dim3 grid(splits, st->num_kv_heads, num_layers * p.nqg);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -635,6 +516,6 @@ extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const
   }
   NKV_CHECK_SUPPORTED(bad == 0, "nkv_attend: unsupported row count %d", M);
   if (splits > 1)
-    hipLaunchKernelGGL(attend_merge_kernel, dim3(st->num_kv_heads, num_layers * p.nqg, qpg * G), dim3(kHeadDim), 0, s, p);
+    hipLaunchKernelGGL(attend_merge_kernel, dim3(st->num_kv_heads, num_layers * p.nqg, qpg * p.G), dim3(kHeadDim), 0, s, p);
   return launch_status("nkv_attend");
 }

@@ -1,0 +1,167 @@
+// Segment machinery shared by the few-query attention kernel (nkv_attend.hip)
+// and the many-query prefill kernel (nkv_prefill.hip): the launch parameters
+// and the description of one attended segment (history block, sink piece,
+// physical ring piece or chunk piece).
+#pragma once
+
+#include "nkv_common.h"
+
+namespace nkv {
+namespace attend_detail {
+
+#ifndef NKV_ATTEND_DECODE_WAVES
+#define NKV_ATTEND_DECODE_WAVES 2  // waves per SIMD the bf16 decode variant is built for (3 spills and measured slower)
+#endif
+constexpr int kAttendWaves = 4;
+constexpr int kAttendThreads = kAttendWaves * kWave;
+constexpr int kPRow = 20;        // floats per key row of the p tile in LDS (16 rows + pad)
+constexpr int kPartStride = 130; // floats per partial row: m, l, acc[128]
+constexpr int kMaxRows = 16;     // MFMA N: query rows per group
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+enum SegType { kSegHist = 0, kSegSink = 1, kSegRecent = 2, kSegChunk = 3 };
+
+struct AttendParams {
+  const void* hist_k;
+  const void* hist_v;
+  int64_t hist_ls;
+  const uint16_t* sink_k;
+  const uint16_t* sink_v;
+  int64_t sink_ls;
+  uint16_t* rec_k;
+  uint16_t* rec_v;
+  int64_t rec_ls;
+  const float* k_scale;     // [L][Hkv][D]
+  const float* v_scale;     // [L][Hkv][cap]
+  const uint16_t* k_tscale; // [L][Hkv][cap*64]
+  const uint16_t* v_tscale;
+  const uint16_t* q;
+  int64_t q_ls;
+  const uint16_t* k_new;
+  const uint16_t* v_new;
+  int64_t kv_ls;
+  const int32_t* ids;
+  int64_t ids_ls;
+  const uint8_t* allowed;
+  float* partial;
+  uint16_t* out;
+  int hkv, G, cap, S, R;
+  int tq, qpg, nqg;
+  int n_chunk, write_slot;
+  int n_hist, sink_len, ring_base, rec_lo, rec_len;
+  int n_sink_seg, n_rec_seg, nseg;
+  int splits;
+  float scale_log2;
+};
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// 8 signed bytes -> 8 bf16 (exact: |x| <= 127 has <= 7 significant bits).
+__device__ __forceinline__ uint4 i8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t src = ((i < 2) ? lo : hi) >> ((i & 1) * 16);
+    const float f0 = static_cast<float>(static_cast<int8_t>(src & 0xffu));
+    const float f1 = static_cast<float>(static_cast<int8_t>((src >> 8) & 0xffu));
+    o[i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// A segment: `len` rows starting at kbase / vbase, row stride `rowb` bytes;
+// rows >= len are never loaded (indices are clamped).  `vlen` = rows that may
+// be valid (a history block with an out-of-range id has vlen 0).
+struct Seg {
+  int type;
+  int len;
+  int vlen;
+  int off;   // sink / chunk: first token; recent: first physical slot
+  int blk;   // history block id
+  int u;     // history segment index (column of `allowed`)
+  int rowb;
+  const char* kbase;
+  const char* vbase;
+};
+
+template <int FMT>
+__device__ __forceinline__ Seg make_seg(const AttendParams& p, int layer, int h, int s) {
+  Seg g;
+  g.blk = 0;
+  g.u = 0;
+  g.off = 0;
+  if (s < p.n_hist) {
+    constexpr int64_t elem = (FMT == NKV_KV_BF16) ? 2 : 1;
+    g.type = kSegHist;
+    g.len = kBlock;
+    g.vlen = kBlock;
+    g.u = s;
+    int blk = p.ids[static_cast<int64_t>(layer) * p.ids_ls + s];
+    if (blk < 0 || blk >= p.cap) {  // never read outside the history
+      blk = 0;
+      g.vlen = 0;
+    }
+    g.blk = blk;
+    const int64_t off = (p.hist_ls * layer + (static_cast<int64_t>(h) * p.cap + blk) * kBlock * kHeadDim) * elem;
+    g.kbase = static_cast<const char*>(p.hist_k) + off;
+    g.vbase = static_cast<const char*>(p.hist_v) + off;
+    g.rowb = kHeadDim * static_cast<int>(elem);
+    return g;
+  }
+  s -= p.n_hist;
+  g.rowb = kHeadDim * 2;
+  if (s < p.n_sink_seg) {
+    g.type = kSegSink;
+    g.off = s * kBlock;
+    g.len = min(kBlock, p.sink_len - g.off);
+    g.vlen = g.len;
+    const int64_t off = p.sink_ls * layer + (static_cast<int64_t>(h) * p.S + g.off) * kHeadDim;
+    g.kbase = reinterpret_cast<const char*>(p.sink_k + off);
+    g.vbase = reinterpret_cast<const char*>(p.sink_v + off);
+    return g;
+  }
+  s -= p.n_sink_seg;
+  if (s < p.n_rec_seg) {
+    g.type = kSegRecent;
+    g.off = s * kBlock;
+    g.len = min(kBlock, p.R - g.off);
+    g.vlen = g.len;
+    const int64_t off = p.rec_ls * layer + (static_cast<int64_t>(h) * p.R + g.off) * kHeadDim;
+    g.kbase = reinterpret_cast<const char*>(p.rec_k + off);
+    g.vbase = reinterpret_cast<const char*>(p.rec_v + off);
+    return g;
+  }
+  s -= p.n_rec_seg;
+  g.type = kSegChunk;
+  g.off = s * kBlock;
+  g.len = min(kBlock, p.n_chunk - g.off);
+  g.vlen = g.len;
+  g.rowb = p.hkv * kHeadDim * 2;
+  const int64_t off = p.kv_ls * layer + (static_cast<int64_t>(g.off) * p.hkv + h) * kHeadDim;
+  g.kbase = reinterpret_cast<const char*>(p.k_new + off);
+  g.vbase = reinterpret_cast<const char*>(p.v_new + off);
+  return g;
+}
+
+}  // namespace attend_detail
+
+// Validates the arguments shared by nkv_attend and nkv_prefill_attend and
+// fills the launch parameters (everything except the query grouping, which
+// each kernel chooses).  Returns NKV_OK or an error code with the message set.
+int fill_attend_params(const char* who, const nkv_store* st, int layer0, int num_layers,
+                       const uint16_t* q, int64_t q_layer_stride, int tq, const uint16_t* k_new,
+                       const uint16_t* v_new, int64_t kv_layer_stride, int n_chunk, int write_slot,
+                       const int32_t* ids, int64_t ids_layer_stride, int n_hist,
+                       const uint8_t* allowed, int sink_len, int ring_base, int rec_lo, int rec_len,
+                       float scale, int splits, float* partial_ws, uint16_t* out,
+                       attend_detail::AttendParams* p);
+
+}  // namespace nkv

@@ -91,7 +91,9 @@ class M12Config:
     Extra fields of this build: ``quant_scale_layout`` ("channel_block" = the
     reference's K-per-channel / V-per-block fp32 scales, "token" = per-token
     per-KV-head fp16 scales) and ``attend_splits`` (workgroups per KV head in
-    the attention kernel; None = automatic).  ``use_index_select``,
+    the attention kernel; None = automatic) and ``mfma_chunk_min_tokens``
+    (prefill / verify chunks of at least this many queries use the
+    matrix-core kernel, shorter ones the few-query kernel).  ``use_index_select``,
     ``decode_kv_pipeline`` and ``gather_sort``'s gather-locality purpose
     belong to the host-offload design and do not change the HBM path
     (``gather_sort`` still orders ``last_block_ids`` ascending).
@@ -130,6 +132,7 @@ class M12Config:
     prefill_adapter: object | None = None
     quant_scale_layout: str = "channel_block"
     attend_splits: int | None = None
+    mfma_chunk_min_tokens: int = 32
 
     def __post_init__(self):
         if self.decode_kv_pipeline and not self.use_index_select:
@@ -153,6 +156,8 @@ class M12Config:
             raise ValueError("quant_scale_layout must be 'channel_block' or 'token'")
         if self.attend_splits is not None and not 1 <= self.attend_splits <= 64:
             raise ValueError("attend_splits must be in [1, 64]")
+        if self.mfma_chunk_min_tokens < 1:
+            raise ValueError("mfma_chunk_min_tokens must be >= 1")
 
     @property
     def kv_format(self) -> str:
@@ -364,10 +369,16 @@ class _SparseCore:
         cfg = self.cfg
         sink_len = min(cfg.sink_tokens, self.valid_len)
         _, off, ln = prefill_recent_slice(self.valid_len, cfg.sink_tokens, cfg.recent_tokens)
-        out = self.attend(q.contiguous(), k.contiguous(), v.contiguous(), n_chunk=q.shape[1],
-                          write_slot=-1, ids=ids, ids_stride=ids_stride,
-                          n_hist=n_hist, allowed=allowed, sink_len=sink_len,
-                          ring_base=self.ring_start, rec_lo=off, rec_len=ln)
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        if q.shape[1] >= cfg.mfma_chunk_min_tokens:
+            out = torch.empty_like(q)
+            self.store.prefill_attend(self.layer0, q, k, v, ids, ids_stride, n_hist, allowed,
+                                      sink_len, self.ring_start, off, ln, cfg.scale, out)
+        else:
+            out = self.attend(q, k, v, n_chunk=q.shape[1], write_slot=-1, ids=ids,
+                              ids_stride=ids_stride, n_hist=n_hist, allowed=allowed,
+                              sink_len=sink_len, ring_base=self.ring_start, rec_lo=off,
+                              rec_len=ln)
         return out, sink_len, ln
 
 
@@ -813,6 +824,26 @@ class M12ModelRuntime:
     def prefill(self, k: torch.Tensor, v: torch.Tensor) -> None:
         """Store a prefill chunk for every layer: k, v [L, T, Hkv, D] bf16."""
         self.core.store_kv(k, v)
+
+    def prefill_chunk(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        """A later prefill chunk for every layer (M12LayerRuntime.prefill_chunk per layer).
+
+        q [L, T, Hq, D], k/v [L, T, Hkv, D] -> o [L, T, Hq, D]: query summaries,
+        selection, attention over [selected | sink | previous recent | chunk],
+        then the chunk is stored (m12_runtime.py:528-651).
+        """
+        cfg = self.cfg
+        if self.core.prefill_len <= 0:
+            raise ValueError("prefill_chunk requires prior history")
+        qs = query_summaries(q.contiguous(), cfg.prefill_query_segments)
+        req = cfg.top_k_blocks if cfg.prefill_top_k_blocks is None else cfg.prefill_top_k_blocks
+        order = _lib.NKV_ORDER_ID_ASC if cfg.gather_sort else _lib.NKV_ORDER_SCORE_DESC
+        ids, _, n = self.core.select(qs, req, order=order)
+        out, _, _ = self.core.chunk_attend(q, k, v, ids, ids.shape[-1], n)
+        self.core.store_kv(k, v)
+        self.last_ids_dev = ids
+        self.last_n_selected = n
+        return out
 
     def select(self, q: torch.Tensor, budget: int | None = None):
         """Decode selection for every layer: q [L, 1, Hq, D] -> (ids [L, 1, K], vals, k)."""

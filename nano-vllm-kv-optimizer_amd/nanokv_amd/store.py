@@ -145,6 +145,18 @@ class SparseKVStore:
             _ptr(allowed), sink_len, ring_base, rec_lo, rec_len, float(scale), splits,
             _ptr(partial_ws), _ptr(out), _stream()), "attend")
 
+    def prefill_attend(self, layer0: int, q, k_new, v_new, ids, ids_layer_stride: int,
+                       n_hist: int, allowed, sink_len: int, ring_base: int, rec_lo: int,
+                       rec_len: int, scale: float, out) -> None:
+        """Many-query causal attention on the matrix cores (chunk = the queries' own tokens)."""
+        self._bf16(q, "q")
+        self._bf16(out, "out")
+        nl, tq = q.shape[0], q.shape[1]
+        _lib.check(self.lib.nkv_prefill_attend(
+            self._desc_ref, layer0, nl, _ptr(q), q.stride(0), tq, _ptr(k_new), _ptr(v_new),
+            k_new.stride(0), _ptr(ids), ids_layer_stride, n_hist, _ptr(allowed), sink_len,
+            ring_base, rec_lo, rec_len, float(scale), _ptr(out), _stream()), "prefill_attend")
+
     def attend_workspace_floats(self, nl: int, tq: int, splits: int) -> int:
         return int(self.lib.nkv_attend_workspace_floats(nl, self.num_kv_heads, self.num_heads,
                                                         tq, splits))

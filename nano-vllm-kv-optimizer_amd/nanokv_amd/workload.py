@@ -60,3 +60,13 @@ def decode_inputs(steps: int, seed: int, *, device="cpu", layers: int = 1):
     k = torch.randn(steps, layers, 1, NUM_KV_HEADS, HEAD_DIM, generator=g, device=device) * scale
     v = torch.randn(steps, layers, 1, NUM_KV_HEADS, HEAD_DIM, generator=g, device=device) * scale
     return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+
+
+def prefill_chunk_inputs(num_tokens: int, seed: int, *, device="cpu", layers: int = 1):
+    """A later prefill chunk: q [L, T, Hq, D] ~ N(0,1), k/v [L, T, Hkv, D] ~ N(0,1)/sqrt(D), bf16."""
+    g = _gen(seed + 104729, device)
+    scale = HEAD_DIM ** -0.5
+    q = torch.randn(layers, num_tokens, NUM_HEADS, HEAD_DIM, generator=g, device=device)
+    k = torch.randn(layers, num_tokens, NUM_KV_HEADS, HEAD_DIM, generator=g, device=device) * scale
+    v = torch.randn(layers, num_tokens, NUM_KV_HEADS, HEAD_DIM, generator=g, device=device) * scale
+    return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)

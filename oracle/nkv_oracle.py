@@ -392,6 +392,29 @@ def attention_fp64(q, k, v, scale: float, mask=None) -> np.ndarray:
     return out.reshape(tq, hq, d)
 
 
+def attention_bf16_probs(q, k, v, scale: float, mask=None) -> np.ndarray:
+    """attention_fp64 with the probabilities rounded to bf16 before P.V.
+
+    The numerics class of flash attention with bf16 operands, which the
+    reference's prefill runs (flash_attn_func, m12_runtime.py:834-839): P is
+    fed to the P.V product in bf16, the normaliser sums the unrounded P.
+    Used only to size the tolerance of the matrix-core prefill kernel.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    tq, hq, d = q.shape
+    s_len, hkv, _ = k.shape
+    g = hq // hkv
+    logits = np.einsum("thgd,shd->thgs", q.reshape(tq, hkv, g, d), k) * scale
+    if mask is not None:
+        logits = np.where(np.asarray(mask)[:, None, None, :], -np.inf, logits)
+    p = np.exp(logits - logits.max(axis=-1, keepdims=True))
+    pb = bf16_round(p.astype(F32)).astype(np.float64)
+    out = np.einsum("thgs,shd->thgd", pb, v) / p.sum(axis=-1, keepdims=True)
+    return out.reshape(tq, hq, d)
+
+
 def causal_mask(tq: int, s_len: int, causal_from: int, attn_mask=None) -> np.ndarray:
     """mask[t, s] = (s >= t + causal_from + 1) & (s >= causal_from), OR attn_mask.
 

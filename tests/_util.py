@@ -30,3 +30,11 @@ def assert_close_bf16(out, ref, *, rel=2.0 ** -7, abs_tol=2e-5, bar=2e-3):
         f"{int(bad.sum())} of {bad.size} outputs off by more than rel {rel} + abs {abs_tol}: "
         f"worst {worst:.3e}")
     return worst
+
+
+# The matrix-core (prefill) kernel rounds the softmax probabilities to bf16 for
+# the P.V product, as the reference's flash-attention prefill does.  With few
+# keys and nearly uniform probabilities that rounding alone moves an output by
+# up to ~1.1e-4 (a CPU emulation of bf16 P reproduces the kernel's worst
+# error exactly), so its outputs get this absolute slack; the 2e-3 bar holds.
+PREFILL_TOL = dict(rel=2.0 ** -7, abs_tol=2e-4)

@@ -54,3 +54,31 @@ def test_bad_arguments_are_rejected_before_any_device_work():
         _lib.check(rc, "attend")
     rc = lib.nkv_query_summaries(None, 0, 1, 8, 32, 128, 1, None, 0, None)
     assert rc == _lib.NKV_ERR_ARG
+
+
+def test_prefill_entry_rejects_bad_arguments_without_device_work():
+    lib = _lib.load()
+    st = _lib.NkvStore()
+    st.num_layers, st.num_heads, st.num_kv_heads = 1, 32, 8
+    st.head_dim, st.block_size, st.r, st.cap_blocks = 128, 64, 4, 16
+    st.sink_tokens, st.recent_tokens, st.kv_format = 64, 512, 0
+    dummy = ctypes.c_void_p(16)   # never dereferenced: every call below fails validation
+    st.hist_k = st.hist_v = st.reps = dummy
+    st.sink_k = st.sink_v = st.recent_k = st.recent_v = dummy
+    # q NULL
+    rc = lib.nkv_prefill_attend(ctypes.byref(st), 0, 1, None, 0, 64, dummy, dummy, 0, None, 0, 0,
+                                None, 0, 0, 0, 0, 1.0, dummy, None)
+    assert rc == _lib.NKV_ERR_ARG and b"nkv_prefill_attend" in lib.nkv_last_error()
+    # recent range beyond the ring
+    rc = lib.nkv_prefill_attend(ctypes.byref(st), 0, 1, dummy, 0, 64, dummy, dummy, 0, None, 0, 0,
+                                None, 0, 0, 500, 100, 1.0, dummy, None)
+    assert rc == _lib.NKV_ERR_ARG and b"recent range" in lib.nkv_last_error()
+    # chunk K/V missing
+    rc = lib.nkv_prefill_attend(ctypes.byref(st), 0, 1, dummy, 0, 64, None, None, 0, None, 0, 0,
+                                None, 0, 0, 0, 0, 1.0, dummy, None)
+    assert rc == _lib.NKV_ERR_ARG and b"k_new/v_new" in lib.nkv_last_error()
+    # GQA group size that does not divide the 128-column query tile
+    st.num_heads, st.num_kv_heads = 24, 8
+    rc = lib.nkv_prefill_attend(ctypes.byref(st), 0, 1, dummy, 0, 64, dummy, dummy, 0, None, 0, 0,
+                                None, 0, 0, 0, 0, 1.0, dummy, None)
+    assert rc == _lib.NKV_ERR_UNSUPPORTED

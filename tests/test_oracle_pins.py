@@ -323,3 +323,22 @@ def test_oracle_recent_window_follows_reference_buffer_ops():
         ob.decode(_rand_bf16(rng, (1, 32, 128)), kn, kn)
     assert np.array_equal(ob.recent_k, np.concatenate([k[T - 128 + 5:], np.stack(news)]))
     assert ob.valid_len == T + 5
+
+
+def test_bf16_probability_rounding_sizes_the_prefill_tolerance():
+    """Few keys, near-uniform softmax: bf16 P alone moves outputs past one bf16
+    ulp of the exact result but stays inside the prefill tolerance."""
+    from tests._util import PREFILL_TOL
+    rng = np.random.default_rng(5)
+    T, S = 90, 254
+    q = O.bf16_round(rng.standard_normal((T, 32, 128)).astype(np.float32))
+    k = O.bf16_round((0.09 * rng.standard_normal((S, 8, 128))).astype(np.float32))
+    v = O.bf16_round((0.09 * rng.standard_normal((S, 8, 128))).astype(np.float32))
+    mask = O.causal_mask(T, S, S - T)
+    exact = O.attention_fp64(q, k, v, 128 ** -0.5, mask)
+    approx = O.bf16_round(O.attention_bf16_probs(q, k, v, 128 ** -0.5, mask).astype(np.float32))
+    err = np.abs(approx - exact)
+    assert (err > 2.0 ** -7 * np.abs(exact) + 2e-5).any()          # beyond the few-query bound
+    assert not (err > PREFILL_TOL["rel"] * np.abs(exact) + PREFILL_TOL["abs_tol"]).any()
+    # and with P exact the same comparison is within one bf16 ulp
+    assert np.abs(O.bf16_round(exact.astype(np.float32)) - exact).max() <= 2.0 ** -8 * np.abs(exact).max()

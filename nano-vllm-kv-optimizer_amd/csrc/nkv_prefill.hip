@@ -16,26 +16,28 @@
 // Hkv = 8, keeping that head's keys in one L2) and the longest causal tiles
 // start first.
 //
-// Per 64-key segment:
-//   * the segment is staged through registers into an LDS buffer (double
-//     buffered, one barrier per segment; the next segment's global loads are
-//     in flight while the current one is computed): K as 64 rows x 256 B with
-//     the 16-byte chunk index XOR-swizzled by the row, V transposed to 128
-//     rows (dims) x 64 keys, keys permuted inside a row so that one 16-byte
-//     LDS read returns the 8 keys an MFMA lane needs;
-//   * S^T = K . Q^T: v_mfma_f32_16x16x32_bf16, A = 16 keys x 32 dims from LDS,
-//     B = 32 dims x 16 columns held in registers for the whole kernel;
+// Per 64-key segment (double-buffered LDS, one barrier per segment):
+//   * staging: bf16 rows go global -> LDS directly (buffer_load ... lds, no
+//     registers; bounds-checked descriptors read rows past the segment as
+//     zero, so no index is clamped).  int8 history rows go through registers
+//     and are dequantised to bf16.  The next segment is in flight while the
+//     current one is computed;
+//   * S^T = K . Q^T: v_mfma_f32_16x16x32_bf16, A = 16 keys x 32 dims read from
+//     the K tile, B = 32 dims x 16 columns held in registers all along;
 //   * online softmax in fp32 per column (exp2, scale folded in); each lane's
 //     column is fixed, so the running max and the rescale stay in the lane;
-//   * O^T += V^T . P^T: A = 16 dims x 32 keys from the transposed V tile,
-//     B = the lane's own probabilities rounded to bf16 (the 32-key
-//     contraction index is ordered as the S^T accumulator holds the keys, so
-//     P never leaves the registers).
+//   * O^T += V^T . P^T: A = 16 dims x 32 keys assembled from the key-major V
+//     tile with two transposing LDS reads (ds_read_b64_tr_b16), B = the
+//     lane's own probabilities rounded to bf16 (the 32-key contraction index
+//     is ordered as the S^T accumulator holds the keys, so P never leaves the
+//     registers).
 //
 // The reference runs this as flash-attention over the packed
 // [selected | sink | recent | chunk] keys with bottom-right causal masking
 // (nanovllm/sparse/m12_runtime.py:592-651, :809-839); the fp32 masked path
 // (:875-896) is the same function.
+#include <type_traits>
+
 #include "nkv_attend_common.h"
 
 namespace nkv {
@@ -45,30 +47,29 @@ using namespace attend_detail;
 constexpr int kPfWaves = 4;
 constexpr int kPfThreads = kPfWaves * kWave;     // 256
 constexpr int kPfCols = 128;                     // (token, head) columns per workgroup
-constexpr int kKTileBytes = kBlock * kHeadDim * 2;
-constexpr int kBufBytes = 2 * kKTileBytes;       // K tile + transposed V tile
+constexpr int kTileBytes = kBlock * kHeadDim * 2;
+constexpr int kBufBytes = 2 * kTileBytes;        // K tile + V tile
+constexpr int kRsrcWord3 = 0x00020000;           // raw buffer, 32-bit data format
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-// Byte offset of 16-byte chunk `chunk` (dims 8 chunk .. +8) of key row `row`.
-__device__ __forceinline__ int k_off(int row, int chunk) {
-  return row * 256 + ((chunk ^ (row & 15)) << 4);
-}
-
-// Byte offset of chunk `chunk` (8 permuted keys) of transposed-V row `dim`.
-// Key k sits in chunk 4 (k / 32) + (k % 16) / 4 at element 4 ((k % 32) / 16) + k % 4.
-__device__ __forceinline__ int vt_off(int dim, int chunk) {
-  const int swz = (dim & 7) ^ ((dim >> 2) & 6);
-  return kKTileBytes + dim * 128 + ((chunk ^ swz) << 4);
-}
+// LDS layout of one stage buffer (bytes), both tiles key-major, 256 B a row:
+//   K tile [0, 16384): key r at r * 256, its 16-byte chunk c (dims 8c .. 8c+7)
+//          at chunk position c ^ (r & 15);
+//   V tile [16384, 32768): key k at 16384 + k * 256, chunk c at position
+//          c ^ (2 (k & 3)).
+// The swizzles make the 16-byte K reads (8 lanes, 8 keys) and the 8-byte
+// transposing V reads (16 lanes, 4 keys x 16 dims) free of bank conflicts.
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   const bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
   return __builtin_bit_cast(uint32_t, v);
 }
-
 
 // 8 int8 codes (lo, hi) -> 8 x bf16(code * scale[e]), rounded to nearest even.
 __device__ __forceinline__ u32x4 dequant8(uint32_t lo, uint32_t hi, const float (&sc)[8]) {
@@ -81,96 +82,83 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t lo, uint32_t hi, const float 
   return u32x4{pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]), pack_bf16(f[6], f[7])};
 }
 
-// One segment in flight between its global loads and its LDS store.
-struct Stage {
-  u32x4 k[4];   // K rows kr0 + 16 j, dims 8 kc .. +8 (int8: 8 bytes in .x/.y)
-  u32x4 v[4];   // V keys vkey0 + j, dims 8 vdg .. +8
-  float ks[4];  // int8 per-token scales of those K rows
-  float vs[4];  // int8 per-token scales of those V keys (per-block: vs[0])
-};
-
-// Thread roles in the staging (tid = 0..255):
-//   K: rows (tid >> 4) + 16 j, j < 4, 16-byte chunk tid & 15;
-//   V: keys vkey0 + j, j < 4, dims 8 vdg .. +8, written transposed as 8 rows
-//      of 4 keys; the mapping makes each quarter-wave's 8-byte LDS writes
-//      cover all 32 banks.
-struct VRole {
-  int key0, dg, chunk, half;
-};
-
-__device__ __forceinline__ VRole v_role(int tid) {
-  const int wave = tid >> 6;
-  const int u = tid & 15;
-  const int quarter = (tid >> 4) & 3;
-  const int lg = 2 * (wave & 1) + (u & 1);
-  const int half = (u >> 1) & 1;
-  VRole r;
-  r.dg = (u >> 2) + 4 * quarter;
-  r.chunk = 4 * (wave >> 1) + lg;
-  r.half = half;
-  r.key0 = 32 * (wave >> 1) + 16 * half + 4 * lg;
-  return r;
+// Bounds-checked descriptor of rows [0, len) of a segment: reads past the
+// last row return zero, and every read of a row stays inside it.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t seg_rsrc(const char* base, const Seg& g) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0, g.len * g.rowb, kRsrcWord3);
 }
 
+// bf16 segment -> LDS buffer `buf` without registers.  Wavefront w copies K
+// and V rows 16w .. 16w+15, four rows (1 KiB) per instruction; lane u lands
+// at buf + 16 u, so it fetches the global chunk that the swizzle puts there.
+//   kx[i] = byte offset of that chunk in K row 16w + 4i + (u >> 4); vx likewise for V.
+__device__ __forceinline__ void dma_segment(const Seg& g, char* buf, int wave, int lane, const int (&kx)[4],
+                                            int vx) {
+  const __amdgpu_buffer_rsrc_t rk = seg_rsrc(g.kbase, g);
+  const __amdgpu_buffer_rsrc_t rv = seg_rsrc(g.vbase, g);
+  const int rowo = (16 * wave + (lane >> 4)) * g.rowb;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    char* dst = buf + (16 * wave + 4 * i) * 256;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)dst, 16, rowo + kx[i], 4 * i * g.rowb, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(dst + kTileBytes), 16, rowo + vx, 4 * i * g.rowb, 0, 0);
+  }
+}
+
+// int8 history block staged through registers: thread tid holds rows
+// (tid >> 4) + 16 j, 8 codes (dims 8 (tid & 15) ..) of K and of V.
+struct I8Stage {
+  u32x2 k[4];
+  u32x2 v[4];
+  float ks[4];   // per-token K scales of those rows
+  float vs[4];   // per-token V scales (per-block layout: vs[0])
+};
+
 template <int FMT>
-__device__ __forceinline__ void load_stage(const AttendParams& p, const Seg& g, int lh, int tid,
-                                           const VRole& vr, Stage& st) {
-  const int last = g.len - 1;
-  const int kr0 = tid >> 4;
-  const int kc = tid & 15;
-  if (FMT != NKV_KV_BF16 && g.type == kSegHist) {
-    const int64_t tb = (static_cast<int64_t>(lh) * p.cap + g.blk) * kBlock;
+__device__ __forceinline__ void load_i8(const AttendParams& p, const Seg& g, int lh, int tid, I8Stage& st) {
+  const __amdgpu_buffer_rsrc_t rk = seg_rsrc(g.kbase, g);
+  const __amdgpu_buffer_rsrc_t rv = seg_rsrc(g.vbase, g);
+  const int r0 = tid >> 4;
+  const int vo = r0 * kHeadDim + (tid & 15) * 8;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    st.k[j] = __builtin_amdgcn_raw_buffer_load_b64(rk, vo, j * 16 * kHeadDim, 0);
+    st.v[j] = __builtin_amdgcn_raw_buffer_load_b64(rv, vo, j * 16 * kHeadDim, 0);
+  }
+  const int64_t tb = (static_cast<int64_t>(lh) * p.cap + g.blk) * kBlock + r0;
+  if (FMT == NKV_KV_INT8_TOKEN) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int row = min(kr0 + 16 * j, last);
-      const int key = min(vr.key0 + j, last);
-      const u32x2 x = *reinterpret_cast<const u32x2*>(g.kbase + row * g.rowb + kc * 8);
-      const u32x2 y = *reinterpret_cast<const u32x2*>(g.vbase + key * g.rowb + vr.dg * 8);
-      st.k[j] = u32x4{x[0], x[1], 0u, 0u};
-      st.v[j] = u32x4{y[0], y[1], 0u, 0u};
-      if (FMT == NKV_KV_INT8_TOKEN) {
-        st.ks[j] = f16_bits_to_f32(p.k_tscale[tb + row]);
-        st.vs[j] = f16_bits_to_f32(p.v_tscale[tb + key]);
-      }
+      st.ks[j] = f16_bits_to_f32(p.k_tscale[tb + 16 * j]);
+      st.vs[j] = f16_bits_to_f32(p.v_tscale[tb + 16 * j]);
     }
-    if (FMT == NKV_KV_INT8_CHANNEL) st.vs[0] = p.v_scale[static_cast<int64_t>(lh) * p.cap + g.blk];
   } else {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      st.k[j] = *reinterpret_cast<const u32x4*>(g.kbase + min(kr0 + 16 * j, last) * g.rowb + kc * 16);
-      st.v[j] = *reinterpret_cast<const u32x4*>(g.vbase + min(vr.key0 + j, last) * g.rowb + vr.dg * 16);
-    }
+    st.vs[0] = p.v_scale[static_cast<int64_t>(lh) * p.cap + g.blk];
   }
 }
 
 template <int FMT>
-__device__ __forceinline__ void store_stage(char* buf, Stage& st, bool int8_seg, const float (&kch)[8],
-                                            int tid, const VRole& vr) {
-  const int kr0 = tid >> 4;
-  const int kc = tid & 15;
-  if (FMT != NKV_KV_BF16 && int8_seg) {
+__device__ __forceinline__ void store_i8(const AttendParams& p, char* buf, const I8Stage& st, int lh, int tid) {
+  const int r0 = tid >> 4;
+  const int c = tid & 15;
+  float kch[8];   // per-(head, dim) K scales of dims 8 c .. 8 c + 7 (channel layout)
+  if (FMT == NKV_KV_INT8_CHANNEL) {
+    const float* ks = p.k_scale + static_cast<int64_t>(lh) * kHeadDim + c * 8;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float ksc[8], vsc[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        ksc[e] = FMT == NKV_KV_INT8_CHANNEL ? kch[e] : st.ks[j];
-        vsc[e] = FMT == NKV_KV_INT8_CHANNEL ? st.vs[0] : st.vs[j];
-      }
-      st.k[j] = dequant8(st.k[j][0], st.k[j][1], ksc);
-      st.v[j] = dequant8(st.v[j][0], st.v[j][1], vsc);
-    }
+    for (int e = 0; e < 8; ++e) kch[e] = ks[e];
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(buf + k_off(kr0 + 16 * j, kc)) = st.k[j];
-  // transpose: dim 8 dg + e gets the 4 keys' e-th values
+  for (int j = 0; j < 4; ++j) {
+    const int r = r0 + 16 * j;
+    float ksc[8], vsc[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-    const int wi = e >> 1;
-    const uint32_t lo = __builtin_amdgcn_perm(st.v[1][wi], st.v[0][wi], sel);
-    const uint32_t hi = __builtin_amdgcn_perm(st.v[3][wi], st.v[2][wi], sel);
-    *reinterpret_cast<u32x2*>(buf + vt_off(8 * vr.dg + e, vr.chunk) + vr.half * 8) = u32x2{lo, hi};
+    for (int e = 0; e < 8; ++e) {
+      ksc[e] = FMT == NKV_KV_INT8_CHANNEL ? kch[e] : st.ks[j];
+      vsc[e] = FMT == NKV_KV_INT8_CHANNEL ? st.vs[0] : st.vs[j];
+    }
+    *reinterpret_cast<u32x4*>(buf + r * 256 + ((c ^ r0) << 4)) = dequant8(st.k[j][0], st.k[j][1], ksc);
+    *reinterpret_cast<u32x4*>(buf + kTileBytes + r * 256 + ((c ^ (2 * (r0 & 3))) << 4)) =
+        dequant8(st.v[j][0], st.v[j][1], vsc);
   }
 }
 
@@ -185,9 +173,57 @@ __device__ __forceinline__ bool needs_mask(const AttendParams& p, const Seg& g, 
   }
 }
 
+// +inf when d <= 0 (key visible), -inf when d > 0: min(S, bound) masks S
+// without lane masks (no SGPR pairs).
+__device__ __forceinline__ float vis_bound(int d) {
+  return __int_as_float(0x7F800000 | ((0 - d) & static_cast<int>(0x80000000u)));
+}
+
+// -inf for the (key, column) pairs of S that the segment hides; S[kt][ct][e]
+// holds key 16 kt + 4 lg + e of column ct.  Key k of the segment is visible
+// to column ct iff k <= thr[ct] (history / sink / chunk), or, for a ring
+// piece, iff k < vlen and the slot's logical position lies in the window.
+__device__ __forceinline__ void apply_mask(const AttendParams& p, const Seg& g, int lg, const int (&tcol)[2],
+                                           const int (&allow)[2], f32x4 (&S)[4][2]) {
+  if (g.type == kSegRecent) {
+    // x = (slot - ring_base - rec_lo) mod R for slot off + key
+    int a = (g.off - p.ring_base - p.rec_lo) % p.R;
+    a = a < 0 ? a + p.R : a;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = 16 * kt + 4 * lg + e;
+        int x = a + key;
+        x -= p.R & ((p.R - 1 - x) >> 31);
+        const float bound = vis_bound(max(key - (g.vlen - 1), x - (p.rec_len - 1)));
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) S[kt][ct][e] = fminf(S[kt][ct][e], bound);
+      }
+    return;
+  }
+  int base[2];   // 4 lg - thr[ct]
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct) {
+    int thr = g.vlen - 1;
+    if (g.type == kSegChunk) thr = min(thr, tcol[ct] - g.off);
+    else if (allow[ct] == 0) thr = -1;
+    base[ct] = 4 * lg - thr;
+  }
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) S[kt][ct][e] = fminf(S[kt][ct][e], vis_bound(base[ct] + 16 * kt + e));
+}
+
 template <int FMT>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendParams p, int nqt) {
-  __shared__ __attribute__((aligned(16))) char lds[2 * kBufBytes];
+  // two stage buffers as separate objects, so that the compiler can tell the
+  // buffer being read from the one the asynchronous copies write
+  __shared__ __attribute__((aligned(16))) char lds0[kBufBytes];
+  __shared__ __attribute__((aligned(16))) char lds1[kBufBytes];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -202,16 +238,22 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
   const int t0 = qt * tpw;
   const int t_last = min(t0 + tpw, p.tq) - 1;
   const int hq = p.hkv * p.G;
-  const VRole vr = v_role(tid);
 
-  float kch[8];
+  // ---- loop-invariant LDS offsets (bytes) -----------------------------------
+  int koff[4];   // K read (QK A operand): key 16 kt + ln, chunk 4 ks + lg; kt -> + 4096 kt
 #pragma unroll
-  for (int e = 0; e < 8; ++e) kch[e] = 1.0f;
-  if (FMT == NKV_KV_INT8_CHANNEL) {
-    const float* ks = p.k_scale + static_cast<int64_t>(lh) * kHeadDim + (tid & 15) * 8;
+  for (int ks = 0; ks < 4; ++ks) koff[ks] = ln * 256 + ((((4 * ks + lg) ^ ln) & 15) << 4);
+  // V transposing read (PV A operand): lane ln addresses key 4 lg + (ln >> 2)
+  // (+ 32 k2 + 16 half), dims 16 dt + 4 (ln & 3) .. +4; the swizzled chunk is
+  // 2 (dt ^ (ln >> 2)) + ((ln & 3) >> 1), so dt & 4 -> + 128 and dt & 3 picks vtr[]
+  int vtr[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) kch[e] = ks[e];
-  }
+  for (int q = 0; q < 4; ++q)
+    vtr[q] = kTileBytes + (4 * lg + (ln >> 2)) * 256 + ((2 * (q ^ (ln >> 2)) + ((ln & 3) >> 1)) << 4) + 8 * (ln & 1);
+  int kx[4];     // copy offsets: K row 16w + 4i + (lane >> 4), global chunk (lane & 15) ^ (row & 15)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) kx[i] = ((ln ^ ((4 * i + lg) & 15))) << 4;
+  const int vx = (ln ^ (2 * lg)) << 4;   // V row & 3 == lane >> 4
 
   // ---- query operands: column c = 32 wave + 16 ct + ln --------------------
   bf16x8 bq[2][4];
@@ -243,23 +285,46 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
   const int n_chunk_seg = p.n_chunk > 0 ? t_last / kBlock + 1 : 0;
   const int nseg = p.n_hist + p.n_sink_seg + p.n_rec_seg + n_chunk_seg;
 
-  Stage stg;
-  Seg nxt = make_seg<FMT>(p, layer, h, 0);
-  load_stage<FMT>(p, nxt, lh, tid, vr, stg);
-  store_stage<FMT>(lds, stg, FMT != NKV_KV_BF16 && nxt.type == kSegHist, kch, tid, vr);
-  __syncthreads();
+  // staging of segment s into buffer `buf`; for int8 history the registers
+  // are written to LDS by finish_stage after the current segment's compute
+  I8Stage i8;
+  int allow_nxt[2] = {1, 1};
+  auto begin_stage = [&](const Seg& g, char* buf) {
+    if (FMT != NKV_KV_BF16 && g.type == kSegHist)
+      load_i8<FMT>(p, g, lh, tid, i8);
+    else
+      dma_segment(g, buf, wave, lane, kx, vx);
+    if (g.type == kSegHist && p.allowed != nullptr) {
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+        allow_nxt[ct] = p.allowed[static_cast<int64_t>(min(tcol[ct], p.tq - 1)) * p.n_hist + g.u];
+    }
+  };
+  auto finish_stage = [&](const Seg& g, char* buf) {
+    if (FMT != NKV_KV_BF16 && g.type == kSegHist) store_i8<FMT>(p, buf, i8, lh, tid);
+    __builtin_amdgcn_s_waitcnt(0);   // the asynchronous copies have landed
+    __syncthreads();
+  };
 
-  for (int s = 0; s < nseg; ++s) {
+  Seg nxt = make_seg<FMT>(p, layer, h, 0);
+  begin_stage(nxt, lds0);
+  finish_stage(nxt, lds0);
+
+  // One segment: compute on buffer P while the next segment is staged into
+  // buffer 1 - P.
+  auto step = [&](auto parity, int s) {
+    constexpr int P = decltype(parity)::value;
+    char* buf = P == 0 ? lds0 : lds1;
+    char* other = P == 0 ? lds1 : lds0;
     const Seg cur = nxt;
+    const int allow_cur[2] = {allow_nxt[0], allow_nxt[1]};
     const bool more = s + 1 < nseg;
     if (more) {
       nxt = make_seg<FMT>(p, layer, h, s + 1);
-      load_stage<FMT>(p, nxt, lh, tid, vr, stg);
+      begin_stage(nxt, other);
     }
-    const char* buf = lds + (s & 1) * kBufBytes;
 
     // ---- S^T = K . Q^T -----------------------------------------------------
-    // S[kt][ct][e]: key 16 kt + 4 lg + e, column (ct, ln)
     f32x4 S[4][2];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
@@ -269,38 +334,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(buf + k_off(16 * kt + ln, 4 * ks + lg));
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(buf + kt * 4096 + koff[ks]);
         S[kt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bq[0][ks], S[kt][0], 0, 0, 0);
         S[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bq[1][ks], S[kt][1], 0, 0, 0);
       }
     }
-
-    // ---- visibility ---------------------------------------------------------
-    if (needs_mask(p, cur, t0)) {
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const int t = tcol[ct];
-        bool col_ok = true;
-        if (cur.type == kSegHist && p.allowed != nullptr)
-          col_ok = p.allowed[static_cast<int64_t>(min(t, p.tq - 1)) * p.n_hist + cur.u] != 0;
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int key = 16 * kt + 4 * lg + e;
-            bool ok = col_ok && key < cur.vlen;
-            if (cur.type == kSegRecent) {
-              int lp = cur.off + key - p.ring_base;
-              if (lp < 0) lp += p.R;
-              ok = ok && static_cast<unsigned>(lp - p.rec_lo) < static_cast<unsigned>(p.rec_len);
-            } else if (cur.type == kSegChunk) {
-              ok = ok && cur.off + key <= t;
-            }
-            if (!ok) S[kt][ct][e] = -INFINITY;
-          }
-        }
-      }
-    }
+    if (needs_mask(p, cur, t0)) apply_mask(p, cur, lg, tcol, allow_cur, S);
 
     // ---- online softmax (fp32) ----------------------------------------------
     float alpha[2];
@@ -348,15 +387,24 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
       }
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(buf + vt_off(16 * dt + ln, 4 * k2 + lg));
+        const char* vp = buf + vtr[dt & 3] + (dt >> 2) * 128 + k2 * 8192;
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vp));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vp + 4096));
+        const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         acc[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[0], acc[dt][0], 0, 0, 0);
         acc[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[1], acc[dt][1], 0, 0, 0);
       }
     }
 
-    if (more) store_stage<FMT>(lds + ((s + 1) & 1) * kBufBytes, stg, FMT != NKV_KV_BF16 && nxt.type == kSegHist,
-                               kch, tid, vr);
-    __syncthreads();
+    if (more)
+      finish_stage(nxt, other);
+    else
+      __syncthreads();
+  };
+
+  for (int s = 0; s < nseg; s += 2) {
+    step(std::integral_constant<int, 0>{}, s);
+    if (s + 1 < nseg) step(std::integral_constant<int, 1>{}, s + 1);
   }
 
   // ---- normalise and store: acc[dt][ct][i] = dim 16 dt + 4 lg + i -----------

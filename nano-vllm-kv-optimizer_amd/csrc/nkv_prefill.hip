@@ -105,60 +105,97 @@ __device__ __forceinline__ void dma_segment(const Seg& g, char* buf, int wave, i
   }
 }
 
-// int8 history block staged through registers: thread tid holds rows
-// (tid >> 4) + 16 j, 8 codes (dims 8 (tid & 15) ..) of K and of V.
-struct I8Stage {
-  u32x2 k[4];
-  u32x2 v[4];
-  float ks[4];   // per-token K scales of those rows
-  float vs[4];   // per-token V scales (per-block layout: vs[0])
-};
+// int8 history block: the raw codes (and the scales) are copied into the
+// destination buffer first, then dequantised in place by dequant_i8 once the
+// copies have landed.  Staging layout inside the buffer:
+//   [0, 512)        K scales (per-token fp16 x 64, or per-channel fp32 x 128)
+//   [512, 768)      V per-token fp16 scales x 64
+//   [16384, 24576)  raw K codes, 64 rows x 128 B
+//   [24576, 32768)  raw V codes, 64 rows x 128 B
+constexpr int kI8Scales = 0;
+constexpr int kI8VScales = 512;
+constexpr int kI8RawK = kTileBytes;
+constexpr int kI8RawV = kTileBytes + kBlock * kHeadDim;
 
 template <int FMT>
-__device__ __forceinline__ void load_i8(const AttendParams& p, const Seg& g, int lh, int tid, I8Stage& st) {
+__device__ __forceinline__ void dma_i8_segment(const AttendParams& p, const Seg& g, int lh, char* buf, int wave,
+                                               int lane) {
   const __amdgpu_buffer_rsrc_t rk = seg_rsrc(g.kbase, g);
   const __amdgpu_buffer_rsrc_t rv = seg_rsrc(g.vbase, g);
-  const int r0 = tid >> 4;
-  const int vo = r0 * kHeadDim + (tid & 15) * 8;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    st.k[j] = __builtin_amdgcn_raw_buffer_load_b64(rk, vo, j * 16 * kHeadDim, 0);
-    st.v[j] = __builtin_amdgcn_raw_buffer_load_b64(rv, vo, j * 16 * kHeadDim, 0);
+  for (int i = 0; i < 2; ++i) {
+    const int o = (2 * wave + i) * 1024;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(buf + kI8RawK + o), 16, lane * 16, o, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(buf + kI8RawV + o), 16, lane * 16, o, 0, 0);
   }
-  const int64_t tb = (static_cast<int64_t>(lh) * p.cap + g.blk) * kBlock + r0;
-  if (FMT == NKV_KV_INT8_TOKEN) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      st.ks[j] = f16_bits_to_f32(p.k_tscale[tb + 16 * j]);
-      st.vs[j] = f16_bits_to_f32(p.v_tscale[tb + 16 * j]);
+  if (wave == 0) {
+    if (FMT == NKV_KV_INT8_TOKEN) {
+      // 64 fp16 scales = 128 B per tensor; lanes 32.. read past it (zeros)
+      const int64_t tb = (static_cast<int64_t>(lh) * p.cap + g.blk) * kBlock;
+      const __amdgpu_buffer_rsrc_t sk = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(p.k_tscale + tb), 0, kBlock * 2, kRsrcWord3);
+      const __amdgpu_buffer_rsrc_t sv = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(p.v_tscale + tb), 0, kBlock * 2, kRsrcWord3);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sk, (lds_void*)(buf + kI8Scales), 4, lane * 4, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sv, (lds_void*)(buf + kI8VScales), 4, lane * 4, 0, 0, 0);
+    } else {
+      // 128 fp32 per-(head, dim) K scales
+      const __amdgpu_buffer_rsrc_t sk = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<float*>(p.k_scale + static_cast<int64_t>(lh) * kHeadDim), 0, kHeadDim * 4, kRsrcWord3);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sk, (lds_void*)(buf + kI8Scales), 4, lane * 4, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sk, (lds_void*)(buf + kI8Scales + 256), 4, lane * 4, 256, 0, 0);
     }
-  } else {
-    st.vs[0] = p.v_scale[static_cast<int64_t>(lh) * p.cap + g.blk];
   }
 }
 
+// In-place dequantisation of a staged int8 block (the copies have landed and
+// are visible): thread tid converts rows (tid >> 4) + 16 j, dims 8 c .. 8 c + 7
+// (c = tid & 15) of K and V to bf16(code * scale) in the K / V tiles.
 template <int FMT>
-__device__ __forceinline__ void store_i8(const AttendParams& p, char* buf, const I8Stage& st, int lh, int tid) {
+__device__ __forceinline__ void dequant_i8(const AttendParams& p, const Seg& g, int lh, char* buf, int tid) {
   const int r0 = tid >> 4;
   const int c = tid & 15;
-  float kch[8];   // per-(head, dim) K scales of dims 8 c .. 8 c + 7 (channel layout)
-  if (FMT == NKV_KV_INT8_CHANNEL) {
-    const float* ks = p.k_scale + static_cast<int64_t>(lh) * kHeadDim + c * 8;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) kch[e] = ks[e];
-  }
+  u32x2 kq[4], vq[4];
+  float ksc[4][8], vsc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = r0 + 16 * j;
-    float ksc[8], vsc[8];
+    kq[j] = *reinterpret_cast<const u32x2*>(buf + kI8RawK + r * kHeadDim + c * 8);
+    vq[j] = *reinterpret_cast<const u32x2*>(buf + kI8RawV + r * kHeadDim + c * 8);
+  }
+  if (FMT == NKV_KV_INT8_TOKEN) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      ksc[e] = FMT == NKV_KV_INT8_CHANNEL ? kch[e] : st.ks[j];
-      vsc[e] = FMT == NKV_KV_INT8_CHANNEL ? st.vs[0] : st.vs[j];
+    for (int j = 0; j < 4; ++j) {
+      const int r = r0 + 16 * j;
+      const float ks = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(buf + kI8Scales + 2 * r));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ksc[j][e] = ks;
+      vsc[j] = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(buf + kI8VScales + 2 * r));
     }
-    *reinterpret_cast<u32x4*>(buf + r * 256 + ((c ^ r0) << 4)) = dequant8(st.k[j][0], st.k[j][1], ksc);
+  } else {
+    const u32x4 s0 = *reinterpret_cast<const u32x4*>(buf + kI8Scales + c * 32);
+    const u32x4 s1 = *reinterpret_cast<const u32x4*>(buf + kI8Scales + c * 32 + 16);
+    const float vs = p.v_scale[static_cast<int64_t>(lh) * p.cap + g.blk];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ksc[j][e] = __uint_as_float(s0[e]);
+        ksc[j][e + 4] = __uint_as_float(s1[e]);
+      }
+      vsc[j] = vs;
+    }
+  }
+  __syncthreads();   // every raw code and scale has been read
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = r0 + 16 * j;
+    float vv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vv[e] = vsc[j];
+    *reinterpret_cast<u32x4*>(buf + r * 256 + ((c ^ r0) << 4)) = dequant8(kq[j][0], kq[j][1], ksc[j]);
     *reinterpret_cast<u32x4*>(buf + kTileBytes + r * 256 + ((c ^ (2 * (r0 & 3))) << 4)) =
-        dequant8(st.v[j][0], st.v[j][1], vsc);
+        dequant8(vq[j][0], vq[j][1], vv);
   }
 }
 
@@ -285,13 +322,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
   const int n_chunk_seg = p.n_chunk > 0 ? t_last / kBlock + 1 : 0;
   const int nseg = p.n_hist + p.n_sink_seg + p.n_rec_seg + n_chunk_seg;
 
-  // staging of segment s into buffer `buf`; for int8 history the registers
-  // are written to LDS by finish_stage after the current segment's compute
-  I8Stage i8;
+  // staging of segment s into buffer `buf`: asynchronous copies issued by
+  // begin_stage, completed (and int8 blocks dequantised) by finish_stage
   int allow_nxt[2] = {1, 1};
   auto begin_stage = [&](const Seg& g, char* buf) {
     if (FMT != NKV_KV_BF16 && g.type == kSegHist)
-      load_i8<FMT>(p, g, lh, tid, i8);
+      dma_i8_segment<FMT>(p, g, lh, buf, wave, lane);
     else
       dma_segment(g, buf, wave, lane, kx, vx);
     if (g.type == kSegHist && p.allowed != nullptr) {
@@ -301,9 +337,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
     }
   };
   auto finish_stage = [&](const Seg& g, char* buf) {
-    if (FMT != NKV_KV_BF16 && g.type == kSegHist) store_i8<FMT>(p, buf, i8, lh, tid);
     __builtin_amdgcn_s_waitcnt(0);   // the asynchronous copies have landed
     __syncthreads();
+    if (FMT != NKV_KV_BF16 && g.type == kSegHist) {
+      dequant_i8<FMT>(p, g, lh, buf, tid);
+      __syncthreads();
+    }
   };
 
   Seg nxt = make_seg<FMT>(p, layer, h, 0);

@@ -34,9 +34,15 @@ CFLAGS = [
 ]
 
 
+# Per-source additions.  The prefill kernel's max / min over MFMA results need
+# no signalling-NaN quieting (NaN inputs still reach the output through exp2
+# and the P.V product), which saves a canonicalisation per logit.
+EXTRA_FLAGS = {"nkv_prefill.hip": ["-fno-honor-nans"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *CFLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stdout}\n{res.stderr}")

@@ -391,7 +391,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
         for (int e = 0; e < 4; ++e) mx = fmaxf(mx, S[kt][ct][e]);
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run[ct], mx * p.scale_log2);
+      // the reference max only moves when a logit exceeds it by more than
+      // 2^8 (p <= 256 is harmless in fp32 and bf16), so the accumulator
+      // rescale below is rare
+      const float cand = mx * p.scale_log2;
+      const float m_new = cand > m_run[ct] + 8.0f ? cand : m_run[ct];
       const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
       alpha[ct] = __builtin_amdgcn_exp2f(m_run[ct] - m_use);
       m_run[ct] = m_new;

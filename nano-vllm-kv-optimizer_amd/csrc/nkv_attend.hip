@@ -33,6 +33,8 @@
 // Same result as the reference's gather + pack + fp32 einsum attention
 // (nanovllm/sparse/m12_runtime.py:1212-1320 and :845-896) up to fp32
 // summation order.
+#include <stdlib.h>
+
 #include "nkv_attend_common.h"
 
 namespace nkv {
@@ -370,6 +372,15 @@ int launch_fmt(int M, dim3 grid, hipStream_t s, const AttendParams& p) {
   }
 }
 
+// NANOKV_ATTEND_STREAM=0 keeps every call on the per-group kernel (A/B runs).
+bool stream_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("NANOKV_ATTEND_STREAM");
+    return !(e != nullptr && e[0] == '0');
+  }();
+  return on;
+}
+
 // Query rows per group and the template row count for a given (tq, G).
 void group_shape(int tq, int G, int* qpg, int* M) {
   int per = kMaxRows / G;          // queries that fit one MFMA tile
@@ -390,7 +401,14 @@ extern "C" int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads,
   int qpg, M;
   group_shape(tq, num_heads / num_kv_heads, &qpg, &M);
   const int64_t nqg = (tq + qpg - 1) / qpg;
-  return static_cast<int64_t>(num_layers) * num_kv_heads * nqg * splits * kMaxRows * kPartStride;
+  const int64_t grouped = static_cast<int64_t>(num_layers) * num_kv_heads * nqg * splits * kMaxRows * kPartStride;
+  // the streaming kernel's partial records (one per pair and workgroup range)
+  const int64_t rows = static_cast<int64_t>(tq) * (num_heads / num_kv_heads);
+  int64_t streamed = 0;
+  if (rows <= 32)
+    streamed = (static_cast<int64_t>(num_layers) * num_kv_heads + kMaxStreamWorkgroups - 1) *
+               (rows <= 16 ? 16 : 32) * kPartStride;
+  return grouped > streamed ? grouped : streamed;
 }
 
 namespace nkv {
@@ -500,13 +518,20 @@ extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const
                                     n_hist, allowed, sink_len, ring_base, rec_lo, rec_len, scale, splits,
                                     partial_ws, out, &p);
   if (rc != NKV_OK) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // bf16 history without a per-query mask: the streaming kernel (whatever
+  // `splits`; partial_ws is sized for it by nkv_attend_workspace_floats)
+  if (st->kv_format == NKV_KV_BF16 && allowed == nullptr && partial_ws != nullptr && stream_enabled()) {
+    AttendParams ps = p;
+    ps.splits = 1;
+    if (launch_attend_stream(ps, num_layers, s) == 0) return launch_status("nkv_attend");
+  }
   int qpg, M;
   group_shape(tq, p.G, &qpg, &M);
   p.qpg = qpg;
   p.nqg = (tq + qpg - 1) / qpg;
 
   dim3 grid(splits, st->num_kv_heads, num_layers * p.nqg);
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int bad = 0;
   switch (st->kv_format) {
     case NKV_KV_BF16: bad = launch_fmt<NKV_KV_BF16>(M, grid, s, p); break;

@@ -92,8 +92,10 @@ struct Seg {
   const char* vbase;
 };
 
+// Segment s of (layer, KV head h); for a history segment `blk` is its block
+// id (ids[layer][s]).
 template <int FMT>
-__device__ __forceinline__ Seg make_seg(const AttendParams& p, int layer, int h, int s) {
+__device__ __forceinline__ Seg make_seg_blk(const AttendParams& p, int layer, int h, int s, int blk) {
   Seg g;
   g.blk = 0;
   g.u = 0;
@@ -104,7 +106,6 @@ __device__ __forceinline__ Seg make_seg(const AttendParams& p, int layer, int h,
     g.len = kBlock;
     g.vlen = kBlock;
     g.u = s;
-    int blk = p.ids[static_cast<int64_t>(layer) * p.ids_ls + s];
     if (blk < 0 || blk >= p.cap) {  // never read outside the history
       blk = 0;
       g.vlen = 0;
@@ -151,7 +152,23 @@ __device__ __forceinline__ Seg make_seg(const AttendParams& p, int layer, int h,
   return g;
 }
 
+template <int FMT>
+__device__ __forceinline__ Seg make_seg(const AttendParams& p, int layer, int h, int s) {
+  const int blk = s < p.n_hist ? p.ids[static_cast<int64_t>(layer) * p.ids_ls + s] : 0;
+  return make_seg_blk<FMT>(p, layer, h, s, blk);
+}
+
 }  // namespace attend_detail
+
+// Streaming few-query attention (nkv_decode.hip): persistent workgroups over
+// the flat (layer, KV head, segment) tile list.  Launches and returns 0, or
+// returns -1 when the call is outside its cases (the caller then uses the
+// per-group kernel).  Its partial records need
+// (layers x Hkv + stream_workgroups(...) - 1) x 16 ceil(rows / 16) x
+// kPartStride floats of partial_ws.
+constexpr int kMaxStreamWorkgroups = 1024;
+int launch_attend_stream(const attend_detail::AttendParams& p, int num_layers, hipStream_t s);
+int stream_workgroups(int num_layers, int num_kv_heads);
 
 // Validates the arguments shared by nkv_attend and nkv_prefill_attend and
 // fills the launch parameters (everything except the query grouping, which

@@ -38,38 +38,16 @@
 // (:875-896) is the same function.
 #include <type_traits>
 
-#include "nkv_attend_common.h"
+#include "nkv_stage.h"
 
 namespace nkv {
 namespace {
 using namespace attend_detail;
+using namespace stage;
 
 constexpr int kPfWaves = 4;
 constexpr int kPfThreads = kPfWaves * kWave;     // 256
 constexpr int kPfCols = 128;                     // (token, head) columns per workgroup
-constexpr int kTileBytes = kBlock * kHeadDim * 2;
-constexpr int kBufBytes = 2 * kTileBytes;        // K tile + V tile
-constexpr int kRsrcWord3 = 0x00020000;           // raw buffer, 32-bit data format
-
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-
-// LDS layout of one stage buffer (bytes), both tiles key-major, 256 B a row:
-//   K tile [0, 16384): key r at r * 256, its 16-byte chunk c (dims 8c .. 8c+7)
-//          at chunk position c ^ (r & 15);
-//   V tile [16384, 32768): key k at 16384 + k * 256, chunk c at position
-//          c ^ (2 (k & 3)).
-// The swizzles make the 16-byte K reads (8 lanes, 8 keys) and the 8-byte
-// transposing V reads (16 lanes, 4 keys x 16 dims) free of bank conflicts.
-
-__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  const bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
-  return __builtin_bit_cast(uint32_t, v);
-}
 
 // 8 int8 codes (lo, hi) -> 8 x bf16(code * scale[e]), rounded to nearest even.
 __device__ __forceinline__ u32x4 dequant8(uint32_t lo, uint32_t hi, const float (&sc)[8]) {
@@ -80,29 +58,6 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t lo, uint32_t hi, const float 
     f[e] = static_cast<float>(static_cast<int8_t>((w >> ((e & 3) * 8)) & 0xffu)) * sc[e];
   }
   return u32x4{pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]), pack_bf16(f[6], f[7])};
-}
-
-// Bounds-checked descriptor of rows [0, len) of a segment: reads past the
-// last row return zero, and every read of a row stays inside it.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t seg_rsrc(const char* base, const Seg& g) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0, g.len * g.rowb, kRsrcWord3);
-}
-
-// bf16 segment -> LDS buffer `buf` without registers.  Wavefront w copies K
-// and V rows 16w .. 16w+15, four rows (1 KiB) per instruction; lane u lands
-// at buf + 16 u, so it fetches the global chunk that the swizzle puts there.
-//   kx[i] = byte offset of that chunk in K row 16w + 4i + (u >> 4); vx likewise for V.
-__device__ __forceinline__ void dma_segment(const Seg& g, char* buf, int wave, int lane, const int (&kx)[4],
-                                            int vx) {
-  const __amdgpu_buffer_rsrc_t rk = seg_rsrc(g.kbase, g);
-  const __amdgpu_buffer_rsrc_t rv = seg_rsrc(g.vbase, g);
-  const int rowo = (16 * wave + (lane >> 4)) * g.rowb;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    char* dst = buf + (16 * wave + 4 * i) * 256;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)dst, 16, rowo + kx[i], 4 * i * g.rowb, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(dst + kTileBytes), 16, rowo + vx, 4 * i * g.rowb, 0, 0);
-  }
 }
 
 // int8 history block: the raw codes (and the scales) are copied into the
@@ -208,12 +163,6 @@ __device__ __forceinline__ bool needs_mask(const AttendParams& p, const Seg& g, 
     case kSegRecent: return !(p.rec_len == p.R && g.len == kBlock);
     default: return g.len < kBlock || g.off + kBlock - 1 > t0;
   }
-}
-
-// +inf when d <= 0 (key visible), -inf when d > 0: min(S, bound) masks S
-// without lane masks (no SGPR pairs).
-__device__ __forceinline__ float vis_bound(int d) {
-  return __int_as_float(0x7F800000 | ((0 - d) & static_cast<int>(0x80000000u)));
 }
 
 // -inf for the (key, column) pairs of S that the segment hides; S[kt][ct][e]

@@ -150,7 +150,13 @@ def test_decode_int8_token_scales_matches_oracle():
 
 
 def test_model_runtime_batches_layers_like_per_layer_runtimes():
-    """M12ModelRuntime (one launch per stage for all layers) == per-layer runtimes."""
+    """M12ModelRuntime (one launch per stage for all layers) == per-layer runtimes.
+
+    Selection is bit-identical.  The attention is split into workgroup ranges
+    over all (layer, KV head) pairs of a launch, so the fp32 summation order
+    (not the math) depends on how many layers share the launch: outputs agree
+    to one bf16 ulp.
+    """
     from nanokv_amd import workload
     from nanokv_amd.sparse import M12Config, M12LayerRuntime, M12ModelRuntime
     L, T, steps = 3, 4096, 3
@@ -170,4 +176,5 @@ def test_model_runtime_batches_layers_like_per_layer_runtimes():
             o_i = rt.decode(qs[s, i].cuda(), ks[s, i].cuda(), vs[s, i].cuda())
             assert torch.equal(model.last_ids_dev[i, 0, :model.last_n_selected].cpu(),
                                rt.last_block_ids.to(torch.int32))
-            assert torch.equal(out[i].cpu(), o_i.cpu())
+            a, b = out[i].float().cpu(), o_i.float().cpu()
+            assert ((a - b).abs() <= 2.0 ** -7 * b.abs() + 1e-6).all()   # one bf16 ulp

@@ -407,9 +407,9 @@ extern "C" int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads,
   // the streaming kernel's partial records (one per pair and workgroup range)
   const int64_t rows = static_cast<int64_t>(tq) * (num_heads / num_kv_heads);
   int64_t streamed = 0;
-  if (rows <= 32)
-    streamed = (static_cast<int64_t>(num_layers) * num_kv_heads + kMaxStreamWorkgroups - 1) *
-               (rows <= 16 ? 16 : 32) * kPartStride;
+  if (rows <= kMaxRows)
+    streamed = (static_cast<int64_t>(num_layers) * num_kv_heads + 4 * kMaxStreamWorkgroups - 1) * kMaxRows *
+               kPartStride;
   return grouped > streamed ? grouped : streamed;
 }
 

@@ -53,6 +53,55 @@ def step_bytes(nblocks, k, sink, recent, kv_format, hkv=8, d=128, r=4, hq=32, B=
             "total": reps + sel + scales + win + qo, "attend": sel + scales + win + qo}
 
 
+class DeviceEvents:
+    """HIP timing events recorded with a device-scope release.
+
+    torch.cuda.Event records with a system-scope release, which on this
+    runtime leaves the GPU idle for several microseconds per record; a
+    per-step pair of them inflates the step time it brackets.  Events made
+    with hipEventReleaseToDevice only order the device's own work, which is
+    all a kernel timing needs.  The handles live in the same HIP runtime as
+    torch's (one libamdhip64.so.7 per process).
+    """
+
+    _RELEASE_TO_DEVICE = 0x40000000
+
+    def __init__(self, n):
+        import ctypes
+        import torch
+        self._c = ctypes
+        self._hip = ctypes.CDLL("libamdhip64.so.7")
+        self._hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        self._hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self._hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self._hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self._stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        self.ev = []
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            rc = self._hip.hipEventCreateWithFlags(ctypes.byref(e), self._RELEASE_TO_DEVICE)
+            if rc != 0:
+                raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+            self.ev.append(e)
+
+    def record(self, i):
+        rc = self._hip.hipEventRecord(self.ev[i], self._stream)
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+
+    def elapsed_ms(self, i, j):
+        ms = self._c.c_float()
+        rc = self._hip.hipEventElapsedTime(self._c.byref(ms), self.ev[i], self.ev[j])
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return ms.value
+
+    def close(self):
+        for e in self.ev:
+            self._hip.hipEventDestroy(e)
+        self.ev = []
+
+
 def cpu_baseline(model, args, qs, ks, vs, seconds):
     """The reference's host-side op sequence timed on this box's cores (bounded sample)."""
     import torch
@@ -210,6 +259,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-layers", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--step-events", choices=["device", "torch"], default="device",
+                    help="timing events: device-scope release (default) or torch.cuda.Event")
     ap.add_argument("--workload", choices=["decode", "prefill"], default="decode",
                     help="decode (the headline line) or the chunked-prefill attention")
     ap.add_argument("--chunk", type=int, default=4096, help="prefill chunk length")
@@ -263,30 +314,49 @@ def main():
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t0
 
-    nsteps = args.warmup + args.steps
+    nsteps = args.warmup + 2 * args.steps
     qs, ks, vs = workload.decode_inputs(nsteps, args.seed, device=dev, layers=L)
 
     for s in range(args.warmup):
         model.decode(qs[s], ks[s], vs[s])
     torch.cuda.synchronize()
 
-    ev_a = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ev_b = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
+    # Two timed regions over the same workload.  A: K steps bracketed by one
+    # event pair -> the step time and `value`.  B: K more steps with an event
+    # pair around each step's attention launches (attend + merge) -> the
+    # kernel's average launch duration for the roofline.  A record leaves the
+    # GPU idle for a few microseconds, so region B's steps run slower than A's
+    # and its launch durations include part of that idle time (conservative).
+    K = args.steps
+    if args.step_events == "torch":
+        tev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * K + 2)]
+        rec = lambda i: tev[i].record()
+        elapsed = lambda i, j: tev[i].elapsed_time(tev[j])
+    else:
+        dev_ev = DeviceEvents(2 * K + 2)
+        rec = dev_ev.record
+        elapsed = dev_ev.elapsed_ms
     torch.cuda.synchronize()
-    start.record()
-    for i in range(args.steps):
+    host_t0 = time.perf_counter()
+    rec(2 * K)
+    for i in range(K):
         s = args.warmup + i
-        ids, _, n = model.select(qs[s])
-        ev_a[i].record()
-        model.core.decode_attend(qs[s], ks[s], vs[s], ids, ids.shape[-1], n)
-        ev_b[i].record()
-    stop.record()
+        model.decode(qs[s], ks[s], vs[s])
+    rec(2 * K + 1)
+    host_us = (time.perf_counter() - host_t0) / K * 1e6  # launch-side time per step
     torch.cuda.synchronize()
-    ms_total = start.elapsed_time(stop)
-    ms_step = ms_total / args.steps
-    attend_us = sum(a.elapsed_time(b) for a, b in zip(ev_a, ev_b)) / args.steps * 1e3
+    ms_step = elapsed(2 * K, 2 * K + 1) / K
+
+    for i in range(K):
+        s = args.warmup + K + i
+        ids, _, n = model.select(qs[s])
+        rec(2 * i)
+        model.core.decode_attend(qs[s], ks[s], vs[s], ids, ids.shape[-1], n)
+        rec(2 * i + 1)
+    torch.cuda.synchronize()
+    attend_us = sum(elapsed(2 * i, 2 * i + 1) for i in range(K)) / K * 1e3
+    if args.step_events != "torch":
+        dev_ev.close()
 
     nb = model.nblocks_filled
     by = step_bytes(nb, args.top_k, cfg.sink_tokens, cfg.recent_tokens, args.kv_format)
@@ -335,6 +405,7 @@ def main():
             "avg_launch_us": round(attend_us, 2),
         },
         "step_roofline_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
+        "host_launch_us_per_step": round(host_us, 1),
         "setup_s": round(setup_s, 1),
     }
     if not args.no_cpu_baseline:

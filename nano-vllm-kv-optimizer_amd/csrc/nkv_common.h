@@ -42,6 +42,9 @@ int launch_status(const char* what);
 // Validate the fields of a store descriptor that every entry point relies on.
 int check_store(const nkv_store* st, int layer0, int num_layers);
 
+// Compute units of the current device (cached per thread); 0 on error.
+int device_cus();
+
 // ------------------------------------------------------------ bf16 / fp16 --
 __device__ __forceinline__ float bf16_lo(uint32_t packed) {
   return __uint_as_float(packed << 16);

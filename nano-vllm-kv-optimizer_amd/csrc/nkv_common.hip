@@ -51,6 +51,19 @@ int check_store(const nkv_store* st, int layer0, int num_layers) {
   return NKV_OK;
 }
 
+int device_cus() {
+  static thread_local int dev_cached = -1, cus = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev != dev_cached) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus = n;
+    dev_cached = dev;
+  }
+  return cus;
+}
+
 }  // namespace nkv
 
 extern "C" int nkv_abi_version(void) { return NKV_ABI_VERSION; }

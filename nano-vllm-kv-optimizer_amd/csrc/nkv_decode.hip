@@ -357,19 +357,6 @@ __global__ __launch_bounds__(kHeadDim) void attend_stream_merge(const AttendPara
   p.out[p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d] = f32_to_bf16(A / L);
 }
 
-int device_cus() {
-  static thread_local int dev_cached = -1, cus = 0;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  if (dev != dev_cached) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cus = n;
-    dev_cached = dev;
-  }
-  return cus;
-}
-
 template <int M>
 void launch_m(const AttendParams& p, const StreamWork& w, hipStream_t s) {
   hipLaunchKernelGGL(attend_wave_kernel<M>, dim3(w.nwg), dim3(kDcThreads), 0, s, p, w);

@@ -13,8 +13,11 @@
 // r representatives.  It streams that 16 KiB tile with fully coalesced 16-byte
 // loads (lane i reads bytes [1024*c + 16*i, +16)), transposes it through LDS
 // with an XOR swizzle (conflict-free ds_read_b128), and then every lane dots
-// its own row with the G query rows of that head; the query values are
-// wave-uniform, so they are read with scalar loads.  Block maxima across the
+// its own row with the G query rows of that head.  The query rows arrive with
+// one vector load issued beside the tile's and are read back as wave-uniform
+// scalars (v_readlane), so no chain of scalar-cache misses sits between the
+// tile's arrival and the wave's exit.  Every load is unconditional (rows past
+// nblocks are clamped and masked), so the waits count exactly.  Block maxima across the
 // r rows use lane shuffles; the maximum across KV heads is an atomicMax on
 // the order-preserving uint32 key of the score, which kernel 2 consumes and
 // resets to zero.
@@ -27,6 +30,8 @@
 // m12_runtime.py:1004-1014 (protected mask) and :1033 (torch.topk).
 #include "nkv_common.h"
 
+#include <stdlib.h>
+
 namespace nkv {
 namespace {
 
@@ -36,6 +41,9 @@ constexpr int kTopkThreads = 256;
 constexpr int kMaxTopk = 1024;
 constexpr int kMaxSelectBlocks = 12288;  // keys + masks + sort buffer stay under 64 KiB of LDS
 constexpr uint32_t kNegInfKey = 0x007fffffu;  // score_key(-inf)
+// s_waitcnt immediate: vmcnt(0), expcnt and lgkmcnt left at their maxima
+// (vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr int kWaitVmcnt0 = (7 << 4) | (15 << 8);
 
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
@@ -43,22 +51,241 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+// x where keep holds, else zero, without turning the load of x into a
+// conditional (exec-masked) one.
+__device__ __forceinline__ uint4 and_mask(uint4 x, bool keep) {
+  const uint32_t m = keep ? 0xffffffffu : 0u;
+  return make_uint4(x.x & m, x.y & m, x.z & m, x.w & m);
+}
+
+// The G query rows of one (query, KV head) as 16 G chunks of 8 bf16, held in
+// vector registers: lane j of set s holds chunk 64 s + j (row (64 s + j) / 16,
+// dims 8 ((64 s + j) % 16) .. +8).  One vector load fetches them together
+// with the tile; the dot loop reads each chunk back as wave-uniform scalars
+// (v_readlane), so no scalar-cache round trip sits on the critical path.
+template <int G>
+struct QueryChunks {
+  static constexpr int kSets = (16 * G + kWave - 1) / kWave;
+  uint4 r[kSets];
+
+  __device__ __forceinline__ void load(const uint16_t* qL, int hq, int h, int n, int lane) {
+    const uint4* qh = reinterpret_cast<const uint4*>(qL + (static_cast<int64_t>(n) * hq + h * G) * kHeadDim);
+#pragma unroll
+    for (int s = 0; s < kSets; ++s) {
+      const int j = s * kWave + lane;
+      r[s] = and_mask(qh[min(j, 16 * G - 1)], j < 16 * G);
+    }
+  }
+
+  // acc[g] += q[g][8 c + e] * rv[e] for e = 0..7 in ascending order
+  __device__ __forceinline__ void fma_chunk(const uint4& rv, int c, float (&acc)[G]) const {
+    const float rf[8] = {bf16_lo(rv.x), bf16_hi(rv.x), bf16_lo(rv.y), bf16_hi(rv.y),
+                         bf16_lo(rv.z), bf16_hi(rv.z), bf16_lo(rv.w), bf16_hi(rv.w)};
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const uint4& src = r[g >> 2];
+      const int ln = ((g & 3) << 4) + c;
+      const uint32_t q0 = __builtin_amdgcn_readlane(src.x, ln);
+      const uint32_t q1 = __builtin_amdgcn_readlane(src.y, ln);
+      const uint32_t q2 = __builtin_amdgcn_readlane(src.z, ln);
+      const uint32_t q3 = __builtin_amdgcn_readlane(src.w, ln);
+      const float qf[8] = {bf16_lo(q0), bf16_hi(q0), bf16_lo(q1), bf16_hi(q1),
+                           bf16_lo(q2), bf16_hi(q2), bf16_lo(q3), bf16_hi(q3)};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g] = __builtin_fmaf(qf[e], rf[e], acc[g]);
+    }
+  }
+};
+
+// 64-bit sort/selection entry: key in the high word, ~id in the low word, so
+// that a larger entry means a larger score, and on equal scores a lower id.
+__device__ __forceinline__ unsigned long long sel_entry(uint32_t key, int id) {
+  return (static_cast<unsigned long long>(key) << 32) |
+         static_cast<unsigned long long>(0xffffffffu - static_cast<uint32_t>(id));
+}
+
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
+  const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), m);
+  const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), m);
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+
+// Same selection as topk_kernel (identical ids, values and order) for one row
+// of at most 64 J blocks, computed by ONE wavefront with no workgroup barrier
+// (pmask: 2 J words of LDS, sel: LDS for max(k, 64) rounded up to a power of
+// two entries).
+// Lane l holds the keys of blocks 64 j + l (j < J) in registers.  The k-th
+// largest key T is found by a 32-step bitwise search: T is the largest value
+// with count(key >= T) >= k, built from the high bit down, each count being
+// J ballots.  Collection is the same ascending-id ballot pass as topk_kernel;
+// up to 64 selected entries are then sorted by a bitonic network across the
+// lanes (shuffles), larger k by the same network over LDS.
+template <int J, bool kAtomicKeys>
+__device__ __forceinline__ void select_row_wave(
+    uint32_t* __restrict__ sk, int nblocks, const int32_t* __restrict__ prot, int nprot,
+    int k_req, int order, int32_t* __restrict__ ids, float* __restrict__ vals,
+    float* __restrict__ scores, uint32_t* pmask, unsigned long long* sel, int lane) {
+  const int nwords = (nblocks + 31) >> 5;
+
+  for (int w = lane; w < nwords; w += kWave) pmask[w] = 0u;
+  wave_lds_sync();
+  for (int i = lane; i < nprot; i += kWave) {
+    const int p = prot[i];
+    if (p >= 0 && p < nblocks) atomicOr(&pmask[p >> 5], 1u << (p & 31));
+  }
+  wave_lds_sync();
+  uint32_t np = 0;
+  for (int w = lane; w < nwords; w += kWave) np += __popc(pmask[w]);
+  for (int o = 32; o > 0; o >>= 1) np += __shfl_xor(np, o);
+  const int avail = nblocks - static_cast<int>(np);
+  const int k = min(k_req, max(1, avail));
+
+  // keys past nblocks are 0, below every key score_key() produces.  Every
+  // read is issued (past nblocks it re-reads the last key), so one wait
+  // covers them all; the atomic form reads and clears in one atomicAnd, an
+  // all-ones mask leaving the re-read key untouched.
+  uint32_t key[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int i = kWave * j + lane;
+    const bool valid = i < nblocks;
+    uint32_t* kp = sk + (valid ? i : nblocks - 1);
+    key[j] = kAtomicKeys ? atomicAnd(kp, valid ? 0u : 0xffffffffu) : *kp;
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int i = kWave * j + lane;
+    if (i < nblocks) {
+      if (!kAtomicKeys) sk[i] = 0u;  // leave the key buffer zeroed for the next scoring pass
+      if (scores) scores[i] = key_score(key[j]);
+      if ((pmask[i >> 5] >> (i & 31)) & 1u) key[j] = kNegInfKey;
+    } else {
+      key[j] = 0u;
+    }
+  }
+
+  // ---- k-th largest key: largest T with count(key >= T) >= k ------------
+  uint32_t T = 0u;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = T | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) cnt += __popcll(__ballot(key[j] >= cand));
+    if (cnt >= k) T = cand;
+  }
+  int above = 0;
+#pragma unroll
+  for (int j = 0; j < J; ++j) above += __popcll(__ballot(key[j] > T));
+
+  // ---- collect in ascending block order ----------------------------------
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  uint32_t base = 0u;
+  uint32_t need = static_cast<uint32_t>(k - above);
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int i = kWave * j + lane;
+    const bool gt = key[j] > T;
+    const bool eq = key[j] == T && i < nblocks;
+    const unsigned long long meq = __ballot(eq);
+    const uint32_t rank = __popcll(meq & lt);
+    const bool take = gt || (eq && rank < need);
+    const unsigned long long mt = __ballot(take);
+    if (take) sel[base + __popcll(mt & lt)] = sel_entry(key[j], i);
+    base += __popcll(mt);
+    const uint32_t neq = __popcll(meq);
+    need -= (neq < need ? neq : need);
+  }
+  wave_lds_sync();
+
+  if (order == NKV_ORDER_SCORE_DESC && k > 1 && k <= kWave) {
+    // descending bitonic sort of 64 lanes (entries past k are 0 and sink)
+    unsigned long long v = lane < k ? sel[lane] : 0ull;
+    for (int size = 2; size <= kWave; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        const unsigned long long w = shfl_xor_u64(v, stride);
+        const bool lower = (lane & stride) == 0;
+        const bool desc = (lane & size) == 0;
+        // the lower lane of a descending pair keeps the larger entry
+        v = (lower == desc) ? (v > w ? v : w) : (v < w ? v : w);
+      }
+    }
+    if (lane < k) {
+      ids[lane] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(v & 0xffffffffull));
+      if (vals) vals[lane] = key_score(static_cast<uint32_t>(v >> 32));
+    }
+    return;
+  }
+  if (order == NKV_ORDER_SCORE_DESC && k > 1) {
+    int n2 = 1;
+    while (n2 < k) n2 <<= 1;
+    for (int i = k + lane; i < n2; i += kWave) sel[i] = 0ull;
+    wave_lds_sync();
+    for (int size = 2; size <= n2; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int i = lane; i < (n2 >> 1); i += kWave) {
+          const int lo = 2 * i - (i & (stride - 1));
+          const int hi = lo + stride;
+          const bool desc = (lo & size) == 0;
+          const unsigned long long a = sel[lo], b = sel[hi];
+          if (desc ? (a < b) : (a > b)) {
+            sel[lo] = b;
+            sel[hi] = a;
+          }
+        }
+        wave_lds_sync();
+      }
+    }
+  }
+  for (int i = lane; i < k; i += kWave) {
+    const unsigned long long e = sel[i];
+    ids[i] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(e & 0xffffffffull));
+    if (vals) vals[i] = key_score(static_cast<uint32_t>(e >> 32));
+  }
+}
+
+
+// Selection fused into the scoring launch: the last workgroup to finish a
+// layer (a per-layer completion counter) selects that layer's rows, one
+// wavefront per row, while other layers are still being scored.  Used for
+// rows of at most kTailMaxBlocks blocks and k <= kTailMaxK.
+constexpr int kTailMaxBlocks = 8 * kWave;  // 8 key registers: the scorer's occupancy stays
+constexpr int kTailMaxK = 256;
+constexpr int kTailWaveBytes = (kTailMaxBlocks / 32) * 4 + kTailMaxK * 8;  // pmask + sel per wavefront
+
+struct SelectTail {
+  uint32_t* counters;  // [num_layers], zero between launches; NULL: no fused selection
+  const int32_t* prot;
+  int nprot, k_req, order, nqo;
+  int32_t* out_ids;    // [layers][nqo][k_req]
+  float* out_vals;     // same shape or NULL
+  float* out_scores;   // [layers][nqo][nblocks] or NULL
+};
+
+__device__ __forceinline__ void select_rows_of_layer(const SelectTail& t, uint32_t* keys, int layer,
+                                                     int nblocks, char* lds, int wave, int lane) {
+  uint32_t* pmask = reinterpret_cast<uint32_t*>(lds + wave * kTailWaveBytes);
+  unsigned long long* sel = reinterpret_cast<unsigned long long*>(lds + wave * kTailWaveBytes + (kTailMaxBlocks / 32) * 4);
+  for (int n = wave; n < t.nqo; n += kScoreWaves) {
+    const int64_t row = static_cast<int64_t>(layer) * t.nqo + n;
+    uint32_t* sk = keys + row * nblocks;
+    int32_t* ids = t.out_ids + row * t.k_req;
+    float* vals = t.out_vals ? t.out_vals + row * t.k_req : nullptr;
+    float* scores = t.out_scores ? t.out_scores + row * nblocks : nullptr;
+    select_row_wave<kTailMaxBlocks / kWave, true>(sk, nblocks, t.prot, t.nprot, t.k_req, t.order, ids,
+                                                  vals, scores, pmask, sel, lane);
+  }
+}
+
+// One (tile, head) unit of score_kernel, computed by one wavefront.
 template <int R, int G>
-__global__ __launch_bounds__(kScoreThreads) void score_kernel(
+__device__ __forceinline__ void score_unit(
     const uint16_t* __restrict__ q, int64_t q_ls, int nq, int per_query,
     const uint16_t* __restrict__ reps, int64_t reps_ls, int hkv, int cap,
-    int nblocks, int units, uint32_t* __restrict__ keys) {
+    int nblocks, uint32_t* __restrict__ keys, int layer, int unit, int lane, uint4* my) {
   constexpr int TB = kWave / R;  // blocks per tile
-  __shared__ uint4 stage[kScoreWaves][64 * 8];  // per wave: 64 rows x 8 chunks (one half), swizzled
-
   const int nqo = per_query ? nq : 1;
-  const int layer = blockIdx.y;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int unit = blockIdx.x * kScoreWaves + wave;  // (tile, head) pair
-  if (unit >= units) return;
   const int h = unit % hkv;
   const int b0 = (unit / hkv) * TB;
-  const int lane = threadIdx.x & 63;
   const int b = b0 + lane / R;
   const int hq = hkv * G;
   const uint16_t* qL = q + static_cast<int64_t>(layer) * q_ls;
@@ -68,6 +295,9 @@ __global__ __launch_bounds__(kScoreThreads) void score_kernel(
   // are then staged and consumed in two halves (dims 0-63, then 64-127), so
   // each wave needs only 8 KiB of LDS.  Half c8 of chunk c: row = (64c+lane)/16.
   const uint4* src = reinterpret_cast<const uint4*>(rL + (static_cast<int64_t>(h) * cap + b0) * R * kHeadDim);
+  QueryChunks<G> qc;
+  qc.load(qL, hq, h, 0, lane);
+  const int last_row = (nblocks - b0) * R - 1;  // rows past it belong to blocks >= nblocks
   uint4 v[16];
 #pragma unroll
   for (int c = 0; c < 16; ++c) {
@@ -76,15 +306,14 @@ __global__ __launch_bounds__(kScoreThreads) void score_kernel(
     const int i = (c & 7) * 64 + lane;
     const int row = i >> 3;
     const int col = (c >> 3) * 8 + (i & 7);
-    v[c] = (b0 + row / R < nblocks) ? src[row * 16 + col] : make_uint4(0u, 0u, 0u, 0u);
+    v[c] = and_mask(src[min(row, last_row) * 16 + col], row <= last_row);
   }
-  uint4* my = stage[wave];
 
   // per query n: dot over both halves in ascending d (half 0 then half 1);
   // each half is re-staged from registers, so only 8 KiB of LDS per wave.
   float best = -INFINITY;
   for (int n = 0; n < nq; ++n) {
-    const uint4* qh = reinterpret_cast<const uint4*>(qL + (static_cast<int64_t>(n) * hq + h * G) * kHeadDim);
+    if (n > 0) qc.load(qL, hq, h, n, lane);
     float acc[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g] = 0.0f;
@@ -98,19 +327,10 @@ __global__ __launch_bounds__(kScoreThreads) void score_kernel(
         my[row * 8 + (col ^ (row & 7))] = v[hf * 8 + c];
       }
       wave_lds_sync();
-#pragma unroll 2
+#pragma unroll 1
       for (int c = 0; c < 8; ++c) {
         const uint4 rv = my[lane * 8 + (c ^ (lane & 7))];
-        const float rf[8] = {bf16_lo(rv.x), bf16_hi(rv.x), bf16_lo(rv.y), bf16_hi(rv.y),
-                             bf16_lo(rv.z), bf16_hi(rv.z), bf16_lo(rv.w), bf16_hi(rv.w)};
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const uint4 qv = qh[g * 16 + hf * 8 + c];
-          const float qf[8] = {bf16_lo(qv.x), bf16_hi(qv.x), bf16_lo(qv.y), bf16_hi(qv.y),
-                               bf16_lo(qv.z), bf16_hi(qv.z), bf16_lo(qv.w), bf16_hi(qv.w)};
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[g] = __builtin_fmaf(qf[e], rf[e], acc[g]);
-        }
+        qc.fma_chunk(rv, hf * 8 + c, acc);
       }
     }
     float m = acc[0];
@@ -127,6 +347,39 @@ __global__ __launch_bounds__(kScoreThreads) void score_kernel(
   }
   if (!per_query && (lane % R) == 0 && b < nblocks)
     atomicMax(&keys[static_cast<int64_t>(layer) * nblocks + b], score_key(best));
+}
+
+template <int R, int G>
+__global__ __launch_bounds__(kScoreThreads) void score_kernel(
+    const uint16_t* __restrict__ q, int64_t q_ls, int nq, int per_query,
+    const uint16_t* __restrict__ reps, int64_t reps_ls, int hkv, int cap,
+    int nblocks, int units, uint32_t* __restrict__ keys, SelectTail tail) {
+  __shared__ uint4 stage[kScoreWaves][64 * 8];  // per wave: 64 rows x 8 chunks (one half), swizzled
+  static_assert(kScoreWaves * kTailWaveBytes <= static_cast<int>(sizeof(stage)), "tail LDS");
+
+  const int layer = blockIdx.y;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int unit = blockIdx.x * kScoreWaves + wave;  // (tile, head) pair
+  if (unit < units) score_unit<R, G>(q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, keys,
+                                     layer, unit, lane, stage[wave]);
+  if (tail.counters == nullptr) return;
+
+  // Fused selection.  The keys are only ever updated by device-scope atomic
+  // read-modify-writes, which all act at one coherence point, so no cache
+  // write-back or invalidation is needed: each wavefront waits until its own
+  // atomicMax updates are performed (vmcnt(0)) before its workgroup's counter
+  // increment (also an atomic) is issued, and the workgroup that brings the
+  // counter to the layer's workgroup count reads and clears the final keys
+  // with atomicExch.
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = atomicAdd(&tail.counters[layer], 1u) == gridDim.x - 1;
+  __syncthreads();
+  if (!s_last) return;
+  if (threadIdx.x == 0) atomicExch(&tail.counters[layer], 0u);  // ready for the next launch
+  select_rows_of_layer(tail, keys, layer, nblocks, reinterpret_cast<char*>(stage), wave, lane);
 }
 
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
@@ -276,24 +529,59 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
   }
 }
 
+// One wavefront per (layer[, query]) row.
+template <int J>
+__global__ __launch_bounds__(kWave) void topk_wave_kernel(
+    uint32_t* __restrict__ score_keys, int nblocks, const int32_t* __restrict__ prot,
+    int nprot, int k_req, int order, int32_t* __restrict__ out_ids,
+    float* __restrict__ out_vals, int k_stride, float* __restrict__ out_scores) {
+  __shared__ uint32_t pmask[J * 2];  // protected bitmap, one bit per block
+  __shared__ unsigned long long sel[kMaxTopk];
+  const int64_t row = blockIdx.x;
+  select_row_wave<J, false>(score_keys + row * nblocks, nblocks, prot, nprot, k_req, order,
+                     out_ids + row * k_stride, out_vals ? out_vals + row * k_stride : nullptr,
+                     out_scores ? out_scores + row * nblocks : nullptr, pmask, sel, threadIdx.x);
+}
+
+// NANOKV_TOPK_WAVE=0 keeps every row on the workgroup top-k kernel (A/B and
+// cross-checks of the two selection kernels).
+bool topk_wave_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("NANOKV_TOPK_WAVE");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
+// NANOKV_SELECT_FUSED=1 selects inside the scoring launch (one launch less,
+// but every scoring workgroup then waits for its key updates to be performed
+// before it retires; measured slower on the 36-layer 32K decode step).
+bool select_fused_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("NANOKV_SELECT_FUSED");
+    return e && e[0] == '1';
+  }();
+  return on;
+}
+
 template <int R, int G>
 void launch_score(dim3 grid, hipStream_t s, const uint16_t* q, int64_t q_ls, int nq,
                   int per_query, const uint16_t* reps, int64_t reps_ls, int hkv, int cap,
-                  int nblocks, int units, uint32_t* keys) {
+                  int nblocks, int units, uint32_t* keys, const SelectTail& tail) {
   hipLaunchKernelGGL((score_kernel<R, G>), grid, dim3(kScoreThreads), 0, s, q, q_ls, nq,
-                     per_query, reps, reps_ls, hkv, cap, nblocks, units, keys);
+                     per_query, reps, reps_ls, hkv, cap, nblocks, units, keys, tail);
 }
 
 template <int R>
 int dispatch_g(int g, dim3 grid, hipStream_t s, const uint16_t* q, int64_t q_ls, int nq,
                int per_query, const uint16_t* reps, int64_t reps_ls, int hkv, int cap,
-               int nblocks, int units, uint32_t* keys) {
+               int nblocks, int units, uint32_t* keys, const SelectTail& tail) {
   switch (g) {
-    case 1: launch_score<R, 1>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
-    case 2: launch_score<R, 2>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
-    case 4: launch_score<R, 4>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
-    case 8: launch_score<R, 8>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
-    case 16: launch_score<R, 16>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
+    case 1: launch_score<R, 1>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys, tail); return 0;
+    case 2: launch_score<R, 2>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys, tail); return 0;
+    case 4: launch_score<R, 4>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys, tail); return 0;
+    case 8: launch_score<R, 8>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys, tail); return 0;
+    case 16: launch_score<R, 16>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys, tail); return 0;
     default: return -1;
   }
 }
@@ -332,21 +620,50 @@ extern "C" int nkv_select(const nkv_store* st, int layer0, int num_layers, const
   const uint16_t* reps = static_cast<const uint16_t*>(st->reps) + layer0 * reps_ls;
   const int units = ((nblocks + TB - 1) / TB) * st->num_kv_heads;
   dim3 grid((units + kScoreWaves - 1) / kScoreWaves, num_layers);
+  // rows of at most kTailMaxBlocks blocks with k <= kTailMaxK are selected
+  // inside the scoring launch; the per-layer counters follow the keys
+  const bool fused = select_fused_enabled() && topk_wave_enabled() && nblocks <= kTailMaxBlocks &&
+                     k <= kTailMaxK;
+  SelectTail tail{};
+  if (fused) {
+    tail.counters = score_keys + static_cast<int64_t>(num_layers) * nqo * nblocks;
+    tail.prot = protected_ids;
+    tail.nprot = n_protected;
+    tail.k_req = k;
+    tail.order = order;
+    tail.nqo = nqo;
+    tail.out_ids = out_ids;
+    tail.out_vals = out_vals;
+    tail.out_scores = out_scores;
+  }
   int bad = 0;
   switch (R) {
-    case 1: bad = dispatch_g<1>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
-    case 2: bad = dispatch_g<2>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
-    case 4: bad = dispatch_g<4>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
-    case 8: bad = dispatch_g<8>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
+    case 1: bad = dispatch_g<1>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys, tail); break;
+    case 2: bad = dispatch_g<2>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys, tail); break;
+    case 4: bad = dispatch_g<4>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys, tail); break;
+    case 8: bad = dispatch_g<8>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys, tail); break;
     default: bad = -1;
   }
   NKV_CHECK_SUPPORTED(bad == 0, "nkv_select: unsupported (r=%d, G=%d)", R, g);
   rc = launch_status("nkv_select/score");
-  if (rc != NKV_OK) return rc;
+  if (rc != NKV_OK || fused) return rc;
 
+  const dim3 rows(num_layers * nqo);
+  if (topk_wave_enabled() && nblocks <= 32 * kWave) {
+    if (nblocks <= 8 * kWave)
+      hipLaunchKernelGGL(topk_wave_kernel<8>, rows, dim3(kWave), 0, s, score_keys, nblocks,
+                         protected_ids, n_protected, k, order, out_ids, out_vals, k, out_scores);
+    else if (nblocks <= 16 * kWave)
+      hipLaunchKernelGGL(topk_wave_kernel<16>, rows, dim3(kWave), 0, s, score_keys, nblocks,
+                         protected_ids, n_protected, k, order, out_ids, out_vals, k, out_scores);
+    else
+      hipLaunchKernelGGL(topk_wave_kernel<32>, rows, dim3(kWave), 0, s, score_keys, nblocks,
+                         protected_ids, n_protected, k, order, out_ids, out_vals, k, out_scores);
+    return launch_status("nkv_select/topk");
+  }
   const int nwords = (nblocks + 31) >> 5;
   const size_t tsmem = static_cast<size_t>(nblocks + nwords) * sizeof(uint32_t);
-  hipLaunchKernelGGL(topk_kernel, dim3(num_layers * nqo), dim3(kTopkThreads), tsmem, s, score_keys,
+  hipLaunchKernelGGL(topk_kernel, rows, dim3(kTopkThreads), tsmem, s, score_keys,
                      nblocks, protected_ids, n_protected, k, order, out_ids, out_vals, k, out_scores);
   return launch_status("nkv_select/topk");
 }

@@ -123,9 +123,13 @@ class SparseKVStore:
 
     def select(self, layer0: int, q, nblocks: int, prot_dev, n_prot: int, k: int, order: int,
                per_query: bool, score_keys, out_scores, out_ids, out_vals) -> None:
-        """score_keys: zeroed uint32 workspace (left zeroed); out_scores may be None."""
+        """score_keys: zeroed uint32 workspace of nl * (nq' * nblocks + 1) words (left
+        zeroed), nq' = nq if per_query else 1; out_scores may be None."""
         self._bf16(q, "q")
         nl, nq = q.shape[0], q.shape[1]
+        need = nl * ((nq if per_query else 1) * nblocks + 1)
+        if score_keys.numel() < need or score_keys.dtype not in (torch.int32, torch.uint32):
+            raise ValueError(f"select: score_keys needs {need} 32-bit words, got {score_keys.numel()}")
         _lib.check(self.lib.nkv_select(
             self._desc_ref, layer0, nl, _ptr(q), q.stride(0), nq, int(per_query), nblocks,
             _ptr(prot_dev), n_prot, k, order, _ptr(score_keys), _ptr(out_scores), _ptr(out_ids),

@@ -48,6 +48,9 @@ def _rand_q(nq, seed):
     (300, 2, 3, {0, 3, 299, 1000}, 24, 6),
     (64, 8, 1, "none", 16, 7),
     (100, 1, 2, "std", 48, 8),
+    (1024, 4, 1, "std", 200, 9),     # wavefront top-k, k > 64: LDS sort path
+    (4096, 4, 1, "std", 64, 10),     # past 2048 blocks: workgroup top-k kernel
+    (3000, 2, 1, "std", 300, 11),    # workgroup kernel, ragged, large k
 ])
 def test_scores_and_ids_bit_exact(nb, r, nq, prot, budget, seed):
     rt = _runtime(nb, r=r, top_k=max(budget, 32))

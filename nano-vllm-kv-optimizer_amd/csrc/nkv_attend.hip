@@ -24,8 +24,9 @@
 //  * softmax: fp32, exp2 with the scale folded in.
 //  * P.V on the vector ALUs in fp32: lane (r, c) owns dims 8c..8c+7 of keys
 //    4j + r; p comes from LDS.  The int8 V scale (per block or per token) is
-//    folded into p.  V loads are issued right after the MFMAs so they overlap
-//    the softmax.
+//    folded into p.  With 4 query rows (decode) V loads are issued together
+//    with the K loads, so a segment's 32 KiB are in flight at once; wider
+//    accumulators issue them right after the MFMAs, overlapping the softmax.
 //  * the 4 wavefronts merge through LDS; with splits > 1 each workgroup
 //    writes a partial (m, l, acc[128]) per query row and a second kernel
 //    merges them (stream order makes the partials visible).
@@ -126,9 +127,28 @@ __global__ __launch_bounds__(kAttendThreads, (FMT == NKV_KV_BF16 && M == 4) ? NK
     const bool int8_seg = (FMT != NKV_KV_BF16) && g.type == kSegHist;
     const int last = g.len - 1;
 
-    // ---- S^T = K . Q^T on the matrix cores -------------------------------
-    // lane (lg, ln) loads dims [32 s + 8 lg, +8) of key 16 i + ln.
+    // ---- K loads, S^T = K . Q^T on the matrix cores, V loads ----------------
+    // K: lane (lg, ln) loads dims [32 s + 8 lg, +8) of key 16 i + ln (the
+    // MFMA A operand); V: lane (lg, ln) loads dims [8 ln, +8) of key 4 j + lg.
+    // With 4 query rows V is issued together with K, so a segment's 32 KiB
+    // are in flight at once (the registers fit 2 waves per SIMD); wider
+    // accumulators issue V after the MFMAs so K and V are not live together.
+    constexpr bool kVEarly = (M == 4);
     f32x4 c[4];
+    uint4 va[16];
+    auto load_v = [&]() __attribute__((always_inline)) {
+      if (int8_seg) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const uint2 r = *reinterpret_cast<const uint2*>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 8);
+          va[j] = make_uint4(r.x, r.y, 0u, 0u);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          va[j] = *reinterpret_cast<const uint4*>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 16);
+      }
+    };
     if (int8_seg) {
       uint2 ka[4][4];
 #pragma unroll
@@ -137,6 +157,7 @@ __global__ __launch_bounds__(kAttendThreads, (FMT == NKV_KV_BF16 && M == 4) ? NK
 #pragma unroll
         for (int s = 0; s < 4; ++s) ka[i][s] = *reinterpret_cast<const uint2*>(rp + s * 32);
       }
+      if (kVEarly) load_v();
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         c[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -153,6 +174,7 @@ __global__ __launch_bounds__(kAttendThreads, (FMT == NKV_KV_BF16 && M == 4) ? NK
 #pragma unroll
         for (int s = 0; s < 4; ++s) ka[i][s] = *reinterpret_cast<const uint4*>(rp + s * 64);
       }
+      if (kVEarly) load_v();
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         c[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -161,23 +183,10 @@ __global__ __launch_bounds__(kAttendThreads, (FMT == NKV_KV_BF16 && M == 4) ? NK
           c[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[i][s]), bq[s], c[i], 0, 0, 0);
       }
     }
-
-    // ---- V loads go out now and overlap the softmax below -----------------
-    // lane (lg, ln) loads dims [8 ln, +8) of key 4 j + lg.  The scheduling
-    // barrier keeps them after the MFMAs so K and V registers are not live
-    // together (occupancy).
-    __builtin_amdgcn_sched_barrier(0);
-    uint4 va[16];
-    if (int8_seg) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint2 r = *reinterpret_cast<const uint2*>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 8);
-        va[j] = make_uint4(r.x, r.y, 0u, 0u);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        va[j] = *reinterpret_cast<const uint4*>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 16);
+    if (!kVEarly) {
+      // the scheduling barrier keeps these loads after the MFMAs
+      __builtin_amdgcn_sched_barrier(0);
+      load_v();
     }
 
     // ---- masking, scale, online softmax ------------------------------------

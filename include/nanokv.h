@@ -97,11 +97,9 @@ const char* nkv_last_error(void);
  * [0, nblocks) are ignored) are scored -inf.  k_eff = min(k, max(1, nblocks
  * - |protected in range|)) ids are returned per (layer[, n]), ordered by
  * `order`; exact ties go to the lower block id.
- * score_keys : uint32 workspace of num_layers * (nq' * nblocks + 1) words
- *              (nq' = per_query ? nq : 1): the score keys [num_layers][nq']
- *              [nblocks] followed by one completion counter per layer.  It
- *              must be zero before the first call; every call leaves it zero.
- *              Calls that share one workspace must not overlap.
+ * score_keys : uint32 workspace [num_layers][nq'][nblocks] (nq' = per_query ?
+ *              nq : 1) that must be zero before the first call; every call
+ *              leaves it zero.  Calls that share one workspace must not overlap.
  * out_scores : fp32 [num_layers][nq'][nblocks] raw scores (before the
  *              protected mask), or NULL.
  * out_ids    : int32 [num_layers][nq'][k] (entries >= k_eff untouched).

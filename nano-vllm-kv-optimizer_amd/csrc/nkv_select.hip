@@ -41,9 +41,6 @@ constexpr int kTopkThreads = 256;
 constexpr int kMaxTopk = 1024;
 constexpr int kMaxSelectBlocks = 12288;  // keys + masks + sort buffer stay under 64 KiB of LDS
 constexpr uint32_t kNegInfKey = 0x007fffffu;  // score_key(-inf)
-// s_waitcnt immediate: vmcnt(0), expcnt and lgkmcnt left at their maxima
-// (vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
-constexpr int kWaitVmcnt0 = (7 << 4) | (15 << 8);
 
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
@@ -120,7 +117,7 @@ __device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v,
 // J ballots.  Collection is the same ascending-id ballot pass as topk_kernel;
 // up to 64 selected entries are then sorted by a bitonic network across the
 // lanes (shuffles), larger k by the same network over LDS.
-template <int J, bool kAtomicKeys>
+template <int J>
 __device__ __forceinline__ void select_row_wave(
     uint32_t* __restrict__ sk, int nblocks, const int32_t* __restrict__ prot, int nprot,
     int k_req, int order, int32_t* __restrict__ ids, float* __restrict__ vals,
@@ -142,21 +139,18 @@ __device__ __forceinline__ void select_row_wave(
 
   // keys past nblocks are 0, below every key score_key() produces.  Every
   // read is issued (past nblocks it re-reads the last key), so one wait
-  // covers them all; the atomic form reads and clears in one atomicAnd, an
-  // all-ones mask leaving the re-read key untouched.
+  // covers them all.
   uint32_t key[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int i = kWave * j + lane;
-    const bool valid = i < nblocks;
-    uint32_t* kp = sk + (valid ? i : nblocks - 1);
-    key[j] = kAtomicKeys ? atomicAnd(kp, valid ? 0u : 0xffffffffu) : *kp;
+    key[j] = sk[i < nblocks ? i : nblocks - 1];
   }
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int i = kWave * j + lane;
     if (i < nblocks) {
-      if (!kAtomicKeys) sk[i] = 0u;  // leave the key buffer zeroed for the next scoring pass
+      sk[i] = 0u;  // leave the key buffer zeroed for the next scoring pass
       if (scores) scores[i] = key_score(key[j]);
       if ((pmask[i >> 5] >> (i & 31)) & 1u) key[j] = kNegInfKey;
     } else {
@@ -244,38 +238,6 @@ __device__ __forceinline__ void select_row_wave(
 }
 
 
-// Selection fused into the scoring launch: the last workgroup to finish a
-// layer (a per-layer completion counter) selects that layer's rows, one
-// wavefront per row, while other layers are still being scored.  Used for
-// rows of at most kTailMaxBlocks blocks and k <= kTailMaxK.
-constexpr int kTailMaxBlocks = 8 * kWave;  // 8 key registers: the scorer's occupancy stays
-constexpr int kTailMaxK = 256;
-constexpr int kTailWaveBytes = (kTailMaxBlocks / 32) * 4 + kTailMaxK * 8;  // pmask + sel per wavefront
-
-struct SelectTail {
-  uint32_t* counters;  // [num_layers], zero between launches; NULL: no fused selection
-  const int32_t* prot;
-  int nprot, k_req, order, nqo;
-  int32_t* out_ids;    // [layers][nqo][k_req]
-  float* out_vals;     // same shape or NULL
-  float* out_scores;   // [layers][nqo][nblocks] or NULL
-};
-
-__device__ __forceinline__ void select_rows_of_layer(const SelectTail& t, uint32_t* keys, int layer,
-                                                     int nblocks, char* lds, int wave, int lane) {
-  uint32_t* pmask = reinterpret_cast<uint32_t*>(lds + wave * kTailWaveBytes);
-  unsigned long long* sel = reinterpret_cast<unsigned long long*>(lds + wave * kTailWaveBytes + (kTailMaxBlocks / 32) * 4);
-  for (int n = wave; n < t.nqo; n += kScoreWaves) {
-    const int64_t row = static_cast<int64_t>(layer) * t.nqo + n;
-    uint32_t* sk = keys + row * nblocks;
-    int32_t* ids = t.out_ids + row * t.k_req;
-    float* vals = t.out_vals ? t.out_vals + row * t.k_req : nullptr;
-    float* scores = t.out_scores ? t.out_scores + row * nblocks : nullptr;
-    select_row_wave<kTailMaxBlocks / kWave, true>(sk, nblocks, t.prot, t.nprot, t.k_req, t.order, ids,
-                                                  vals, scores, pmask, sel, lane);
-  }
-}
-
 // One (tile, head) unit of score_kernel, computed by one wavefront.
 template <int R, int G>
 __device__ __forceinline__ void score_unit(
@@ -353,33 +315,13 @@ template <int R, int G>
 __global__ __launch_bounds__(kScoreThreads) void score_kernel(
     const uint16_t* __restrict__ q, int64_t q_ls, int nq, int per_query,
     const uint16_t* __restrict__ reps, int64_t reps_ls, int hkv, int cap,
-    int nblocks, int units, uint32_t* __restrict__ keys, SelectTail tail) {
+    int nblocks, int units, uint32_t* __restrict__ keys) {
   __shared__ uint4 stage[kScoreWaves][64 * 8];  // per wave: 64 rows x 8 chunks (one half), swizzled
-  static_assert(kScoreWaves * kTailWaveBytes <= static_cast<int>(sizeof(stage)), "tail LDS");
-
-  const int layer = blockIdx.y;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
   const int unit = blockIdx.x * kScoreWaves + wave;  // (tile, head) pair
-  if (unit < units) score_unit<R, G>(q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, keys,
-                                     layer, unit, lane, stage[wave]);
-  if (tail.counters == nullptr) return;
-
-  // Fused selection.  The keys are only ever updated by device-scope atomic
-  // read-modify-writes, which all act at one coherence point, so no cache
-  // write-back or invalidation is needed: each wavefront waits until its own
-  // atomicMax updates are performed (vmcnt(0)) before its workgroup's counter
-  // increment (also an atomic) is issued, and the workgroup that brings the
-  // counter to the layer's workgroup count reads and clears the final keys
-  // with atomicExch.
-  __shared__ int s_last;
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = atomicAdd(&tail.counters[layer], 1u) == gridDim.x - 1;
-  __syncthreads();
-  if (!s_last) return;
-  if (threadIdx.x == 0) atomicExch(&tail.counters[layer], 0u);  // ready for the next launch
-  select_rows_of_layer(tail, keys, layer, nblocks, reinterpret_cast<char*>(stage), wave, lane);
+  if (unit >= units) return;
+  score_unit<R, G>(q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, keys, blockIdx.y, unit,
+                   threadIdx.x & 63, stage[wave]);
 }
 
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
@@ -538,7 +480,7 @@ __global__ __launch_bounds__(kWave) void topk_wave_kernel(
   __shared__ uint32_t pmask[J * 2];  // protected bitmap, one bit per block
   __shared__ unsigned long long sel[kMaxTopk];
   const int64_t row = blockIdx.x;
-  select_row_wave<J, false>(score_keys + row * nblocks, nblocks, prot, nprot, k_req, order,
+  select_row_wave<J>(score_keys + row * nblocks, nblocks, prot, nprot, k_req, order,
                      out_ids + row * k_stride, out_vals ? out_vals + row * k_stride : nullptr,
                      out_scores ? out_scores + row * nblocks : nullptr, pmask, sel, threadIdx.x);
 }
@@ -553,35 +495,24 @@ bool topk_wave_enabled() {
   return on;
 }
 
-// NANOKV_SELECT_FUSED=1 selects inside the scoring launch (one launch less,
-// but every scoring workgroup then waits for its key updates to be performed
-// before it retires; measured slower on the 36-layer 32K decode step).
-bool select_fused_enabled() {
-  static const bool on = [] {
-    const char* e = getenv("NANOKV_SELECT_FUSED");
-    return e && e[0] == '1';
-  }();
-  return on;
-}
-
 template <int R, int G>
 void launch_score(dim3 grid, hipStream_t s, const uint16_t* q, int64_t q_ls, int nq,
                   int per_query, const uint16_t* reps, int64_t reps_ls, int hkv, int cap,
-                  int nblocks, int units, uint32_t* keys, const SelectTail& tail) {
+                  int nblocks, int units, uint32_t* keys) {
   hipLaunchKernelGGL((score_kernel<R, G>), grid, dim3(kScoreThreads), 0, s, q, q_ls, nq,
-                     per_query, reps, reps_ls, hkv, cap, nblocks, units, keys, tail);
+                     per_query, reps, reps_ls, hkv, cap, nblocks, units, keys);
 }
 
 template <int R>
 int dispatch_g(int g, dim3 grid, hipStream_t s, const uint16_t* q, int64_t q_ls, int nq,
                int per_query, const uint16_t* reps, int64_t reps_ls, int hkv, int cap,
-               int nblocks, int units, uint32_t* keys, const SelectTail& tail) {
+               int nblocks, int units, uint32_t* keys) {
   switch (g) {
-    case 1: launch_score<R, 1>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys, tail); return 0;
-    case 2: launch_score<R, 2>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys, tail); return 0;
-    case 4: launch_score<R, 4>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys, tail); return 0;
-    case 8: launch_score<R, 8>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys, tail); return 0;
-    case 16: launch_score<R, 16>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys, tail); return 0;
+    case 1: launch_score<R, 1>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
+    case 2: launch_score<R, 2>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
+    case 4: launch_score<R, 4>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
+    case 8: launch_score<R, 8>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
+    case 16: launch_score<R, 16>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
     default: return -1;
   }
 }
@@ -620,33 +551,17 @@ extern "C" int nkv_select(const nkv_store* st, int layer0, int num_layers, const
   const uint16_t* reps = static_cast<const uint16_t*>(st->reps) + layer0 * reps_ls;
   const int units = ((nblocks + TB - 1) / TB) * st->num_kv_heads;
   dim3 grid((units + kScoreWaves - 1) / kScoreWaves, num_layers);
-  // rows of at most kTailMaxBlocks blocks with k <= kTailMaxK are selected
-  // inside the scoring launch; the per-layer counters follow the keys
-  const bool fused = select_fused_enabled() && topk_wave_enabled() && nblocks <= kTailMaxBlocks &&
-                     k <= kTailMaxK;
-  SelectTail tail{};
-  if (fused) {
-    tail.counters = score_keys + static_cast<int64_t>(num_layers) * nqo * nblocks;
-    tail.prot = protected_ids;
-    tail.nprot = n_protected;
-    tail.k_req = k;
-    tail.order = order;
-    tail.nqo = nqo;
-    tail.out_ids = out_ids;
-    tail.out_vals = out_vals;
-    tail.out_scores = out_scores;
-  }
   int bad = 0;
   switch (R) {
-    case 1: bad = dispatch_g<1>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys, tail); break;
-    case 2: bad = dispatch_g<2>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys, tail); break;
-    case 4: bad = dispatch_g<4>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys, tail); break;
-    case 8: bad = dispatch_g<8>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys, tail); break;
+    case 1: bad = dispatch_g<1>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
+    case 2: bad = dispatch_g<2>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
+    case 4: bad = dispatch_g<4>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
+    case 8: bad = dispatch_g<8>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
     default: bad = -1;
   }
   NKV_CHECK_SUPPORTED(bad == 0, "nkv_select: unsupported (r=%d, G=%d)", R, g);
   rc = launch_status("nkv_select/score");
-  if (rc != NKV_OK || fused) return rc;
+  if (rc != NKV_OK) return rc;
 
   const dim3 rows(num_layers * nqo);
   if (topk_wave_enabled() && nblocks <= 32 * kWave) {

@@ -310,7 +310,7 @@ class _SparseCore:
         nl, nq = q.shape[0], q.shape[1]
         nqo = nq if per_query else 1
         prot, n_prot = self.protected_dev()
-        keys = self._zeroed_keys(nl * (nqo * nb + 1))  # keys + one completion counter per layer
+        keys = self._zeroed_keys(nl * nqo * nb)
         scores = self._buf("scores", nl * nqo * nb, torch.float32)
         ids = self._buf("ids", nl * nqo * requested, torch.int32).view(nl, nqo, requested)
         vals = self._buf("vals", nl * nqo * requested, torch.float32).view(nl, nqo, requested)

@@ -123,11 +123,11 @@ class SparseKVStore:
 
     def select(self, layer0: int, q, nblocks: int, prot_dev, n_prot: int, k: int, order: int,
                per_query: bool, score_keys, out_scores, out_ids, out_vals) -> None:
-        """score_keys: zeroed uint32 workspace of nl * (nq' * nblocks + 1) words (left
+        """score_keys: zeroed uint32 workspace of nl * nq' * nblocks words (left
         zeroed), nq' = nq if per_query else 1; out_scores may be None."""
         self._bf16(q, "q")
         nl, nq = q.shape[0], q.shape[1]
-        need = nl * ((nq if per_query else 1) * nblocks + 1)
+        need = nl * (nq if per_query else 1) * nblocks
         if score_keys.numel() < need or score_keys.dtype not in (torch.int32, torch.uint32):
             raise ValueError(f"select: score_keys needs {need} 32-bit words, got {score_keys.numel()}")
         _lib.check(self.lib.nkv_select(

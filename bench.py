@@ -259,6 +259,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-layers", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--layer-streams", type=int, default=1,
+                    help="streams the decode step's layer ranges are spread over")
     ap.add_argument("--step-events", choices=["device", "torch"], default="device",
                     help="timing events: device-scope release (default) or torch.cuda.Event")
     ap.add_argument("--workload", choices=["decode", "prefill"], default="decode",
@@ -300,7 +302,7 @@ def main():
     cfg = M12Config(max_model_len=T, top_k_blocks=args.top_k, quant_history=quant,
                     quant_scale_layout="token" if args.kv_format == "int8_token" else "channel_block",
                     attend_splits=args.splits)
-    model = M12ModelRuntime(L, cfg, device=dev)
+    model = M12ModelRuntime(L, cfg, device=dev, layer_streams=args.layer_streams)
 
     t0 = time.perf_counter()
     kh = torch.empty(L, T, 8, 128, dtype=torch.bfloat16, device=dev)
@@ -322,11 +324,12 @@ def main():
     torch.cuda.synchronize()
 
     # Two timed regions over the same workload.  A: K steps bracketed by one
-    # event pair -> the step time and `value`.  B: K more steps with an event
-    # pair around each step's attention launches (attend + merge) -> the
-    # kernel's average launch duration for the roofline.  A record leaves the
-    # GPU idle for a few microseconds, so region B's steps run slower than A's
-    # and its launch durations include part of that idle time (conservative).
+    # event pair -> the step time and `value` (model.decode: the layers split
+    # over --layer-streams streams).  B: K more steps, all layers on one
+    # stream, with an event pair around each step's attention launches
+    # (attend + merge) -> the kernel's average launch duration for the
+    # roofline.  A record leaves the GPU idle for a few microseconds, so
+    # region B's launch durations include part of that idle time (conservative).
     K = args.steps
     if args.step_events == "torch":
         tev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * K + 2)]
@@ -387,6 +390,7 @@ def main():
                          f"top-{args.top_k} + sink {cfg.sink_tokens} + recent {cfg.recent_tokens}, "
                          f"r=4, {args.kv_format} history"),
             "layers": L, "context": T, "top_k": args.top_k, "kv_format": args.kv_format,
+            "layer_streams": args.layer_streams,
         },
         "us_per_layer_step": round(us_layer, 4),
         "hbm_gbps": round(step_gbps, 1),

@@ -162,6 +162,42 @@ int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads, int num_he
                                     int tq, int splits);
 
 /*
+ * The whole sparse decode layer-step for `num_layers` layers in one call:
+ * nkv_select (per_query=0, NKV_ORDER_SCORE_DESC, no out_scores / out_vals)
+ * then nkv_attend (tq = 1, n_chunk = 1, allowed = NULL) for every layer.
+ *
+ * Replaces steps 2 + 5 (with the recent-ring append of step 1) of
+ * M12LayerRuntime.decode (nanovllm/sparse/m12_runtime.py:1141-1346) for a
+ * batch of independent layers.
+ *
+ * The layers are split into min(nstreams, num_layers) contiguous ranges;
+ * range r is enqueued on streams[r] (streams[0] is the caller's stream; the
+ * others first wait for the work already on streams[0], and streams[0] waits
+ * for all of them before this returns).  Each range makes exactly the
+ * launches a single-range call would for its layers, so results do not
+ * depend on nstreams.  The first multi-stream call on a host thread creates
+ * nstreams events (no timing, no system-scope fence) for the current
+ * device, kept for the thread's lifetime.
+ * q, out : bf16 [num_layers][1][Hq][D]; k_new, v_new: bf16 [num_layers][1][Hkv][D]
+ *          (contiguous).
+ * score_keys : as nkv_select, [num_layers][nblocks].
+ * out_ids    : int32 [num_layers][k]; n_hist: the ids attended per layer
+ *              (k_eff of nkv_select, 1 <= n_hist <= k).
+ * sink_len, write_slot, ring_base, rec_lo, rec_len, scale, splits: as nkv_attend.
+ * partial_ws : >= nkv_decode_step_workspace_floats(...) floats (splits > 1).
+ */
+int nkv_decode_step(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
+                    const uint16_t* k_new, const uint16_t* v_new, int nblocks,
+                    const int32_t* protected_ids, int n_protected, int k, int n_hist,
+                    int sink_len, int write_slot, int ring_base, int rec_lo, int rec_len,
+                    float scale, int splits, uint32_t* score_keys, int32_t* out_ids,
+                    float* partial_ws, uint16_t* out, int nstreams, void* const* streams);
+
+/* Floats of partial_ws needed by nkv_decode_step (one attention workspace per range). */
+int64_t nkv_decode_step_workspace_floats(int num_layers, int num_kv_heads, int num_heads,
+                                         int splits, int nstreams);
+
+/*
  * Segmented causal GQA attention for a chunk of many queries, on the matrix
  * cores (bf16 MFMA for Q.K^T and P.V, fp32 softmax and accumulation).
  *

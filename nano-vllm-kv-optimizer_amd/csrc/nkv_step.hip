@@ -1,0 +1,134 @@
+// The sparse decode layer-step for a batch of layers in one host call:
+// selection (score + top-k) then attention, with the layers split into
+// contiguous ranges enqueued on several streams.
+//
+// Replaces, for every layer of a model at once, steps 2 and 5 of
+// M12LayerRuntime.decode (nanovllm/sparse/m12_runtime.py:1141-1346): the
+// selection of _gpu_select (:959-1055) and the attention over
+// [selected | sink | recent | new token] (:1212-1320), with the recent-ring
+// shift + append of step 1 (:1164-1172) done by the attention launch.
+//
+// The layers are independent, so each range runs exactly the launches a
+// single-range call would make for those layers (same kernels, same launch
+// shapes: the attention split count is the caller's), and the results are
+// identical.  What the ranges can buy is overlap: one range's launch-bound
+// top-k and merge kernels, and every kernel's tail, run beside another
+// range's bandwidth-bound scoring and attention.  The per-call joins cost
+// GPU time too (on the 36-layer 32K step two ranges measured 135 us against
+// 128 us for one), so one range is the default of the Python runtime.
+#include <vector>
+
+#include "nkv_common.h"
+
+namespace nkv {
+namespace {
+
+constexpr int kMaxStepStreams = 8;
+
+// Events of this host thread for the current device, created on first use
+// (disable-timing events; they live as long as the thread).
+int step_events(int n, hipEvent_t* out) {
+  struct PerDevice {
+    int dev;
+    std::vector<hipEvent_t> ev;
+  };
+  static thread_local std::vector<PerDevice> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  PerDevice* pd = nullptr;
+  for (auto& c : cache)
+    if (c.dev == dev) pd = &c;
+  if (pd == nullptr) {
+    cache.push_back(PerDevice{dev, {}});
+    pd = &cache.back();
+  }
+  while (static_cast<int>(pd->ev.size()) < n) {
+    hipEvent_t e;
+    // the joins are between streams of one device: no system-scope fence
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventDisableSystemFence) != hipSuccess)
+      return -1;
+    pd->ev.push_back(e);
+  }
+  for (int i = 0; i < n; ++i) out[i] = pd->ev[i];
+  return 0;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  set_error("%s: %s", what, hipGetErrorString(e));
+  return NKV_ERR_HIP;
+}
+
+}  // namespace
+}  // namespace nkv
+
+using namespace nkv;
+
+extern "C" int64_t nkv_decode_step_workspace_floats(int num_layers, int num_kv_heads, int num_heads,
+                                                    int splits, int nstreams) {
+  if (nstreams < 1 || nstreams > kMaxStepStreams || num_layers < 1) return 0;
+  const int per = (num_layers + nstreams - 1) / nstreams;  // the largest range
+  const int64_t f = nkv_attend_workspace_floats(per, num_kv_heads, num_heads, 1, splits);
+  return f > 0 ? f * nstreams : 0;
+}
+
+extern "C" int nkv_decode_step(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
+                               const uint16_t* k_new, const uint16_t* v_new, int nblocks,
+                               const int32_t* protected_ids, int n_protected, int k, int n_hist,
+                               int sink_len, int write_slot, int ring_base, int rec_lo, int rec_len,
+                               float scale, int splits, uint32_t* score_keys, int32_t* out_ids,
+                               float* partial_ws, uint16_t* out, int nstreams, void* const* streams) {
+  int rc = check_store(st, layer0, num_layers);
+  if (rc != NKV_OK) return rc;
+  NKV_CHECK_ARG(nstreams >= 1 && nstreams <= kMaxStepStreams, "nkv_decode_step: nstreams must be in [1, %d] (got %d)",
+                kMaxStepStreams, nstreams);
+  NKV_CHECK_ARG(streams != nullptr, "nkv_decode_step: streams is NULL");
+  NKV_CHECK_ARG(q != nullptr && k_new != nullptr && v_new != nullptr && score_keys != nullptr &&
+                    out_ids != nullptr && out != nullptr,
+                "nkv_decode_step: q, k_new, v_new, score_keys, out_ids and out must be non-NULL");
+  NKV_CHECK_ARG(n_hist >= 1 && n_hist <= k, "nkv_decode_step: n_hist must be in [1, k] (got %d, k=%d)", n_hist, k);
+  NKV_CHECK_ARG(splits > 1 ? partial_ws != nullptr : true, "nkv_decode_step: splits > 1 needs partial_ws");
+  const int nranges = nstreams < num_layers ? nstreams : num_layers;
+
+  // contiguous per-layer strides: q/out [L][1][Hq][D], k/v [L][1][Hkv][D],
+  // ids [L][k], keys [L][nblocks]
+  const int64_t q_ls = static_cast<int64_t>(st->num_heads) * kHeadDim;
+  const int64_t kv_ls = static_cast<int64_t>(st->num_kv_heads) * kHeadDim;
+  const int per = (num_layers + nranges - 1) / nranges;
+  const int64_t ws_range = nkv_attend_workspace_floats(per, st->num_kv_heads, st->num_heads, 1, splits);
+
+  hipStream_t s0 = reinterpret_cast<hipStream_t>(streams[0]);
+  hipEvent_t ev[kMaxStepStreams];
+  if (nranges > 1) {
+    NKV_CHECK_ARG(step_events(nranges, ev) == 0, "nkv_decode_step: could not create stream events");
+    const hipError_t e = hipEventRecord(ev[0], s0);
+    if (e != hipSuccess) return hip_fail(e, "nkv_decode_step: hipEventRecord");
+  }
+  for (int r = 0; r < nranges; ++r) {
+    const int l0 = static_cast<int>(static_cast<int64_t>(r) * num_layers / nranges);
+    const int l1 = static_cast<int>(static_cast<int64_t>(r + 1) * num_layers / nranges);
+    const int nl = l1 - l0;
+    void* sr = streams[r];
+    if (r > 0) {
+      const hipError_t e = hipStreamWaitEvent(reinterpret_cast<hipStream_t>(sr), ev[0], 0);
+      if (e != hipSuccess) return hip_fail(e, "nkv_decode_step: hipStreamWaitEvent");
+    }
+    rc = nkv_select(st, layer0 + l0, nl, q + l0 * q_ls, q_ls, 1, 0, nblocks, protected_ids, n_protected, k,
+                    NKV_ORDER_SCORE_DESC, score_keys + static_cast<int64_t>(l0) * nblocks, nullptr,
+                    out_ids + static_cast<int64_t>(l0) * k, nullptr, sr);
+    if (rc != NKV_OK) return rc;
+    rc = nkv_attend(st, layer0 + l0, nl, q + l0 * q_ls, q_ls, 1, k_new + l0 * kv_ls, v_new + l0 * kv_ls, kv_ls,
+                    1, write_slot, out_ids + static_cast<int64_t>(l0) * k, k, n_hist, nullptr, sink_len,
+                    ring_base, rec_lo, rec_len, scale, splits, partial_ws ? partial_ws + r * ws_range : nullptr,
+                    out + l0 * q_ls, sr);
+    if (rc != NKV_OK) return rc;
+    if (r > 0) {
+      const hipError_t e = hipEventRecord(ev[r], reinterpret_cast<hipStream_t>(sr));
+      if (e != hipSuccess) return hip_fail(e, "nkv_decode_step: hipEventRecord");
+    }
+  }
+  for (int r = 1; r < nranges; ++r) {
+    const hipError_t e = hipStreamWaitEvent(s0, ev[r], 0);
+    if (e != hipSuccess) return hip_fail(e, "nkv_decode_step: hipStreamWaitEvent");
+  }
+  return NKV_OK;
+}

@@ -216,12 +216,12 @@ class _SparseCore:
             self._ws[name] = t
         return t[:numel]
 
-    def _zeroed_keys(self, numel: int) -> torch.Tensor:
+    def _zeroed_keys(self, numel: int, ws: str = "") -> torch.Tensor:
         """Score-key workspace: zero before first use, left zero by every select."""
-        t = self._ws.get("keys")
+        t = self._ws.get("keys" + ws)
         if t is None or t.numel() < numel:
             t = torch.zeros(max(numel, 1), dtype=torch.int32, device=self.device)
-            self._ws["keys"] = t
+            self._ws["keys" + ws] = t
         return t[:numel]
 
     def reset(self) -> None:
@@ -299,8 +299,13 @@ class _SparseCore:
         return min(int(requested), max(1, nb - n_prot))
 
     def select(self, q: torch.Tensor, requested: int, *, per_query: bool = False,
-               order: int = _lib.NKV_ORDER_SCORE_DESC):
-        """q: [nl, nq, Hq, D] bf16 -> (ids [nl, nq', requested] int32, vals, k_eff)."""
+               order: int = _lib.NKV_ORDER_SCORE_DESC, lo: int = 0, ws: str = "",
+               ids_out: torch.Tensor | None = None):
+        """q: [nl, nq, Hq, D] bf16 -> (ids [nl, nq', requested] int32, vals, k_eff).
+
+        lo: first layer of q relative to this core's range; ws tags the
+        workspaces (calls in flight together on different streams need their
+        own); ids_out: optional destination for the ids."""
         nb = self.nblocks_filled
         if nb <= 0:
             raise ValueError("selection needs at least one history block")
@@ -310,11 +315,14 @@ class _SparseCore:
         nl, nq = q.shape[0], q.shape[1]
         nqo = nq if per_query else 1
         prot, n_prot = self.protected_dev()
-        keys = self._zeroed_keys(nl * nqo * nb)
-        scores = self._buf("scores", nl * nqo * nb, torch.float32)
-        ids = self._buf("ids", nl * nqo * requested, torch.int32).view(nl, nqo, requested)
-        vals = self._buf("vals", nl * nqo * requested, torch.float32).view(nl, nqo, requested)
-        self.store.select(self.layer0, q, nb, prot, n_prot, requested, order, per_query,
+        keys = self._zeroed_keys(nl * nqo * nb, ws)
+        scores = self._buf("scores" + ws, nl * nqo * nb, torch.float32)
+        if ids_out is None:
+            ids = self._buf("ids" + ws, nl * nqo * requested, torch.int32).view(nl, nqo, requested)
+        else:
+            ids = ids_out
+        vals = self._buf("vals" + ws, nl * nqo * requested, torch.float32).view(nl, nqo, requested)
+        self.store.select(self.layer0 + lo, q, nb, prot, n_prot, requested, order, per_query,
                           keys, scores, ids, vals)
         self._last_scores = scores.view(nl, nqo, nb)
         return ids, vals, self.effective_k(requested)
@@ -330,7 +338,7 @@ class _SparseCore:
         return max(1, min(-(-nseg // 4), want, 64))
 
     def attend(self, q, k_new, v_new, *, n_chunk, write_slot, ids, ids_stride,
-               n_hist, allowed, sink_len, ring_base, rec_lo, rec_len):
+               n_hist, allowed, sink_len, ring_base, rec_lo, rec_len, lo=0, ws="", out=None):
         cfg = self.cfg
         nl, tq = q.shape[0], q.shape[1]
         g = cfg.num_heads // cfg.num_kv_heads
@@ -339,30 +347,54 @@ class _SparseCore:
         R = cfg.recent_tokens
         nseg = n_hist + -(-sink_len // 64) + (-(-R // 64) if rec_len else 0) + -(-n_chunk // 64)
         splits = self._splits(nseg, nqg)
-        out = torch.empty_like(q)
-        part = self._buf("partial", self.store.attend_workspace_floats(nl, tq, splits), torch.float32)
-        self.store.attend(self.layer0, q, k_new, v_new, n_chunk, write_slot, ids,
+        if out is None:
+            out = torch.empty_like(q)
+        part = self._buf("partial" + ws, self.store.attend_workspace_floats(nl, tq, splits), torch.float32)
+        self.store.attend(self.layer0 + lo, q, k_new, v_new, n_chunk, write_slot, ids,
                           ids_stride, n_hist, allowed, sink_len, ring_base, rec_lo, rec_len,
                           cfg.scale, splits, part, out)
         return out
 
-    def decode_attend(self, q, k, v, ids, ids_stride, n_hist):
-        """Decode step 1 + 3-5 (m12_runtime.py:1164-1320): q [nl,1,Hq,D], k/v [nl,1,Hkv,D]."""
+    def decode_attend(self, q, k, v, ids, ids_stride, n_hist, *, lo=0, ws="", out=None,
+                      advance=True):
+        """Decode step 1 + 3-5 (m12_runtime.py:1164-1320): q [nl,1,Hq,D], k/v [nl,1,Hkv,D].
+
+        lo / ws / out: layer sub-range, workspace tag and output destination
+        (see select); advance=False leaves the ring position and length for
+        advance_decode()."""
+        w = self.decode_window()
+        out = self.attend(q.contiguous(), k.contiguous(), v.contiguous(), n_chunk=1,
+                          write_slot=w["write_slot"], ids=ids,
+                          ids_stride=ids_stride, n_hist=n_hist, allowed=None,
+                          sink_len=w["sink_len"], ring_base=w["ring_base"],
+                          rec_lo=w["rec_lo"], rec_len=w["rec_len"], lo=lo, ws=ws, out=out)
+        if advance:
+            self.advance_decode()
+        return out, w["sink_len"], w["rec_len"] + 1
+
+    def decode_window(self) -> dict:
+        """Segments of this step's decode attention.  The logical recent window
+        after the shift is [R - rec_len, R); its last slot is the new token,
+        attended as a one-token chunk and stored into the freed physical slot
+        (the old logical slot 0), so the ring part is the rec_len - 1 before it."""
         cfg = self.cfg
         R = cfg.recent_tokens
-        sink_len = min(cfg.sink_tokens, self.valid_len)
         rec_len = min(R, self.valid_len + 1)
-        # logical window after the shift = [R - rec_len, R); its last slot is
-        # the new token, attended as a one-token chunk and stored into the
-        # freed physical slot (the old logical slot 0).
-        out = self.attend(q.contiguous(), k.contiguous(), v.contiguous(), n_chunk=1,
-                          write_slot=self.ring_start, ids=ids,
-                          ids_stride=ids_stride, n_hist=n_hist, allowed=None,
-                          sink_len=sink_len, ring_base=(self.ring_start + 1) % R,
-                          rec_lo=R - rec_len, rec_len=rec_len - 1)
-        self.ring_start = (self.ring_start + 1) % R
+        return {"sink_len": min(cfg.sink_tokens, self.valid_len), "write_slot": self.ring_start,
+                "ring_base": (self.ring_start + 1) % R, "rec_lo": R - rec_len,
+                "rec_len": rec_len - 1}
+
+    def decode_splits(self, n_hist: int) -> int:
+        """The attention split count decode_attend uses for n_hist selected blocks."""
+        w = self.decode_window()
+        B, R = self.cfg.block_size, self.cfg.recent_tokens
+        nseg = n_hist + -(-w["sink_len"] // B) + (-(-R // B) if w["rec_len"] else 0) + 1
+        return self._splits(nseg, 1)
+
+    def advance_decode(self) -> None:
+        """The decode token is in the ring: move the ring start, grow the length."""
+        self.ring_start = (self.ring_start + 1) % self.cfg.recent_tokens
         self.valid_len += 1
-        return out, sink_len, rec_len
 
     def chunk_attend(self, q, k, v, ids, ids_stride, n_hist, allowed=None):
         """[selected | sink | previous recent | chunk (causal)] (m12_runtime.py:592-639, :725-758)."""
@@ -793,9 +825,18 @@ class M12ModelRuntime:
     layers (grid dimension = layer).  Inputs carry a leading layer dimension:
     q [L, T, Hq, D], k/v [L, T, Hkv, D].  Semantics per layer are exactly
     those of M12LayerRuntime (all layers share the sequence bookkeeping).
+
+    decode() is one native call (nkv_decode_step): selection then attention
+    for every layer, the layers split into `layer_streams` contiguous ranges
+    on as many streams (the caller's current stream first).  The layers are
+    independent and each range makes the launches a one-range call would, so
+    the result does not depend on layer_streams.  More ranges let one range's
+    launch-bound top-k and merge kernels overlap another's bandwidth-bound
+    kernels, but each step then pays two cross-stream joins; on the 36-layer
+    32K step one range is faster (128 vs 135 us), hence the default.
     """
 
-    def __init__(self, num_layers: int, cfg: M12Config, device=None):
+    def __init__(self, num_layers: int, cfg: M12Config, device=None, layer_streams: int = 1):
         _check_hip_shapes(cfg)
         self.cfg = cfg
         self.num_layers = num_layers
@@ -809,6 +850,10 @@ class M12ModelRuntime:
         self.core = _SparseCore(cfg, self.store, 0, num_layers)
         self.last_ids_dev: torch.Tensor | None = None
         self.last_n_selected = 0
+        if layer_streams < 1:
+            raise ValueError("layer_streams must be >= 1")
+        self.layer_streams = min(layer_streams, num_layers)
+        self._side_streams: list = []   # created on the first decode (default priority)
 
     @property
     def valid_len(self) -> int:
@@ -853,8 +898,29 @@ class M12ModelRuntime:
 
     def decode(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         """One decode step for every layer: q [L, 1, Hq, D], k/v [L, 1, Hkv, D] -> o [L, 1, Hq, D]."""
-        ids, _, n = self.select(q)
-        out, _, _ = self.core.decode_attend(q, k, v, ids, ids.shape[-1], n)
+        cfg, core = self.cfg, self.core
+        if core.nblocks_filled <= 0:
+            raise ValueError("selection needs at least one history block")
+        req = cfg.top_k_blocks if cfg.decode_top_k_blocks is None else cfg.decode_top_k_blocks
+        L, nb = self.num_layers, core.nblocks_filled
+        dev = self.store.device
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        if len(self._side_streams) < self.layer_streams - 1:
+            self._side_streams = [torch.cuda.Stream(dev) for _ in range(self.layer_streams - 1)]
+        streams = [torch.cuda.current_stream(dev).cuda_stream] + [s.cuda_stream for s in self._side_streams]
+        prot, n_prot = core.protected_dev()
+        n = core.effective_k(req)
+        splits = core.decode_splits(n)
+        w = core.decode_window()
+        out = torch.empty_like(q)
+        ids = torch.empty(L, 1, req, dtype=torch.int32, device=dev)
+        keys = core._zeroed_keys(L * nb, "/step")
+        part = core._buf("partial/step", self.store.decode_step_workspace_floats(L, splits, len(streams)),
+                         torch.float32)
+        self.store.decode_step(0, q, k, v, nb, prot, n_prot, req, n, w["sink_len"], w["write_slot"],
+                               w["ring_base"], w["rec_lo"], w["rec_len"], cfg.scale, splits, keys, ids,
+                               part, out, streams)
+        core.advance_decode()
         self.last_ids_dev = ids
         self.last_n_selected = n
         return out

@@ -165,6 +165,33 @@ class SparseKVStore:
         return int(self.lib.nkv_attend_workspace_floats(nl, self.num_kv_heads, self.num_heads,
                                                         tq, splits))
 
+    def decode_step(self, layer0: int, q, k_new, v_new, nblocks: int, prot_dev, n_prot: int,
+                    k: int, n_hist: int, sink_len: int, write_slot: int, ring_base: int,
+                    rec_lo: int, rec_len: int, scale: float, splits: int, score_keys, out_ids,
+                    partial_ws, out, streams) -> None:
+        """nkv_decode_step: selection + attention for q.shape[0] layers, the layer
+        ranges on `streams` (raw stream handles, the caller's first)."""
+        self._bf16(q, "q")
+        self._bf16(out, "out")
+        nl = q.shape[0]
+        if not (q.is_contiguous() and k_new.is_contiguous() and v_new.is_contiguous()
+                and out.is_contiguous() and out_ids.is_contiguous()):
+            raise ValueError("decode_step: q, k_new, v_new, out and out_ids must be contiguous")
+        if q.shape[1] != 1 or k_new.shape[:2] != (nl, 1) or out.shape != q.shape:
+            raise ValueError("decode_step: expects q/out [L, 1, Hq, D] and k/v [L, 1, Hkv, D]")
+        if out_ids.numel() < nl * k or score_keys.numel() < nl * nblocks:
+            raise ValueError("decode_step: out_ids or score_keys too small")
+        arr = (ctypes.c_void_p * len(streams))(*streams)
+        _lib.check(self.lib.nkv_decode_step(
+            self._desc_ref, layer0, nl, _ptr(q), _ptr(k_new), _ptr(v_new), nblocks, _ptr(prot_dev),
+            n_prot, k, n_hist, sink_len, write_slot, ring_base, rec_lo, rec_len, float(scale), splits,
+            _ptr(score_keys), _ptr(out_ids), _ptr(partial_ws), _ptr(out), len(streams), arr),
+            "decode_step")
+
+    def decode_step_workspace_floats(self, nl: int, splits: int, nstreams: int) -> int:
+        return int(self.lib.nkv_decode_step_workspace_floats(nl, self.num_kv_heads, self.num_heads,
+                                                             splits, nstreams))
+
 
 def query_summaries(q, nsegments: int):
     """prefill_query_summaries on device: q [nl, T, Hq, D] -> [nl, nseg, Hq, D] bf16."""

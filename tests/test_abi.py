@@ -82,3 +82,32 @@ def test_prefill_entry_rejects_bad_arguments_without_device_work():
     rc = lib.nkv_prefill_attend(ctypes.byref(st), 0, 1, dummy, 0, 64, dummy, dummy, 0, None, 0, 0,
                                 None, 0, 0, 0, 0, 1.0, dummy, None)
     assert rc == _lib.NKV_ERR_UNSUPPORTED
+
+
+def test_decode_step_rejects_bad_arguments_without_device_work():
+    lib = _lib.load()
+    st = _lib.NkvStore()
+    st.num_layers, st.num_heads, st.num_kv_heads = 4, 32, 8
+    st.head_dim, st.block_size, st.r, st.cap_blocks = 128, 64, 4, 16
+    st.sink_tokens, st.recent_tokens, st.kv_format = 64, 512, 0
+    dummy = ctypes.c_void_p(16)   # never dereferenced: every call below fails validation
+    st.hist_k = st.hist_v = st.reps = dummy
+    st.sink_k = st.sink_v = st.recent_k = st.recent_v = dummy
+    streams = (ctypes.c_void_p * 2)(None, None)
+
+    def call(nstreams=2, streams_arr=streams, n_hist=32, q=dummy, partial=dummy, splits=3):
+        return lib.nkv_decode_step(ctypes.byref(st), 0, 4, q, dummy, dummy, 16, dummy, 1, 32, n_hist,
+                                   64, 0, 1, 0, 511, 1.0, splits, dummy, dummy, partial, dummy,
+                                   nstreams, streams_arr)
+
+    assert call(nstreams=0) == _lib.NKV_ERR_ARG and b"nstreams" in lib.nkv_last_error()
+    assert call(nstreams=9) == _lib.NKV_ERR_ARG and b"nstreams" in lib.nkv_last_error()
+    assert call(streams_arr=None) == _lib.NKV_ERR_ARG and b"streams is NULL" in lib.nkv_last_error()
+    assert call(q=None) == _lib.NKV_ERR_ARG and b"non-NULL" in lib.nkv_last_error()
+    assert call(n_hist=33) == _lib.NKV_ERR_ARG and b"n_hist" in lib.nkv_last_error()
+    assert call(n_hist=0) == _lib.NKV_ERR_ARG and b"n_hist" in lib.nkv_last_error()
+    assert call(partial=None) == _lib.NKV_ERR_ARG and b"partial_ws" in lib.nkv_last_error()
+    # one attention workspace per range, sized for the largest range
+    per = lib.nkv_attend_workspace_floats(2, 8, 32, 1, 3)
+    assert lib.nkv_decode_step_workspace_floats(4, 8, 32, 3, 2) == 2 * per
+    assert lib.nkv_decode_step_workspace_floats(4, 8, 32, 3, 0) == 0

@@ -178,3 +178,31 @@ def test_model_runtime_batches_layers_like_per_layer_runtimes():
                                rt.last_block_ids.to(torch.int32))
             a, b = out[i].float().cpu(), o_i.float().cpu()
             assert ((a - b).abs() <= 2.0 ** -7 * b.abs() + 1e-6).all()   # one bf16 ulp
+
+
+@pytest.mark.parametrize("streams", [2, 3])
+def test_layer_streams_identical_to_one_stream(streams):
+    """decode() with the layers split over several streams gives bit-identical
+    ids and outputs to the single-stream step (the layers are independent and
+    each keeps its launch shape), step after step as the ring advances."""
+    from nanokv_amd import workload
+    from nanokv_amd.sparse import M12Config, M12ModelRuntime
+    L, T, steps = 5, 8192, 4
+    cfg = M12Config(max_model_len=T + 64)
+    one = M12ModelRuntime(L, cfg, layer_streams=1)
+    many = M12ModelRuntime(L, cfg, layer_streams=streams)
+    hist = [workload.history(T, 300 + i) for i in range(L)]
+    k = torch.stack([h[0] for h in hist]).cuda()
+    v = torch.stack([h[1] for h in hist]).cuda()
+    one.prefill(k, v)
+    many.prefill(k, v)
+    qs, ks, vs = workload.decode_inputs(steps, 11, layers=L)
+    for s in range(steps):
+        q, kk, vv = qs[s].cuda(), ks[s].cuda(), vs[s].cuda()
+        o1 = one.decode(q, kk, vv)
+        o2 = many.decode(q, kk, vv)
+        assert one.last_n_selected == many.last_n_selected
+        n = one.last_n_selected
+        assert torch.equal(one.last_ids_dev[:, :, :n], many.last_ids_dev[:, :, :n])
+        assert torch.equal(o1, o2)
+        assert many.valid_len == one.valid_len

@@ -17,11 +17,11 @@
 // start first.
 //
 // Per 64-key segment (double-buffered LDS, one barrier per segment):
-//   * staging: bf16 rows go global -> LDS directly (buffer_load ... lds, no
+//   * staging: rows go global -> LDS directly (buffer_load ... lds, no
 //     registers; bounds-checked descriptors read rows past the segment as
-//     zero, so no index is clamped).  int8 history rows go through registers
-//     and are dequantised to bf16.  The next segment is in flight while the
-//     current one is computed;
+//     zero, so no index is clamped).  int8 history rows land raw with their
+//     scales and are dequantised to bf16 in LDS after the copy.  The next
+//     segment is in flight while the current one is computed;
 //   * S^T = K . Q^T: v_mfma_f32_16x16x32_bf16, A = 16 keys x 32 dims read from
 //     the K tile, B = 32 dims x 16 columns held in registers all along;
 //   * online softmax in fp32 per column (exp2, scale folded in); each lane's

@@ -36,6 +36,8 @@
 // summation order.
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "nkv_attend_common.h"
 
 namespace nkv {
@@ -52,7 +54,7 @@ constexpr int attend_lds_floats() {
 }
 
 template <int FMT, int M>
-__global__ __launch_bounds__(kAttendThreads, (FMT == NKV_KV_BF16 && M == 4) ? NKV_ATTEND_DECODE_WAVES : 1) void attend_kernel(const AttendParams p) {
+__global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 1) void attend_kernel(const AttendParams p) {
   __shared__ __attribute__((aligned(16))) float s_lds[attend_lds_floats<M>()];
   __shared__ float s_alpha[kAttendWaves][kMaxRows];
 
@@ -122,9 +124,12 @@ __global__ __launch_bounds__(kAttendThreads, (FMT == NKV_KV_BF16 && M == 4) ? NK
 
   float* my_p = s_lds + wave * kBlock * kPRow;
   const int nwaves = p.splits * kAttendWaves;
-  for (int sidx = split * kAttendWaves + wave; sidx < p.nseg; sidx += nwaves) {
+  // One segment of this wavefront.  int8 history segments (always the first
+  // n_hist segments) and bf16 segments are two instantiations of the body, run
+  // by two loops in segment order, so neither carries the other's registers.
+  auto segment = [&](const int sidx, auto int8_tag) __attribute__((always_inline)) {
+    constexpr bool int8_seg = decltype(int8_tag)::value;
     const Seg g = make_seg<FMT>(p, layer, h, sidx);
-    const bool int8_seg = (FMT != NKV_KV_BF16) && g.type == kSegHist;
     const int last = g.len - 1;
 
     // ---- K loads, S^T = K . Q^T on the matrix cores, V loads ----------------
@@ -210,7 +215,7 @@ __global__ __launch_bounds__(kAttendThreads, (FMT == NKV_KV_BF16 && M == 4) ? NK
         } else if (g.type == kSegChunk) {
           ok = ok && (g.off + tk) <= my_t;
         }
-        if (FMT == NKV_KV_INT8_TOKEN && g.type == kSegHist)
+        if (FMT == NKV_KV_INT8_TOKEN && int8_seg)
           v *= f16_bits_to_f32(p.k_tscale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap * kBlock +
                                           static_cast<int64_t>(g.blk) * kBlock + tk]);
         v = ok ? v * p.scale_log2 : -INFINITY;
@@ -223,7 +228,7 @@ __global__ __launch_bounds__(kAttendThreads, (FMT == NKV_KV_BF16 && M == 4) ? NK
     const float m_new = fmaxf(m_run, cmax);
     const float alpha = (m_new == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
     float vs_blk = 1.0f;
-    if (FMT == NKV_KV_INT8_CHANNEL && g.type == kSegHist)
+    if (FMT == NKV_KV_INT8_CHANNEL && int8_seg)
       vs_blk = p.v_scale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap + g.blk];
     float lsum = 0.0f;
 #pragma unroll
@@ -234,7 +239,7 @@ __global__ __launch_bounds__(kAttendThreads, (FMT == NKV_KV_BF16 && M == 4) ? NK
         const float pe = (x[i][e] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(x[i][e] - m_new);
         lsum += pe;
         float pv = pe * vs_blk;
-        if (FMT == NKV_KV_INT8_TOKEN && g.type == kSegHist)
+        if (FMT == NKV_KV_INT8_TOKEN && int8_seg)
           pv *= f16_bits_to_f32(p.v_tscale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap * kBlock +
                                            static_cast<int64_t>(g.blk) * kBlock + tk]);
         my_p[tk * kPRow + ln] = pv;
@@ -278,7 +283,11 @@ __global__ __launch_bounds__(kAttendThreads, (FMT == NKV_KV_BF16 && M == 4) ? NK
       }
     }
     wave_lds_sync();
-  }
+  };
+  int sidx = split * kAttendWaves + wave;
+  if (FMT != NKV_KV_BF16)
+    for (; sidx < p.n_hist; sidx += nwaves) segment(sidx, std::true_type{});
+  for (; sidx < p.nseg; sidx += nwaves) segment(sidx, std::false_type{});
 
   // ---- reduce the wave's state across lane groups --------------------------
   l_run += __shfl_xor(l_run, 16);

@@ -10,7 +10,7 @@ namespace nkv {
 namespace attend_detail {
 
 #ifndef NKV_ATTEND_DECODE_WAVES
-#define NKV_ATTEND_DECODE_WAVES 2  // waves per SIMD the bf16 decode variant is built for (3 spills and measured slower)
+#define NKV_ATTEND_DECODE_WAVES 2  // waves per SIMD the 4-row (decode) variants are built for (3 spills and measured slower)
 #endif
 constexpr int kAttendWaves = 4;
 constexpr int kAttendThreads = kAttendWaves * kWave;

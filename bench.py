@@ -245,6 +245,94 @@ def bench_prefill(args, dev):
     }
 
 
+def verify_bytes(u_mean, nblocks, tq, kv_format, hkv=8, d=128, r=4, hq=32, B=64, sink=64, recent=512):
+    """Algorithmic bytes of one lossless verify layer-step: reps + the union's
+    blocks (K+V) + sink + recent + the chunk's K/V + q and o."""
+    elem = 1 if kv_format != "bf16" else 2
+    reps = nblocks * hkv * r * d * 2
+    union = u_mean * hkv * B * d * 2 * elem
+    scales = 0 if kv_format == "bf16" else (u_mean * hkv * 4 if kv_format == "int8" else u_mean * hkv * B * 2 * 2)
+    ring = (sink + recent) * hkv * d * 2 * 2
+    chunk = tq * hkv * d * 2 * 2
+    qo = tq * hq * d * 2 * 2
+    return reps + union + scales + ring + chunk + qo
+
+
+def bench_verify(args, dev):
+    """Speculative verify: Tq = 6 draft + target tokens of every layer against its history.
+
+    A round is one lossless verification pass for all layers (M12ModelRuntime.verify:
+    per-query Top-K, device-side union + per-query mask, causal attention over
+    [union | sink | recent | the Tq tokens]) followed by a rollback, so every
+    round sees the same state.
+    """
+    import torch
+
+    from nanokv_amd import workload
+    from nanokv_amd.sparse import M12Config, M12ModelRuntime
+
+    L, T0, tq = args.layers, args.context, args.verify_tokens
+    quant = args.kv_format != "bf16"
+    extra = {} if args.mfma_chunk_min is None else {"mfma_chunk_min_tokens": args.mfma_chunk_min}
+    cfg = M12Config(max_model_len=T0 + 64, top_k_blocks=args.top_k, quant_history=quant,
+                    quant_scale_layout="token" if args.kv_format == "int8_token" else "channel_block",
+                    **extra)
+    model = M12ModelRuntime(L, cfg, device=dev)
+    kh = torch.empty(L, T0, 8, 128, dtype=torch.bfloat16, device=dev)
+    vh = torch.empty_like(kh)
+    for i in range(L):
+        k, v, _, _ = workload.history(T0, args.seed + i, device=dev)
+        kh[i].copy_(k)
+        vh[i].copy_(v)
+    model.prefill(kh, vh)
+    del kh, vh
+    g = torch.Generator(device=dev).manual_seed(args.seed + 31)
+    nrounds = args.warmup + args.steps
+    qs = torch.randn(nrounds, L, tq, 32, 128, generator=g, device=dev).to(torch.bfloat16)
+    ks = (torch.randn(nrounds, L, tq, 8, 128, generator=g, device=dev) * 128 ** -0.5).to(torch.bfloat16)
+    vs = (torch.randn(nrounds, L, tq, 8, 128, generator=g, device=dev) * 128 ** -0.5).to(torch.bfloat16)
+    for i in range(args.warmup):
+        model.verify(qs[i], ks[i], vs[i], lossless=True)
+        model.rollback_verified()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        model.verify(qs[args.warmup + i], ks[args.warmup + i], vs[args.warmup + i], lossless=True)
+        model.rollback_verified()
+    stop.record()
+    torch.cuda.synchronize()
+    ms_round = start.elapsed_time(stop) / args.steps
+    u_mean = float(model.last_union_count_dev.float().mean())  # the last round's unions
+    by = verify_bytes(u_mean, model.nblocks_filled, tq, args.kv_format) * L
+    return {
+        "metric": "µs per lossless speculative-verify round (all layers)",
+        "value": round(ms_round * 1e3, 2),
+        "unit": "µs",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_round, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if args.kv_format == "bf16" else "int8",
+        "data": "synthetic (seeded N(0,1)/sqrt(128) K/V history and draft K/V, N(0,1) queries)",
+        "config": {
+            "workload": (f"lossless speculative verify, {tq} tokens vs {T0}-token history x {L} layers, "
+                         f"per-query top-{args.top_k}, union + per-query mask, sink {cfg.sink_tokens} + "
+                         f"recent {cfg.recent_tokens}, {args.kv_format} history"),
+            "layers": L, "context": T0, "verify_tokens": tq, "top_k": args.top_k,
+            "kv_format": args.kv_format,
+        },
+        "us_per_layer_round": round(ms_round * 1e3 / L, 4),
+        "union_blocks_mean": round(u_mean, 1),
+        "hbm_gbps": round(by / (ms_round * 1e-3) / 1e9, 1),
+        "step_roofline_frac": round(by / (ms_round * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -263,8 +351,12 @@ def main():
                     help="streams the decode step's layer ranges are spread over")
     ap.add_argument("--step-events", choices=["device", "torch"], default="device",
                     help="timing events: device-scope release (default) or torch.cuda.Event")
-    ap.add_argument("--workload", choices=["decode", "prefill"], default="decode",
-                    help="decode (the headline line) or the chunked-prefill attention")
+    ap.add_argument("--verify-tokens", type=int, default=6, help="verify: queries per round")
+    ap.add_argument("--mfma-chunk-min", type=int, default=None,
+                    help="verify: M12Config.mfma_chunk_min_tokens (chunks this long use the MFMA kernel)")
+    ap.add_argument("--workload", choices=["decode", "prefill", "verify"], default="decode",
+                    help="decode (the headline line), the chunked-prefill attention, or "
+                         "lossless speculative verify (use --context 16384)")
     ap.add_argument("--chunk", type=int, default=4096, help="prefill chunk length")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (counter calibration)")
@@ -296,6 +388,9 @@ def main():
         return
     if args.workload == "prefill":
         print(json.dumps(bench_prefill(args, dev)), flush=True)
+        return
+    if args.workload == "verify":
+        print(json.dumps(bench_verify(args, dev)), flush=True)
         return
     L, T = args.layers, args.context
     quant = args.kv_format != "bf16"

@@ -135,8 +135,10 @@ int nkv_select(const nkv_store* st, int layer0, int num_layers,
  * attended recent window.
  * q      : bf16 [num_layers][tq][Hq][D] (layer stride q_layer_stride).
  * k_new, v_new : bf16 [num_layers][n_chunk][Hkv][D] (layer stride kv_layer_stride).
- * ids    : int32 [num_layers][ids_layer_stride]; ids outside [0, cap) attend nothing.
- * allowed: uint8 [tq][n_hist] (shared by layers) or NULL.
+ * ids    : int32 [num_layers][ids_layer_stride]; ids outside [0, cap) attend
+ *          nothing (and cost no loads: a union padded with -1 is fine).
+ * allowed: uint8 [tq][n_hist] per layer, layer stride allowed_layer_stride
+ *          (0: one mask shared by all layers, else >= tq * n_hist), or NULL.
  * out    : bf16 [num_layers][tq][Hq][D] (layer stride q_layer_stride).
  * partial_ws : fp32 workspace, >= nkv_attend_workspace_floats(...) floats
  *              (unused when splits == 1).
@@ -152,7 +154,7 @@ int nkv_attend(const nkv_store* st, int layer0, int num_layers,
                const uint16_t* k_new, const uint16_t* v_new, int64_t kv_layer_stride,
                int n_chunk, int write_slot,
                const int32_t* ids, int64_t ids_layer_stride, int n_hist,
-               const uint8_t* allowed, int sink_len,
+               const uint8_t* allowed, int64_t allowed_layer_stride, int sink_len,
                int ring_base, int rec_lo, int rec_len,
                float scale, int splits,
                float* partial_ws, uint16_t* out, void* stream);
@@ -198,6 +200,28 @@ int64_t nkv_decode_step_workspace_floats(int num_layers, int num_kv_heads, int n
                                          int splits, int nstreams);
 
 /*
+ * Union of per-query selections, for lossless speculative verify.
+ *
+ * Replaces the host-side union + mask of M12LayerRuntime._gpu_select_per_query
+ * (nanovllm/sparse/m12_runtime.py:1057-1087: torch.unique of the per-query
+ * Top-K ids, searchsorted, scatter into `allowed`) for num_layers layers at
+ * once, on the device, so verify needs no device-to-host round trip.
+ *
+ * ids         : int32 [num_layers][tq][k], the per-query selections of
+ *               nkv_select (per_query = 1); the first k_eff of each row are used.
+ * out_union   : int32 [num_layers][umax]: the distinct ids ascending, then -1.
+ * out_count   : int32 [num_layers]: the union sizes.
+ * out_allowed : uint8 [num_layers][tq][umax]: 1 where union[u] is among
+ *               query t's ids (0 past the union).
+ * Feed out_union (n_hist = umax) and out_allowed (allowed_layer_stride =
+ * tq * umax) to nkv_attend / nkv_prefill_attend.
+ * Constraints: 1 <= tq <= 16, 1 <= k_eff <= k, tq * k_eff <= 4096,
+ *              umax >= tq * k_eff.
+ */
+int nkv_select_union(const int32_t* ids, int num_layers, int tq, int k, int k_eff, int umax,
+                     int32_t* out_union, int32_t* out_count, uint8_t* out_allowed, void* stream);
+
+/*
  * Segmented causal GQA attention for a chunk of many queries, on the matrix
  * cores (bf16 MFMA for Q.K^T and P.V, fp32 softmax and accumulation).
  *
@@ -218,7 +242,7 @@ int nkv_prefill_attend(const nkv_store* st, int layer0, int num_layers,
                        const uint16_t* q, int64_t q_layer_stride, int tq,
                        const uint16_t* k_new, const uint16_t* v_new, int64_t kv_layer_stride,
                        const int32_t* ids, int64_t ids_layer_stride, int n_hist,
-                       const uint8_t* allowed, int sink_len,
+                       const uint8_t* allowed, int64_t allowed_layer_stride, int sink_len,
                        int ring_base, int rec_lo, int rec_len,
                        float scale, uint16_t* out, void* stream);
 

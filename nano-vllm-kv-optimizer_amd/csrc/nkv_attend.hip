@@ -130,6 +130,9 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
   auto segment = [&](const int sidx, auto int8_tag) __attribute__((always_inline)) {
     constexpr bool int8_seg = decltype(int8_tag)::value;
     const Seg g = make_seg<FMT>(p, layer, h, sidx);
+    // an id outside the history attends nothing: no loads (a fully masked
+    // segment would leave m, l and acc exactly as they are)
+    if (g.type == kSegHist && g.vlen == 0) return;
     const int last = g.len - 1;
 
     // ---- K loads, S^T = K . Q^T on the matrix cores, V loads ----------------
@@ -197,7 +200,9 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
     // ---- masking, scale, online softmax ------------------------------------
     // c[i][e]: key tk = 16 i + 4 lg + e, query row ln.
     const uint8_t* allow_row =
-        (g.type == kSegHist && p.allowed != nullptr) ? p.allowed + static_cast<int64_t>(my_t) * p.n_hist : nullptr;
+        (g.type == kSegHist && p.allowed != nullptr)
+            ? p.allowed + p.allowed_ls * layer + static_cast<int64_t>(my_t) * p.n_hist
+            : nullptr;
     const bool seg_allowed = allow_row == nullptr || allow_row[g.u] != 0;
     float x[4][4];
     float cmax = -INFINITY;
@@ -437,7 +442,8 @@ int fill_attend_params(const char* who, const nkv_store* st, int layer0, int num
                        const uint16_t* q, int64_t q_layer_stride, int tq, const uint16_t* k_new,
                        const uint16_t* v_new, int64_t kv_layer_stride, int n_chunk, int write_slot,
                        const int32_t* ids, int64_t ids_layer_stride, int n_hist,
-                       const uint8_t* allowed, int sink_len, int ring_base, int rec_lo, int rec_len,
+                       const uint8_t* allowed, int64_t allowed_layer_stride, int sink_len,
+                       int ring_base, int rec_lo, int rec_len,
                        float scale, int splits, float* partial_ws, uint16_t* out,
                        AttendParams* pp) {
   int rc = check_store(st, layer0, num_layers);
@@ -497,7 +503,11 @@ int fill_attend_params(const char* who, const nkv_store* st, int layer0, int num
   p.kv_ls = kv_layer_stride;
   p.ids = ids;
   p.ids_ls = ids_layer_stride;
+  NKV_CHECK_ARG(allowed_layer_stride == 0 || allowed_layer_stride >= static_cast<int64_t>(tq) * n_hist,
+                "%s: allowed_layer_stride %lld is neither 0 (shared) nor >= tq * n_hist", who,
+                static_cast<long long>(allowed_layer_stride));
   p.allowed = allowed;
+  p.allowed_ls = allowed ? allowed_layer_stride : 0;
   p.partial = partial_ws;
   p.out = out;
   p.hkv = st->num_kv_heads;
@@ -529,14 +539,14 @@ extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const
                           int64_t q_layer_stride, int tq, const uint16_t* k_new,
                           const uint16_t* v_new, int64_t kv_layer_stride, int n_chunk,
                           int write_slot, const int32_t* ids, int64_t ids_layer_stride,
-                          int n_hist, const uint8_t* allowed, int sink_len, int ring_base,
-                          int rec_lo, int rec_len, float scale, int splits, float* partial_ws,
-                          uint16_t* out, void* stream) {
+                          int n_hist, const uint8_t* allowed, int64_t allowed_layer_stride,
+                          int sink_len, int ring_base, int rec_lo, int rec_len, float scale, int splits,
+                          float* partial_ws, uint16_t* out, void* stream) {
   AttendParams p;
   const int rc = fill_attend_params("nkv_attend", st, layer0, num_layers, q, q_layer_stride, tq, k_new,
                                     v_new, kv_layer_stride, n_chunk, write_slot, ids, ids_layer_stride,
-                                    n_hist, allowed, sink_len, ring_base, rec_lo, rec_len, scale, splits,
-                                    partial_ws, out, &p);
+                                    n_hist, allowed, allowed_layer_stride, sink_len, ring_base, rec_lo,
+                                    rec_len, scale, splits, partial_ws, out, &p);
   if (rc != NKV_OK) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   // bf16 history without a per-query mask: the streaming kernel (whatever

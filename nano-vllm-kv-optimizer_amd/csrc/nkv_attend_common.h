@@ -44,7 +44,8 @@ struct AttendParams {
   int64_t kv_ls;
   const int32_t* ids;
   int64_t ids_ls;
-  const uint8_t* allowed;
+  const uint8_t* allowed;   // [tq][n_hist] per layer, layer stride allowed_ls (0: shared)
+  int64_t allowed_ls;
   float* partial;
   uint16_t* out;
   int hkv, G, cap, S, R;
@@ -177,7 +178,8 @@ int fill_attend_params(const char* who, const nkv_store* st, int layer0, int num
                        const uint16_t* q, int64_t q_layer_stride, int tq, const uint16_t* k_new,
                        const uint16_t* v_new, int64_t kv_layer_stride, int n_chunk, int write_slot,
                        const int32_t* ids, int64_t ids_layer_stride, int n_hist,
-                       const uint8_t* allowed, int sink_len, int ring_base, int rec_lo, int rec_len,
+                       const uint8_t* allowed, int64_t allowed_layer_stride, int sink_len,
+                       int ring_base, int rec_lo, int rec_len,
                        float scale, int splits, float* partial_ws, uint16_t* out,
                        attend_detail::AttendParams* p);
 

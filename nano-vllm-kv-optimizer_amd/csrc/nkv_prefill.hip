@@ -282,7 +282,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
     if (g.type == kSegHist && p.allowed != nullptr) {
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct)
-        allow_nxt[ct] = p.allowed[static_cast<int64_t>(min(tcol[ct], p.tq - 1)) * p.n_hist + g.u];
+        allow_nxt[ct] = p.allowed[p.allowed_ls * layer + static_cast<int64_t>(min(tcol[ct], p.tq - 1)) * p.n_hist + g.u];
     }
   };
   auto finish_stage = [&](const Seg& g, char* buf) {
@@ -294,21 +294,38 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
     }
   };
 
-  Seg nxt = make_seg<FMT>(p, layer, h, 0);
+  // the next segment at or after s that attends anything (its block id in
+  // *blk): history ids outside [0, cap) (a union padded with -1) are passed
+  // over, never staged
+  auto next_seg = [&](int s, int* blk) {
+    *blk = 0;
+    for (; s < p.n_hist; ++s) {
+      *blk = p.ids[static_cast<int64_t>(layer) * p.ids_ls + s];
+      if (*blk >= 0 && *blk < p.cap) break;
+    }
+    return s;
+  };
+
+  int blk_first;
+  const int s_first = next_seg(0, &blk_first);
+  Seg nxt = make_seg_blk<FMT>(p, layer, h, s_first, blk_first);
   begin_stage(nxt, lds0);
   finish_stage(nxt, lds0);
 
   // One segment: compute on buffer P while the next segment is staged into
   // buffer 1 - P.
+  // Returns the segment after s.
   auto step = [&](auto parity, int s) {
     constexpr int P = decltype(parity)::value;
     char* buf = P == 0 ? lds0 : lds1;
     char* other = P == 0 ? lds1 : lds0;
     const Seg cur = nxt;
     const int allow_cur[2] = {allow_nxt[0], allow_nxt[1]};
-    const bool more = s + 1 < nseg;
+    int blk_next;
+    const int s_next = next_seg(s + 1, &blk_next);
+    const bool more = s_next < nseg;
     if (more) {
-      nxt = make_seg<FMT>(p, layer, h, s + 1);
+      nxt = make_seg_blk<FMT>(p, layer, h, s_next, blk_next);
       begin_stage(nxt, other);
     }
 
@@ -392,11 +409,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
       finish_stage(nxt, other);
     else
       __syncthreads();
+    return s_next;
   };
 
-  for (int s = 0; s < nseg; s += 2) {
-    step(std::integral_constant<int, 0>{}, s);
-    if (s + 1 < nseg) step(std::integral_constant<int, 1>{}, s + 1);
+  for (int s = s_first; s < nseg;) {
+    s = step(std::integral_constant<int, 0>{}, s);
+    if (s < nseg) s = step(std::integral_constant<int, 1>{}, s);
   }
 
   // ---- normalise and store: acc[dt][ct][i] = dim 16 dt + 4 lg + i -----------
@@ -427,12 +445,13 @@ extern "C" int nkv_prefill_attend(const nkv_store* st, int layer0, int num_layer
                                   int64_t q_layer_stride, int tq, const uint16_t* k_new,
                                   const uint16_t* v_new, int64_t kv_layer_stride, const int32_t* ids,
                                   int64_t ids_layer_stride, int n_hist, const uint8_t* allowed,
-                                  int sink_len, int ring_base, int rec_lo, int rec_len, float scale,
-                                  uint16_t* out, void* stream) {
+                                  int64_t allowed_layer_stride, int sink_len, int ring_base, int rec_lo,
+                                  int rec_len, float scale, uint16_t* out, void* stream) {
   AttendParams p;
   const int rc = fill_attend_params("nkv_prefill_attend", st, layer0, num_layers, q, q_layer_stride, tq,
                                     k_new, v_new, kv_layer_stride, tq, -1, ids, ids_layer_stride, n_hist,
-                                    allowed, sink_len, ring_base, rec_lo, rec_len, scale, 1, nullptr, out, &p);
+                                    allowed, allowed_layer_stride, sink_len, ring_base, rec_lo, rec_len,
+                                    scale, 1, nullptr, out, &p);
   if (rc != NKV_OK) return rc;
   NKV_CHECK_SUPPORTED(p.G >= 1 && kPfCols % p.G == 0,
                       "nkv_prefill_attend: query heads per KV head (%d) must divide %d", p.G, kPfCols);

@@ -485,6 +485,83 @@ __global__ __launch_bounds__(kWave) void topk_wave_kernel(
                      out_scores ? out_scores + row * nblocks : nullptr, pmask, sel, threadIdx.x);
 }
 
+constexpr int kUnionThreads = 256;
+constexpr int kUnionMax = 4096;  // tq * k_eff ids per layer
+
+// Union of one layer's per-query selections (one workgroup per layer): the
+// tq x k_eff ids are sorted in LDS (bitonic), the first id of every run of
+// equal ids is kept at its workgroup prefix-count position, and each query's
+// ids are located in the union by binary search to set its mask row.
+__global__ __launch_bounds__(kUnionThreads) void union_kernel(
+    const int32_t* __restrict__ ids, int tq, int k, int k_eff, int umax, int32_t* __restrict__ out_union,
+    int32_t* __restrict__ out_count, uint8_t* __restrict__ out_allowed) {
+  __shared__ int32_t a[kUnionMax];
+  __shared__ int32_t u[kUnionMax];
+  __shared__ int32_t wsum[kUnionThreads / kWave];
+  __shared__ int32_t s_total;
+  const int layer = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int n = tq * k_eff;
+  int n2 = 1;
+  while (n2 < n) n2 <<= 1;
+  const int32_t* src = ids + static_cast<int64_t>(layer) * tq * k;
+  for (int i = tid; i < n2; i += kUnionThreads) a[i] = i < n ? src[(i / k_eff) * k + i % k_eff] : INT32_MAX;
+  __syncthreads();
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < (n2 >> 1); i += kUnionThreads) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool asc = (lo & size) == 0;
+        const int32_t x = a[lo], y = a[hi];
+        if (asc ? (x > y) : (x < y)) {
+          a[lo] = y;
+          a[hi] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // thread t keeps the run starts of [t * per, (t + 1) * per)
+  const int per = (n + kUnionThreads - 1) / kUnionThreads;
+  const int i0 = min(tid * per, n), i1 = min(i0 + per, n);
+  int cnt = 0;
+  for (int i = i0; i < i1; ++i) cnt += (i == 0 || a[i] != a[i - 1]);
+  int incl = cnt;
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
+  }
+  if (lane == kWave - 1) wsum[wave] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += wsum[w];
+  int pos = base + incl - cnt;
+  for (int i = i0; i < i1; ++i)
+    if (i == 0 || a[i] != a[i - 1]) u[pos++] = a[i];
+  if (tid == kUnionThreads - 1) s_total = base + incl;
+  __syncthreads();
+  const int U = s_total;
+  int32_t* ou = out_union + static_cast<int64_t>(layer) * umax;
+  for (int i = tid; i < umax; i += kUnionThreads) ou[i] = i < U ? u[i] : -1;
+  if (tid == 0) out_count[layer] = U;
+  uint8_t* oa = out_allowed + static_cast<int64_t>(layer) * tq * umax;
+  for (int i = tid; i < tq * umax; i += kUnionThreads) oa[i] = 0;
+  __syncthreads();  // the zeros are written before the ones
+  for (int i = tid; i < n; i += kUnionThreads) {
+    const int t = i / k_eff;
+    const int32_t id = src[t * k + i % k_eff];
+    int lo = 0, hi = U;  // first union entry >= id (the id itself)
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (u[mid] < id) lo = mid + 1;
+      else hi = mid;
+    }
+    oa[static_cast<int64_t>(t) * umax + lo] = 1;
+  }
+}
+
 // NANOKV_TOPK_WAVE=0 keeps every row on the workgroup top-k kernel (A/B and
 // cross-checks of the two selection kernels).
 bool topk_wave_enabled() {
@@ -581,4 +658,19 @@ extern "C" int nkv_select(const nkv_store* st, int layer0, int num_layers, const
   hipLaunchKernelGGL(topk_kernel, rows, dim3(kTopkThreads), tsmem, s, score_keys,
                      nblocks, protected_ids, n_protected, k, order, out_ids, out_vals, k, out_scores);
   return launch_status("nkv_select/topk");
+}
+
+extern "C" int nkv_select_union(const int32_t* ids, int num_layers, int tq, int k, int k_eff, int umax,
+                                int32_t* out_union, int32_t* out_count, uint8_t* out_allowed, void* stream) {
+  NKV_CHECK_ARG(ids != nullptr && out_union != nullptr && out_count != nullptr && out_allowed != nullptr,
+                "nkv_select_union: ids, out_union, out_count and out_allowed must be non-NULL");
+  NKV_CHECK_ARG(num_layers >= 1, "nkv_select_union: num_layers must be >= 1 (got %d)", num_layers);
+  NKV_CHECK_ARG(tq >= 1 && tq <= 16, "nkv_select_union: tq must be in [1, 16] (got %d)", tq);
+  NKV_CHECK_ARG(k_eff >= 1 && k_eff <= k, "nkv_select_union: k_eff must be in [1, k] (got %d, k=%d)", k_eff, k);
+  NKV_CHECK_SUPPORTED(tq * k_eff <= kUnionMax, "nkv_select_union: tq * k_eff = %d exceeds %d", tq * k_eff,
+                      kUnionMax);
+  NKV_CHECK_ARG(umax >= tq * k_eff, "nkv_select_union: umax %d < tq * k_eff = %d", umax, tq * k_eff);
+  hipLaunchKernelGGL(union_kernel, dim3(num_layers), dim3(kUnionThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                     ids, tq, k, k_eff, umax, out_union, out_count, out_allowed);
+  return launch_status("nkv_select_union");
 }

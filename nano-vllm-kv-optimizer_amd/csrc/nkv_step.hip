@@ -117,7 +117,7 @@ extern "C" int nkv_decode_step(const nkv_store* st, int layer0, int num_layers, 
                     out_ids + static_cast<int64_t>(l0) * k, nullptr, sr);
     if (rc != NKV_OK) return rc;
     rc = nkv_attend(st, layer0 + l0, nl, q + l0 * q_ls, q_ls, 1, k_new + l0 * kv_ls, v_new + l0 * kv_ls, kv_ls,
-                    1, write_slot, out_ids + static_cast<int64_t>(l0) * k, k, n_hist, nullptr, sink_len,
+                    1, write_slot, out_ids + static_cast<int64_t>(l0) * k, k, n_hist, nullptr, 0, sink_len,
                     ring_base, rec_lo, rec_len, scale, splits, partial_ws ? partial_ws + r * ws_range : nullptr,
                     out + l0 * q_ls, sr);
     if (rc != NKV_OK) return rc;

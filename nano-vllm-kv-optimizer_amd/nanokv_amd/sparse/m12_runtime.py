@@ -93,7 +93,10 @@ class M12Config:
     per-KV-head fp16 scales) and ``attend_splits`` (workgroups per KV head in
     the attention kernel; None = automatic) and ``mfma_chunk_min_tokens``
     (prefill / verify chunks of at least this many queries use the
-    matrix-core kernel, shorter ones the few-query kernel).  ``use_index_select``,
+    matrix-core kernel, shorter ones the few-query kernel; None = automatic:
+    the matrix-core kernel as soon as the chunk's query rows, tokens x heads
+    per KV head, exceed the few-query kernel's 16-row group, which it would
+    otherwise split, reading every block once per group).  ``use_index_select``,
     ``decode_kv_pipeline`` and ``gather_sort``'s gather-locality purpose
     belong to the host-offload design and do not change the HBM path
     (``gather_sort`` still orders ``last_block_ids`` ascending).
@@ -132,7 +135,7 @@ class M12Config:
     prefill_adapter: object | None = None
     quant_scale_layout: str = "channel_block"
     attend_splits: int | None = None
-    mfma_chunk_min_tokens: int = 32
+    mfma_chunk_min_tokens: int | None = None
 
     def __post_init__(self):
         if self.decode_kv_pipeline and not self.use_index_select:
@@ -156,8 +159,8 @@ class M12Config:
             raise ValueError("quant_scale_layout must be 'channel_block' or 'token'")
         if self.attend_splits is not None and not 1 <= self.attend_splits <= 64:
             raise ValueError("attend_splits must be in [1, 64]")
-        if self.mfma_chunk_min_tokens < 1:
-            raise ValueError("mfma_chunk_min_tokens must be >= 1")
+        if self.mfma_chunk_min_tokens is not None and self.mfma_chunk_min_tokens < 1:
+            raise ValueError("mfma_chunk_min_tokens must be >= 1 or None")
 
     @property
     def kv_format(self) -> str:
@@ -338,7 +341,8 @@ class _SparseCore:
         return max(1, min(-(-nseg // 4), want, 64))
 
     def attend(self, q, k_new, v_new, *, n_chunk, write_slot, ids, ids_stride,
-               n_hist, allowed, sink_len, ring_base, rec_lo, rec_len, lo=0, ws="", out=None):
+               n_hist, allowed, sink_len, ring_base, rec_lo, rec_len, lo=0, ws="", out=None,
+               allowed_stride=0):
         cfg = self.cfg
         nl, tq = q.shape[0], q.shape[1]
         g = cfg.num_heads // cfg.num_kv_heads
@@ -352,7 +356,7 @@ class _SparseCore:
         part = self._buf("partial" + ws, self.store.attend_workspace_floats(nl, tq, splits), torch.float32)
         self.store.attend(self.layer0 + lo, q, k_new, v_new, n_chunk, write_slot, ids,
                           ids_stride, n_hist, allowed, sink_len, ring_base, rec_lo, rec_len,
-                          cfg.scale, splits, part, out)
+                          cfg.scale, splits, part, out, allowed_stride)
         return out
 
     def decode_attend(self, q, k, v, ids, ids_stride, n_hist, *, lo=0, ws="", out=None,
@@ -396,21 +400,26 @@ class _SparseCore:
         self.ring_start = (self.ring_start + 1) % self.cfg.recent_tokens
         self.valid_len += 1
 
-    def chunk_attend(self, q, k, v, ids, ids_stride, n_hist, allowed=None):
-        """[selected | sink | previous recent | chunk (causal)] (m12_runtime.py:592-639, :725-758)."""
+    def chunk_attend(self, q, k, v, ids, ids_stride, n_hist, allowed=None, allowed_stride=0):
+        """[selected | sink | previous recent | chunk (causal)] (m12_runtime.py:592-639, :725-758).
+
+        allowed: uint8 [tq, n_hist] shared by the layers, or per layer with
+        layer stride allowed_stride."""
         cfg = self.cfg
         sink_len = min(cfg.sink_tokens, self.valid_len)
         _, off, ln = prefill_recent_slice(self.valid_len, cfg.sink_tokens, cfg.recent_tokens)
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-        if q.shape[1] >= cfg.mfma_chunk_min_tokens:
+        tq, g = q.shape[1], cfg.num_heads // cfg.num_kv_heads
+        if (tq * g > 16 if cfg.mfma_chunk_min_tokens is None else tq >= cfg.mfma_chunk_min_tokens):
             out = torch.empty_like(q)
             self.store.prefill_attend(self.layer0, q, k, v, ids, ids_stride, n_hist, allowed,
-                                      sink_len, self.ring_start, off, ln, cfg.scale, out)
+                                      sink_len, self.ring_start, off, ln, cfg.scale, out,
+                                      allowed_stride)
         else:
             out = self.attend(q, k, v, n_chunk=q.shape[1], write_slot=-1, ids=ids,
                               ids_stride=ids_stride, n_hist=n_hist, allowed=allowed,
                               sink_len=sink_len, ring_base=self.ring_start, rec_lo=off,
-                              rec_len=ln)
+                              rec_len=ln, allowed_stride=allowed_stride)
         return out, sink_len, ln
 
 
@@ -854,6 +863,8 @@ class M12ModelRuntime:
             raise ValueError("layer_streams must be >= 1")
         self.layer_streams = min(layer_streams, num_layers)
         self._side_streams: list = []   # created on the first decode (default priority)
+        self.last_union_dev: torch.Tensor | None = None
+        self.last_union_count_dev: torch.Tensor | None = None
 
     @property
     def valid_len(self) -> int:
@@ -889,6 +900,50 @@ class M12ModelRuntime:
         self.last_ids_dev = ids
         self.last_n_selected = n
         return out
+
+    def verify(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
+               lossless: bool = False) -> torch.Tensor:
+        """One speculative verification pass for every layer (M12LayerRuntime.verify_tokens,
+        m12_runtime.py:656-758): q [L, Tq, Hq, D], k/v [L, Tq, Hkv, D] -> o [L, Tq, Hq, D].
+
+        shared: one selection from the Tq queries (max-reduced scores).  lossless:
+        a Top-K per query, their union and the per-query mask built on the device
+        (nkv_select_union, no host round trip), so query t attends only its own
+        blocks.  The Tq tokens are attended causally and held pending:
+        commit_verified(n) appends the first n to the recent window,
+        rollback_verified() drops them."""
+        cfg, core = self.cfg, self.core
+        if core.prefill_len <= 0:
+            raise ValueError("verify requires a complete prefill")
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        L, tq = q.shape[0], q.shape[1]
+        req = cfg.top_k_blocks
+        if lossless:
+            if tq > 16:
+                raise ValueError("per-query selection supports at most 16 queries")
+            ids, _, kk = core.select(q, req, per_query=True)
+            umax = tq * kk
+            dev = self.store.device
+            union = core._buf("union", L * umax, torch.int32).view(L, umax)
+            count = core._buf("union_count", L, torch.int32)
+            allowed = core._buf("allowed", L * tq * umax, torch.uint8).view(L, tq, umax)
+            self.store.select_union(ids, kk, umax, union, count, allowed)
+            out, _, _ = core.chunk_attend(q, k, v, union, umax, umax, allowed, allowed_stride=tq * umax)
+            self.last_union_dev, self.last_union_count_dev = union, count
+        else:
+            ids, _, n = core.select(q, req)
+            out, _, _ = core.chunk_attend(q, k, v, ids, ids.shape[-1], n)
+            self.last_union_dev, self.last_union_count_dev = ids[:, 0, :n], None
+        core.pending = (k, v)
+        return out
+
+    def commit_verified(self, n: int) -> None:
+        """Append the first n pending verified tokens of every layer to the recent window."""
+        self.core.commit(n)
+
+    def rollback_verified(self) -> None:
+        """Discard the pending verification pass."""
+        self.core.pending = None
 
     def select(self, q: torch.Tensor, budget: int | None = None):
         """Decode selection for every layer: q [L, 1, Hq, D] -> (ids [L, 1, K], vals, k)."""

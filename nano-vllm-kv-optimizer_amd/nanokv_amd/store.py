@@ -138,7 +138,7 @@ class SparseKVStore:
     def attend(self, layer0: int, q, k_new, v_new, n_chunk: int,
                write_slot: int, ids, ids_layer_stride: int, n_hist: int, allowed,
                sink_len: int, ring_base: int, rec_lo: int, rec_len: int, scale: float,
-               splits: int, partial_ws, out) -> None:
+               splits: int, partial_ws, out, allowed_layer_stride: int = 0) -> None:
         self._bf16(q, "q")
         self._bf16(out, "out")
         nl, tq = q.shape[0], q.shape[1]
@@ -146,20 +146,34 @@ class SparseKVStore:
         _lib.check(self.lib.nkv_attend(
             self._desc_ref, layer0, nl, _ptr(q), q.stride(0), tq, _ptr(k_new), _ptr(v_new),
             kv_stride, n_chunk, write_slot, _ptr(ids), ids_layer_stride, n_hist,
-            _ptr(allowed), sink_len, ring_base, rec_lo, rec_len, float(scale), splits,
-            _ptr(partial_ws), _ptr(out), _stream()), "attend")
+            _ptr(allowed), allowed_layer_stride, sink_len, ring_base, rec_lo, rec_len, float(scale),
+            splits, _ptr(partial_ws), _ptr(out), _stream()), "attend")
 
     def prefill_attend(self, layer0: int, q, k_new, v_new, ids, ids_layer_stride: int,
                        n_hist: int, allowed, sink_len: int, ring_base: int, rec_lo: int,
-                       rec_len: int, scale: float, out) -> None:
+                       rec_len: int, scale: float, out, allowed_layer_stride: int = 0) -> None:
         """Many-query causal attention on the matrix cores (chunk = the queries' own tokens)."""
         self._bf16(q, "q")
         self._bf16(out, "out")
         nl, tq = q.shape[0], q.shape[1]
         _lib.check(self.lib.nkv_prefill_attend(
             self._desc_ref, layer0, nl, _ptr(q), q.stride(0), tq, _ptr(k_new), _ptr(v_new),
-            k_new.stride(0), _ptr(ids), ids_layer_stride, n_hist, _ptr(allowed), sink_len,
-            ring_base, rec_lo, rec_len, float(scale), _ptr(out), _stream()), "prefill_attend")
+            k_new.stride(0), _ptr(ids), ids_layer_stride, n_hist, _ptr(allowed),
+            allowed_layer_stride, sink_len, ring_base, rec_lo, rec_len, float(scale), _ptr(out),
+            _stream()), "prefill_attend")
+
+    def select_union(self, ids, k_eff: int, umax: int, out_union, out_count, out_allowed) -> None:
+        """nkv_select_union: ids [L, tq, k] int32 per-query selections -> union [L, umax]
+        (ascending, -1 padded), counts [L], allowed [L, tq, umax] uint8."""
+        nl, tq, k = ids.shape
+        if not ids.is_contiguous() or ids.dtype != torch.int32:
+            raise ValueError("select_union: ids must be contiguous int32 [L, tq, k]")
+        if (out_union.numel() < nl * umax or out_count.numel() < nl
+                or out_allowed.numel() < nl * tq * umax):
+            raise ValueError("select_union: output buffers too small")
+        _lib.check(self.lib.nkv_select_union(_ptr(ids), nl, tq, k, k_eff, umax, _ptr(out_union),
+                                             _ptr(out_count), _ptr(out_allowed), _stream()),
+                   "select_union")
 
     def attend_workspace_floats(self, nl: int, tq: int, splits: int) -> int:
         return int(self.lib.nkv_attend_workspace_floats(nl, self.num_kv_heads, self.num_heads,

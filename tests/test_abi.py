@@ -48,7 +48,7 @@ def test_bad_arguments_are_rejected_before_any_device_work():
     st = _lib.NkvStore()
     st.head_dim, st.block_size = 64, 64
     rc = lib.nkv_attend(ctypes.byref(st), 0, 1, None, 0, 1, None, None, 0, 0, -1, None, 0, 0,
-                        None, 0, 0, 0, 0, 1.0, 1, None, None, None)
+                        None, 0, 0, 0, 0, 0, 1.0, 1, None, None, None)
     assert rc == _lib.NKV_ERR_UNSUPPORTED
     with pytest.raises(ValueError, match="head_dim"):
         _lib.check(rc, "attend")
@@ -67,20 +67,20 @@ def test_prefill_entry_rejects_bad_arguments_without_device_work():
     st.sink_k = st.sink_v = st.recent_k = st.recent_v = dummy
     # q NULL
     rc = lib.nkv_prefill_attend(ctypes.byref(st), 0, 1, None, 0, 64, dummy, dummy, 0, None, 0, 0,
-                                None, 0, 0, 0, 0, 1.0, dummy, None)
+                                None, 0, 0, 0, 0, 0, 1.0, dummy, None)
     assert rc == _lib.NKV_ERR_ARG and b"nkv_prefill_attend" in lib.nkv_last_error()
     # recent range beyond the ring
     rc = lib.nkv_prefill_attend(ctypes.byref(st), 0, 1, dummy, 0, 64, dummy, dummy, 0, None, 0, 0,
-                                None, 0, 0, 500, 100, 1.0, dummy, None)
+                                None, 0, 0, 0, 500, 100, 1.0, dummy, None)
     assert rc == _lib.NKV_ERR_ARG and b"recent range" in lib.nkv_last_error()
     # chunk K/V missing
     rc = lib.nkv_prefill_attend(ctypes.byref(st), 0, 1, dummy, 0, 64, None, None, 0, None, 0, 0,
-                                None, 0, 0, 0, 0, 1.0, dummy, None)
+                                None, 0, 0, 0, 0, 0, 1.0, dummy, None)
     assert rc == _lib.NKV_ERR_ARG and b"k_new/v_new" in lib.nkv_last_error()
     # GQA group size that does not divide the 128-column query tile
     st.num_heads, st.num_kv_heads = 24, 8
     rc = lib.nkv_prefill_attend(ctypes.byref(st), 0, 1, dummy, 0, 64, dummy, dummy, 0, None, 0, 0,
-                                None, 0, 0, 0, 0, 1.0, dummy, None)
+                                None, 0, 0, 0, 0, 0, 1.0, dummy, None)
     assert rc == _lib.NKV_ERR_UNSUPPORTED
 
 
@@ -111,3 +111,31 @@ def test_decode_step_rejects_bad_arguments_without_device_work():
     per = lib.nkv_attend_workspace_floats(2, 8, 32, 1, 3)
     assert lib.nkv_decode_step_workspace_floats(4, 8, 32, 3, 2) == 2 * per
     assert lib.nkv_decode_step_workspace_floats(4, 8, 32, 3, 0) == 0
+
+
+def test_select_union_rejects_bad_arguments_without_device_work():
+    lib = _lib.load()
+    d = ctypes.c_void_p(16)   # never dereferenced: every call below fails validation
+    assert lib.nkv_select_union(None, 1, 6, 32, 32, 192, d, d, d, None) == _lib.NKV_ERR_ARG
+    assert lib.nkv_select_union(d, 1, 0, 32, 32, 192, d, d, d, None) == _lib.NKV_ERR_ARG
+    assert lib.nkv_select_union(d, 1, 17, 32, 32, 544, d, d, d, None) == _lib.NKV_ERR_ARG
+    assert lib.nkv_select_union(d, 1, 6, 32, 33, 198, d, d, d, None) == _lib.NKV_ERR_ARG
+    assert b"k_eff" in lib.nkv_last_error()
+    assert lib.nkv_select_union(d, 1, 6, 32, 32, 191, d, d, d, None) == _lib.NKV_ERR_ARG
+    assert b"umax" in lib.nkv_last_error()
+    assert lib.nkv_select_union(d, 1, 16, 512, 512, 8192, d, d, d, None) == _lib.NKV_ERR_UNSUPPORTED
+
+
+def test_attend_rejects_a_short_allowed_layer_stride():
+    lib = _lib.load()
+    st = _lib.NkvStore()
+    st.num_layers, st.num_heads, st.num_kv_heads = 2, 32, 8
+    st.head_dim, st.block_size, st.r, st.cap_blocks = 128, 64, 4, 16
+    st.sink_tokens, st.recent_tokens, st.kv_format = 64, 512, 0
+    d = ctypes.c_void_p(16)   # never dereferenced: the call fails validation
+    st.hist_k = st.hist_v = st.reps = d
+    st.sink_k = st.sink_v = st.recent_k = st.recent_v = d
+    # tq = 6 queries x n_hist = 10 blocks need a per-layer stride >= 60
+    rc = lib.nkv_attend(ctypes.byref(st), 0, 2, d, 6 * 32 * 128, 6, d, d, 6 * 8 * 128, 6, -1, d, 10, 10,
+                        d, 59, 64, 0, 0, 511, 1.0, 1, None, d, None)
+    assert rc == _lib.NKV_ERR_ARG and b"allowed_layer_stride" in lib.nkv_last_error()

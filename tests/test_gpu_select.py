@@ -175,3 +175,38 @@ def test_select_rejects_empty_history():
     rt = _runtime(0, max_blocks=8)
     with pytest.raises(ValueError, match="history block"):
         rt._gpu_select(_rand_q(1, 0)[0].cuda())
+
+
+@pytest.mark.parametrize("L,tq,k,k_eff,hi,seed", [
+    (3, 6, 32, 32, 120, 0),     # verify shape, heavy overlap between queries
+    (2, 6, 32, 29, 4000, 1),    # k_eff < k, few duplicates
+    (1, 1, 8, 8, 100, 2),       # one query: the union is its sorted ids
+    (2, 16, 256, 256, 9000, 3), # the largest supported union (4096 ids)
+])
+def test_select_union_matches_unique_and_searchsorted(L, tq, k, k_eff, hi, seed):
+    """nkv_select_union against the reference's host ops (m12_runtime.py:1057-1087):
+    torch.unique of the per-query ids, searchsorted, scatter into the mask."""
+    from nanokv_amd.store import SparseKVStore
+    rng = np.random.default_rng(seed)
+    ids = np.full((L, tq, k), -7, dtype=np.int32)          # entries past k_eff must be ignored
+    for l in range(L):
+        for t in range(tq):
+            ids[l, t, :k_eff] = rng.choice(hi, size=k_eff, replace=False)
+    umax = tq * k_eff + 5
+    st = SparseKVStore(1, num_heads=32, num_kv_heads=8, head_dim=128, block_size=64, r=4,
+                       cap_blocks=8, sink_tokens=64, recent_tokens=512, kv_format="bf16")
+    d_ids = torch.from_numpy(ids).cuda()
+    union = torch.full((L, umax), 123, dtype=torch.int32, device="cuda")
+    count = torch.zeros(L, dtype=torch.int32, device="cuda")
+    allowed = torch.full((L, tq, umax), 9, dtype=torch.uint8, device="cuda")
+    st.select_union(d_ids, k_eff, umax, union, count, allowed)
+    union, count, allowed = union.cpu().numpy(), count.cpu().numpy(), allowed.cpu().numpy()
+    for l in range(L):
+        u = np.unique(ids[l, :, :k_eff])
+        assert count[l] == u.size
+        assert np.array_equal(union[l, :u.size], u)
+        assert (union[l, u.size:] == -1).all()
+        want = np.zeros((tq, umax), dtype=np.uint8)
+        for t in range(tq):
+            want[t, np.searchsorted(u, ids[l, t, :k_eff])] = 1
+        assert np.array_equal(allowed[l], want)

@@ -115,16 +115,23 @@ def test_small_chunks_exercise_recent_carry():
         assert_close_bf16(to_np(out), o_ref)
 
 
+@pytest.mark.parametrize("kernel", ["mfma", "few_query"])
 @pytest.mark.parametrize("lossless", [False, True])
 @pytest.mark.parametrize("quant", [False, True])
-def test_verify_commit_rollback_then_decode(lossless, quant):
-    rt, ob = _pair(16384 + 64, quant_history=quant)
+def test_verify_commit_rollback_then_decode(lossless, quant, kernel):
+    """6-token verify through the matrix-core kernel (the automatic choice: 24
+    query rows exceed one 16-row group) and through the few-query kernel."""
+    rt, ob = _pair(16384 + 64, quant_history=quant,
+                   mfma_chunk_min_tokens=None if kernel == "mfma" else 64)
     k0, v0 = _rand((16384, 8, 128), 140, 0.09), _rand((16384, 8, 128), 141, 0.09)
     rt.prefill_first(None, k0.cuda(), v0.cuda())
     ob.store_kv(to_np(k0), to_np(v0), with_reps=False)
     _sync_reps(rt, ob)
     rt.verify_lossless = lossless
-    tol = dict(rel=2.0 ** -6, abs_tol=2e-4) if quant else {}
+    # int8: rel 2^-6 (q x scale rounded to bf16); the matrix-core kernel feeds
+    # P to bf16 MFMA (PREFILL_TOL); decode after verify is the few-query kernel
+    tol = dict(rel=2.0 ** -6, abs_tol=2e-4) if quant else (PREFILL_TOL if kernel == "mfma" else {})
+    dec_tol = dict(rel=2.0 ** -6, abs_tol=2e-4) if quant else {}
     for rnd, accept in enumerate((3, 0, 6)):
         tq = 6
         q = _rand((tq, 32, 128), 150 + rnd)
@@ -144,7 +151,7 @@ def test_verify_commit_rollback_then_decode(lossless, quant):
     out = rt.decode(q.cuda(), k.cuda(), v.cuda())
     ids_or, _, o_ref = ob.decode(to_np(q), to_np(k), to_np(v))
     assert rt.last_block_ids.tolist() == ids_or.tolist()
-    assert_close_bf16(to_np(out), o_ref, **tol)
+    assert_close_bf16(to_np(out), o_ref, **dec_tol)
 
 
 def test_reset_reuses_buffers_without_inheriting_history():

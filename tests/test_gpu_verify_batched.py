@@ -1,0 +1,76 @@
+"""Speculative verify for all layers at once (M12ModelRuntime.verify) against the
+per-layer runtime (M12LayerRuntime.verify_tokens, itself checked against the
+oracle in test_gpu_store_verify.py): the same union of per-query selections
+(built on the device here, on the host there), outputs within one bf16 ulp
+(the attention splits its segments differently), and the same ring after
+commit / rollback, checked by a following decode step.
+"""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+def _one_ulp(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return bool(((a - b).abs() <= 2.0 ** -7 * b.abs() + 1e-6).all())
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "few_query"])
+@pytest.mark.parametrize("lossless", [True, False])
+@pytest.mark.parametrize("quant", [False, True])
+def test_batched_verify_matches_per_layer(lossless, quant, kernel):
+    """Through the matrix-core kernel (the automatic choice for 6 tokens: the
+    union's -1 padding is passed over) and the few-query kernel (per-layer
+    masks through allowed_layer_stride, padding skipped per wavefront)."""
+    from nanokv_amd.sparse import M12Config, M12LayerRuntime, M12ModelRuntime
+    L, T, tq = 3, 16384, 6
+    cfg = M12Config(max_model_len=T + 64, quant_history=quant,
+                    mfma_chunk_min_tokens=None if kernel == "mfma" else 64)
+    model = M12ModelRuntime(L, cfg)
+    layers = [M12LayerRuntime(i, cfg) for i in range(L)]
+    k0 = torch.stack([_rand((T, 8, 128), 500 + i, 0.09) for i in range(L)]).cuda()
+    v0 = torch.stack([_rand((T, 8, 128), 600 + i, 0.09) for i in range(L)]).cuda()
+    model.prefill(k0, v0)
+    for i, rt in enumerate(layers):
+        rt.prefill_first(None, k0[i], v0[i])
+        rt.verify_lossless = lossless
+    for rnd, accept in enumerate((3, 0, 6)):
+        q = torch.stack([_rand((tq, 32, 128), 700 + 10 * rnd + i) for i in range(L)]).cuda()
+        k = torch.stack([_rand((tq, 8, 128), 800 + 10 * rnd + i, 0.09) for i in range(L)]).cuda()
+        v = torch.stack([_rand((tq, 8, 128), 900 + 10 * rnd + i, 0.09) for i in range(L)]).cuda()
+        out = model.verify(q, k, v, lossless=lossless)
+        for i, rt in enumerate(layers):
+            o_i = rt.verify_tokens(q[i], k[i], v[i])
+            ids_i = rt.last_verify_block_ids.tolist()
+            if lossless:
+                n = int(model.last_union_count_dev[i])
+                assert model.last_union_dev[i, :n].tolist() == ids_i
+                assert (model.last_union_dev[i, n:] == -1).all()
+            else:
+                assert sorted(model.last_union_dev[i].tolist()) == sorted(ids_i)
+            assert _one_ulp(out[i], o_i)
+            if rnd == 1:
+                rt.rollback_verified()
+            else:
+                rt.commit_verified(accept)
+        if rnd == 1:
+            model.rollback_verified()
+        else:
+            model.commit_verified(accept)
+        assert model.valid_len == layers[0].valid_len
+    q = torch.stack([_rand((1, 32, 128), 1000 + i) for i in range(L)]).cuda()
+    k = torch.stack([_rand((1, 8, 128), 1100 + i, 0.09) for i in range(L)]).cuda()
+    v = torch.stack([_rand((1, 8, 128), 1200 + i, 0.09) for i in range(L)]).cuda()
+    out = model.decode(q, k, v)
+    for i, rt in enumerate(layers):
+        o_i = rt.decode(q[i], k[i], v[i])
+        n = model.last_n_selected
+        assert model.last_ids_dev[i, 0, :n].cpu().tolist() == rt.last_block_ids.tolist()
+        assert _one_ulp(out[i], o_i)

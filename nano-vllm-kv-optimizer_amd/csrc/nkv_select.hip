@@ -124,6 +124,17 @@ __device__ __forceinline__ void select_row_wave(
     float* __restrict__ scores, uint32_t* pmask, unsigned long long* sel, int lane) {
   const int nwords = (nblocks + 31) >> 5;
 
+  // The key reads go out first (they do not depend on the protected set), so
+  // their latency overlaps the protected-id reads.  Keys past nblocks are 0,
+  // below every key score_key() produces.  Every read is issued (past nblocks
+  // it re-reads the last key), so one wait covers them all.
+  uint32_t key[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int i = kWave * j + lane;
+    key[j] = sk[i < nblocks ? i : nblocks - 1];
+  }
+
   for (int w = lane; w < nwords; w += kWave) pmask[w] = 0u;
   wave_lds_sync();
   for (int i = lane; i < nprot; i += kWave) {
@@ -137,15 +148,6 @@ __device__ __forceinline__ void select_row_wave(
   const int avail = nblocks - static_cast<int>(np);
   const int k = min(k_req, max(1, avail));
 
-  // keys past nblocks are 0, below every key score_key() produces.  Every
-  // read is issued (past nblocks it re-reads the last key), so one wait
-  // covers them all.
-  uint32_t key[J];
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int i = kWave * j + lane;
-    key[j] = sk[i < nblocks ? i : nblocks - 1];
-  }
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int i = kWave * j + lane;

@@ -233,10 +233,13 @@ int nkv_select_union(const int32_t* ids, int num_layers, int tq, int k, int k_ef
  * reference's pack does (m12_runtime.py:1262-1267, fused_dequant.py:34-44).
  *
  * Same key set and argument meaning as nkv_attend with n_chunk = tq (query t
- * is chunk token t and sees chunk tokens c <= t), write_slot = -1 and
- * splits = 1.  Queries are tiled 128/G tokens x G heads per workgroup
- * (G = Hq / Hkv must divide 128).  No workspace.
- * Constraints: 1 <= tq <= 65536, n_hist <= 4096.
+ * is chunk token t and sees chunk tokens c <= t) and write_slot = -1.
+ * Queries are tiled 128/G tokens x G heads per workgroup (G = Hq / Hkv must
+ * divide 128).  splits > 1 cuts each tile's segment list into that many
+ * workgroups (few tiles: short chunks, verify) whose partial softmax states a
+ * second kernel on the same stream merges; partial_ws then needs
+ * nkv_prefill_workspace_floats(...) floats.
+ * Constraints: 1 <= tq <= 65536, n_hist <= 4096, 1 <= splits <= 64.
  */
 int nkv_prefill_attend(const nkv_store* st, int layer0, int num_layers,
                        const uint16_t* q, int64_t q_layer_stride, int tq,
@@ -244,7 +247,11 @@ int nkv_prefill_attend(const nkv_store* st, int layer0, int num_layers,
                        const int32_t* ids, int64_t ids_layer_stride, int n_hist,
                        const uint8_t* allowed, int64_t allowed_layer_stride, int sink_len,
                        int ring_base, int rec_lo, int rec_len,
-                       float scale, uint16_t* out, void* stream);
+                       float scale, int splits, float* partial_ws, uint16_t* out, void* stream);
+
+/* Floats of partial_ws needed by nkv_prefill_attend (0 when splits == 1). */
+int64_t nkv_prefill_workspace_floats(int num_layers, int num_kv_heads, int num_heads, int tq,
+                                     int splits);
 
 /*
  * Append one prefill chunk to the history of `num_layers` layers.

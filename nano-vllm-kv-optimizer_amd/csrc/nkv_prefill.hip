@@ -48,6 +48,9 @@ using namespace stage;
 constexpr int kPfWaves = 4;
 constexpr int kPfThreads = kPfWaves * kWave;     // 256
 constexpr int kPfCols = 128;                     // (token, head) columns per workgroup
+// split partial record of one column: m (reference max, log2 units), l, two
+// pad words, acc[128] (16-byte aligned for vector stores)
+constexpr int kPfPart = 4 + kHeadDim;
 
 // 8 int8 codes (lo, hi) -> 8 x bf16(code * scale[e]), rounded to nearest even.
 __device__ __forceinline__ u32x4 dequant8(uint32_t lo, uint32_t hi, const float (&sc)[8]) {
@@ -269,7 +272,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
   float l_run[2] = {0.0f, 0.0f};
 
   const int n_chunk_seg = p.n_chunk > 0 ? t_last / kBlock + 1 : 0;
-  const int nseg = p.n_hist + p.n_sink_seg + p.n_rec_seg + n_chunk_seg;
+  const int nseg_all = p.n_hist + p.n_sink_seg + p.n_rec_seg + n_chunk_seg;
+  // split-K: this workgroup attends segments [seg_lo, nseg) of the list
+  const int split = blockIdx.z;
+  const int seg_lo = static_cast<int>(static_cast<int64_t>(split) * nseg_all / p.splits);
+  const int nseg = static_cast<int>(static_cast<int64_t>(split + 1) * nseg_all / p.splits);
 
   // staging of segment s into buffer `buf`: asynchronous copies issued by
   // begin_stage, completed (and int8 blocks dequantised) by finish_stage
@@ -307,10 +314,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
   };
 
   int blk_first;
-  const int s_first = next_seg(0, &blk_first);
-  Seg nxt = make_seg_blk<FMT>(p, layer, h, s_first, blk_first);
-  begin_stage(nxt, lds0);
-  finish_stage(nxt, lds0);
+  const int s_first = next_seg(seg_lo, &blk_first);
+  Seg nxt = make_seg_blk<FMT>(p, layer, h, s_first < nseg ? s_first : 0, blk_first);
+  if (s_first < nseg) {   // uniform: a split may have nothing left to attend
+    begin_stage(nxt, lds0);
+    finish_stage(nxt, lds0);
+  }
 
   // One segment: compute on buffer P while the next segment is staged into
   // buffer 1 - P.
@@ -424,7 +433,21 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
     const int t = tcol[ct];
-    if (t <= t_last) {
+    if (p.splits > 1) {
+      // this split's (m, l, acc) of the column, merged by prefill_merge_kernel
+      if (t <= t_last) {
+        const int col = wave * 32 + ct * 16 + ln;
+        float* rec = p.partial +
+                     ((((static_cast<int64_t>(layer) * p.hkv + h) * nqt + qt) * p.splits + split) * kPfCols + col) *
+                         kPfPart;
+        if (lg == 0) {
+          rec[0] = m_run[ct];
+          rec[1] = l;
+        }
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(rec + 4 + 16 * dt + 4 * lg) = acc[dt][ct];
+      }
+    } else if (t <= t_last) {
       const float inv = 1.0f / l;
       uint16_t* orow = p.out + p.q_ls * layer + (static_cast<int64_t>(t) * hq + hcol[ct]) * kHeadDim + 4 * lg;
 #pragma unroll
@@ -436,28 +459,67 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
   }
 }
 
+// Merge the split partials of one (layer, KV head, query tile, column): one
+// thread per dim, the usual rescale of each split's (m, l, acc) to the
+// largest reference max.
+__global__ __launch_bounds__(kHeadDim) void prefill_merge_kernel(const AttendParams p, int nqt) {
+  const int h = blockIdx.x % p.hkv;
+  const int qt = blockIdx.x / p.hkv;
+  const int layer = blockIdx.y;
+  const int col = blockIdx.z;
+  const int t = qt * (kPfCols / p.G) + col / p.G;
+  if (t >= p.tq) return;
+  const int d = threadIdx.x;
+  const int64_t sstride = static_cast<int64_t>(kPfCols) * kPfPart;
+  const float* base =
+      p.partial + (((static_cast<int64_t>(layer) * p.hkv + h) * nqt + qt) * p.splits * kPfCols + col) * kPfPart;
+  float mt = -INFINITY;
+  for (int s = 0; s < p.splits; ++s) mt = fmaxf(mt, base[s * sstride]);
+  float L = 0.0f, A = 0.0f;
+  for (int s = 0; s < p.splits; ++s) {
+    const float* r = base + s * sstride;
+    const float sw = (r[0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(r[0] - mt);
+    L += r[1] * sw;
+    A += r[4 + d] * sw;
+  }
+  const int hh = h * p.G + col % p.G;
+  p.out[p.q_ls * layer + (static_cast<int64_t>(t) * p.hkv * p.G + hh) * kHeadDim + d] = f32_to_bf16(A / L);
+}
+
 }  // namespace
 }  // namespace nkv
 
 using namespace nkv;
+
+extern "C" int64_t nkv_prefill_workspace_floats(int num_layers, int num_kv_heads, int num_heads, int tq,
+                                                int splits) {
+  if (num_layers < 1 || num_kv_heads < 1 || num_heads < num_kv_heads || num_heads % num_kv_heads != 0 ||
+      tq < 1 || splits < 1)
+    return 0;
+  const int G = num_heads / num_kv_heads;
+  if (kPfCols % G != 0) return 0;
+  const int64_t nqt = (tq + kPfCols / G - 1) / (kPfCols / G);
+  return splits == 1 ? 0 : static_cast<int64_t>(num_layers) * num_kv_heads * nqt * splits * kPfCols * kPfPart;
+}
 
 extern "C" int nkv_prefill_attend(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
                                   int64_t q_layer_stride, int tq, const uint16_t* k_new,
                                   const uint16_t* v_new, int64_t kv_layer_stride, const int32_t* ids,
                                   int64_t ids_layer_stride, int n_hist, const uint8_t* allowed,
                                   int64_t allowed_layer_stride, int sink_len, int ring_base, int rec_lo,
-                                  int rec_len, float scale, uint16_t* out, void* stream) {
+                                  int rec_len, float scale, int splits, float* partial_ws, uint16_t* out,
+                                  void* stream) {
   AttendParams p;
   const int rc = fill_attend_params("nkv_prefill_attend", st, layer0, num_layers, q, q_layer_stride, tq,
                                     k_new, v_new, kv_layer_stride, tq, -1, ids, ids_layer_stride, n_hist,
                                     allowed, allowed_layer_stride, sink_len, ring_base, rec_lo, rec_len,
-                                    scale, 1, nullptr, out, &p);
+                                    scale, splits, partial_ws, out, &p);
   if (rc != NKV_OK) return rc;
   NKV_CHECK_SUPPORTED(p.G >= 1 && kPfCols % p.G == 0,
                       "nkv_prefill_attend: query heads per KV head (%d) must divide %d", p.G, kPfCols);
   const int tpw = kPfCols / p.G;
   const int nqt = (tq + tpw - 1) / tpw;
-  const dim3 grid(nqt * st->num_kv_heads, num_layers);
+  const dim3 grid(nqt * st->num_kv_heads, num_layers, splits);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (st->kv_format) {
     case NKV_KV_BF16: hipLaunchKernelGGL(prefill_kernel<NKV_KV_BF16>, grid, dim3(kPfThreads), 0, s, p, nqt); break;
@@ -469,5 +531,8 @@ extern "C" int nkv_prefill_attend(const nkv_store* st, int layer0, int num_layer
       break;
     default: NKV_CHECK_SUPPORTED(false, "nkv_prefill_attend: unknown kv_format %d", st->kv_format);
   }
+  if (splits > 1)
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3(nqt * st->num_kv_heads, num_layers, min(kPfCols, tq * p.G)),
+                       dim3(kHeadDim), 0, s, p, nqt);
   return launch_status("nkv_prefill_attend");
 }

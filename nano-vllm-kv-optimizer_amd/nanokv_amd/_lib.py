@@ -75,7 +75,8 @@ SIGNATURES = {
                              _I, _P, _P, _P, _P, _I, ctypes.POINTER(ctypes.c_void_p)]),
     "nkv_decode_step_workspace_floats": (_I64, [_I, _I, _I, _I, _I]),
     "nkv_prefill_attend": (_I, [_SP, _I, _I, _P, _I64, _I, _P, _P, _I64, _P, _I64, _I, _P, _I64,
-                                _I, _I, _I, _I, _F, _P, _P]),
+                                _I, _I, _I, _I, _F, _I, _P, _P, _P]),
+    "nkv_prefill_workspace_floats": (_I64, [_I, _I, _I, _I, _I]),
     "nkv_select_union": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
     "nkv_store_chunk": (_I, [_SP, _I, _I, _P, _P, _I64, _I, _I, _I, _I, _P]),
     "nkv_build_reps": (_I, [_SP, _I, _I, _P, _I64, _I, _I, _P]),

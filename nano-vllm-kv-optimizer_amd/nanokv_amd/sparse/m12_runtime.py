@@ -340,6 +340,15 @@ class _SparseCore:
         want = max(1, round(900 / (self.store.num_kv_heads * self.nl * nqg)))
         return max(1, min(-(-nseg // 4), want, 64))
 
+    def _prefill_splits(self, tq: int, nseg: int) -> int:
+        """Split-K for the matrix-core kernel: about 1024 workgroups per launch
+        when the query tiles alone give far fewer (short chunks, verify), each
+        split keeping at least 4 segments."""
+        g = self.cfg.num_heads // self.cfg.num_kv_heads
+        tiles = -(-tq // (128 // g)) * self.store.num_kv_heads * self.nl
+        want = max(1, round(1024 / tiles))
+        return max(1, min(want, nseg // 4, 64))
+
     def attend(self, q, k_new, v_new, *, n_chunk, write_slot, ids, ids_stride,
                n_hist, allowed, sink_len, ring_base, rec_lo, rec_len, lo=0, ws="", out=None,
                allowed_stride=0):
@@ -412,9 +421,16 @@ class _SparseCore:
         tq, g = q.shape[1], cfg.num_heads // cfg.num_kv_heads
         if (tq * g > 16 if cfg.mfma_chunk_min_tokens is None else tq >= cfg.mfma_chunk_min_tokens):
             out = torch.empty_like(q)
+            B = cfg.block_size
+            nseg = n_hist + -(-sink_len // B) + (-(-cfg.recent_tokens // B) if ln else 0) + -(-tq // B)
+            splits = self._prefill_splits(tq, nseg)
+            part = None
+            if splits > 1:
+                part = self._buf("pf_partial", self.store.prefill_workspace_floats(self.nl, tq, splits),
+                                 torch.float32)
             self.store.prefill_attend(self.layer0, q, k, v, ids, ids_stride, n_hist, allowed,
                                       sink_len, self.ring_start, off, ln, cfg.scale, out,
-                                      allowed_stride)
+                                      allowed_stride, splits, part)
         else:
             out = self.attend(q, k, v, n_chunk=q.shape[1], write_slot=-1, ids=ids,
                               ids_stride=ids_stride, n_hist=n_hist, allowed=allowed,

@@ -151,7 +151,8 @@ class SparseKVStore:
 
     def prefill_attend(self, layer0: int, q, k_new, v_new, ids, ids_layer_stride: int,
                        n_hist: int, allowed, sink_len: int, ring_base: int, rec_lo: int,
-                       rec_len: int, scale: float, out, allowed_layer_stride: int = 0) -> None:
+                       rec_len: int, scale: float, out, allowed_layer_stride: int = 0,
+                       splits: int = 1, partial_ws=None) -> None:
         """Many-query causal attention on the matrix cores (chunk = the queries' own tokens)."""
         self._bf16(q, "q")
         self._bf16(out, "out")
@@ -159,8 +160,12 @@ class SparseKVStore:
         _lib.check(self.lib.nkv_prefill_attend(
             self._desc_ref, layer0, nl, _ptr(q), q.stride(0), tq, _ptr(k_new), _ptr(v_new),
             k_new.stride(0), _ptr(ids), ids_layer_stride, n_hist, _ptr(allowed),
-            allowed_layer_stride, sink_len, ring_base, rec_lo, rec_len, float(scale), _ptr(out),
-            _stream()), "prefill_attend")
+            allowed_layer_stride, sink_len, ring_base, rec_lo, rec_len, float(scale), splits,
+            _ptr(partial_ws), _ptr(out), _stream()), "prefill_attend")
+
+    def prefill_workspace_floats(self, nl: int, tq: int, splits: int) -> int:
+        return int(self.lib.nkv_prefill_workspace_floats(nl, self.num_kv_heads, self.num_heads,
+                                                         tq, splits))
 
     def select_union(self, ids, k_eff: int, umax: int, out_union, out_count, out_allowed) -> None:
         """nkv_select_union: ids [L, tq, k] int32 per-query selections -> union [L, umax]

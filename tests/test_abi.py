@@ -67,20 +67,20 @@ def test_prefill_entry_rejects_bad_arguments_without_device_work():
     st.sink_k = st.sink_v = st.recent_k = st.recent_v = dummy
     # q NULL
     rc = lib.nkv_prefill_attend(ctypes.byref(st), 0, 1, None, 0, 64, dummy, dummy, 0, None, 0, 0,
-                                None, 0, 0, 0, 0, 0, 1.0, dummy, None)
+                                None, 0, 0, 0, 0, 0, 1.0, 1, None, dummy, None)
     assert rc == _lib.NKV_ERR_ARG and b"nkv_prefill_attend" in lib.nkv_last_error()
     # recent range beyond the ring
     rc = lib.nkv_prefill_attend(ctypes.byref(st), 0, 1, dummy, 0, 64, dummy, dummy, 0, None, 0, 0,
-                                None, 0, 0, 0, 500, 100, 1.0, dummy, None)
+                                None, 0, 0, 0, 500, 100, 1.0, 1, None, dummy, None)
     assert rc == _lib.NKV_ERR_ARG and b"recent range" in lib.nkv_last_error()
     # chunk K/V missing
     rc = lib.nkv_prefill_attend(ctypes.byref(st), 0, 1, dummy, 0, 64, None, None, 0, None, 0, 0,
-                                None, 0, 0, 0, 0, 0, 1.0, dummy, None)
+                                None, 0, 0, 0, 0, 0, 1.0, 1, None, dummy, None)
     assert rc == _lib.NKV_ERR_ARG and b"k_new/v_new" in lib.nkv_last_error()
     # GQA group size that does not divide the 128-column query tile
     st.num_heads, st.num_kv_heads = 24, 8
     rc = lib.nkv_prefill_attend(ctypes.byref(st), 0, 1, dummy, 0, 64, dummy, dummy, 0, None, 0, 0,
-                                None, 0, 0, 0, 0, 0, 1.0, dummy, None)
+                                None, 0, 0, 0, 0, 0, 1.0, 1, None, dummy, None)
     assert rc == _lib.NKV_ERR_UNSUPPORTED
 
 

@@ -1,13 +1,20 @@
 """Speculative verify for all layers at once (M12ModelRuntime.verify) against the
 per-layer runtime (M12LayerRuntime.verify_tokens, itself checked against the
 oracle in test_gpu_store_verify.py): the same union of per-query selections
-(built on the device here, on the host there), outputs within one bf16 ulp
-(the attention splits its segments differently), and the same ring after
+(built on the device here, on the host there), and the same ring after
 commit / rollback, checked by a following decode step.
+
+The outputs are two approximations of the same attention: the few-query
+kernel's fp32 sums are split differently (one bf16 ulp apart); the
+matrix-core kernel also rounds P to bf16 against each split's running max
+and the two runtimes choose different split counts, so each is within
+PREFILL_TOL of the exact result and they are within twice that of each other.
 """
 
 import pytest
 import torch
+
+from tests._util import PREFILL_TOL
 
 pytestmark = pytest.mark.gpu
 
@@ -17,9 +24,9 @@ def _rand(shape, seed, scale=1.0):
     return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
 
 
-def _one_ulp(a, b):
+def _close(a, b, rel, abs_tol):
     a, b = a.float().cpu(), b.float().cpu()
-    return bool(((a - b).abs() <= 2.0 ** -7 * b.abs() + 1e-6).all())
+    return bool(((a - b).abs() <= rel * b.abs() + abs_tol).all() and (a - b).abs().max() <= 2e-3)
 
 
 @pytest.mark.parametrize("kernel", ["mfma", "few_query"])
@@ -33,6 +40,8 @@ def test_batched_verify_matches_per_layer(lossless, quant, kernel):
     L, T, tq = 3, 16384, 6
     cfg = M12Config(max_model_len=T + 64, quant_history=quant,
                     mfma_chunk_min_tokens=None if kernel == "mfma" else 64)
+    # verify outputs (see the module docstring); decode is the few-query kernel
+    v_tol = (2 * PREFILL_TOL["rel"], 2 * PREFILL_TOL["abs_tol"]) if kernel == "mfma" else (2.0 ** -7, 1e-6)
     model = M12ModelRuntime(L, cfg)
     layers = [M12LayerRuntime(i, cfg) for i in range(L)]
     k0 = torch.stack([_rand((T, 8, 128), 500 + i, 0.09) for i in range(L)]).cuda()
@@ -55,7 +64,7 @@ def test_batched_verify_matches_per_layer(lossless, quant, kernel):
                 assert (model.last_union_dev[i, n:] == -1).all()
             else:
                 assert sorted(model.last_union_dev[i].tolist()) == sorted(ids_i)
-            assert _one_ulp(out[i], o_i)
+            assert _close(out[i], o_i, *v_tol)
             if rnd == 1:
                 rt.rollback_verified()
             else:
@@ -73,4 +82,4 @@ def test_batched_verify_matches_per_layer(lossless, quant, kernel):
         o_i = rt.decode(q[i], k[i], v[i])
         n = model.last_n_selected
         assert model.last_ids_dev[i, 0, :n].cpu().tolist() == rt.last_block_ids.tolist()
-        assert _one_ulp(out[i], o_i)
+        assert _close(out[i], o_i, 2.0 ** -7, 1e-6)

@@ -101,22 +101,16 @@ __device__ __forceinline__ unsigned long long sel_entry(uint32_t key, int id) {
          static_cast<unsigned long long>(0xffffffffu - static_cast<uint32_t>(id));
 }
 
-__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
-  const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), m);
-  const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), m);
-  return (static_cast<unsigned long long>(hi) << 32) | lo;
-}
-
 // Same selection as topk_kernel (identical ids, values and order) for one row
 // of at most 64 J blocks, computed by ONE wavefront with no workgroup barrier
 // (pmask: 2 J words of LDS, sel: LDS for max(k, 64) rounded up to a power of
 // two entries).
 // Lane l holds the keys of blocks 64 j + l (j < J) in registers.  The k-th
-// largest key T is found by a 32-step bitwise search: T is the largest value
-// with count(key >= T) >= k, built from the high bit down, each count being
-// J ballots.  Collection is the same ascending-id ballot pass as topk_kernel;
-// up to 64 selected entries are then sorted by a bitonic network across the
-// lanes (shuffles), larger k by the same network over LDS.
+// largest key T is found by a bitwise search of at most 32 steps: T is the
+// largest value with count(key >= T) >= k, built from the high bit down, each
+// count being J ballots.  Collection is the same ascending-id ballot pass as
+// topk_kernel; up to 64 selected entries are then placed by their rank among
+// the selection, larger k sorted by a bitonic network over LDS.
 template <int J>
 __device__ __forceinline__ void select_row_wave(
     uint32_t* __restrict__ sk, int nblocks, const int32_t* __restrict__ prot, int nprot,
@@ -142,25 +136,30 @@ __device__ __forceinline__ void select_row_wave(
     if (p >= 0 && p < nblocks) atomicOr(&pmask[p >> 5], 1u << (p & 31));
   }
   wave_lds_sync();
-  uint32_t np = 0;
-  for (int w = lane; w < nwords; w += kWave) np += __popc(pmask[w]);
-  for (int o = 32; o > 0; o >>= 1) np += __shfl_xor(np, o);
-  const int avail = nblocks - static_cast<int>(np);
-  const int k = min(k_req, max(1, avail));
 
+  // blocks in range and not protected, counted with ballots
+  int avail = 0;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int i = kWave * j + lane;
-    if (i < nblocks) {
+    const bool valid = i < nblocks;
+    const bool prot_i = valid && ((pmask[i >> 5] >> (i & 31)) & 1u);
+    if (valid) {
       sk[i] = 0u;  // leave the key buffer zeroed for the next scoring pass
       if (scores) scores[i] = key_score(key[j]);
-      if ((pmask[i >> 5] >> (i & 31)) & 1u) key[j] = kNegInfKey;
+      if (prot_i) key[j] = kNegInfKey;
     } else {
       key[j] = 0u;
     }
+    avail += __popcll(__ballot(valid && !prot_i));
   }
+  const int k = min(k_req, max(1, avail));
 
   // ---- k-th largest key: largest T with count(key >= T) >= k ------------
+  // Once count(key >= T) == k the k keys >= T are the selection itself (every
+  // key equal to the k-th largest is among them), so the search stops there:
+  // the collection below then takes exactly those keys, as it would with the
+  // fully resolved T.
   uint32_t T = 0u;
   for (int bit = 31; bit >= 0; --bit) {
     const uint32_t cand = T | (1u << bit);
@@ -168,6 +167,7 @@ __device__ __forceinline__ void select_row_wave(
 #pragma unroll
     for (int j = 0; j < J; ++j) cnt += __popcll(__ballot(key[j] >= cand));
     if (cnt >= k) T = cand;
+    if (cnt == k) break;
   }
   int above = 0;
 #pragma unroll
@@ -194,20 +194,22 @@ __device__ __forceinline__ void select_row_wave(
   wave_lds_sync();
 
   if (order == NKV_ORDER_SCORE_DESC && k > 1 && k <= kWave) {
-    // descending bitonic sort of 64 lanes (entries past k are 0 and sink)
-    unsigned long long v = lane < k ? sel[lane] : 0ull;
-    for (int size = 2; size <= kWave; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        const unsigned long long w = shfl_xor_u64(v, stride);
-        const bool lower = (lane & stride) == 0;
-        const bool desc = (lane & size) == 0;
-        // the lower lane of a descending pair keeps the larger entry
-        v = (lower == desc) ? (v > w ? v : w) : (v < w ? v : w);
-      }
+    // Rank sort: the entries are distinct (the id is part of each), so the
+    // position of entry e in the descending order is the number of entries
+    // larger than e.  Lane l < k ranks sel[l] against all k entries, read as
+    // LDS broadcasts two at a time (sel holds at least 64 entries, so the
+    // pair read at j = k - 1 stays inside it; its second entry is ignored).
+    const unsigned long long e = sel[lane < k ? lane : 0];
+    int rank = 0;
+    const int kp = (k + 1) & ~1;
+#pragma unroll 8
+    for (int j = 0; j < kp; j += 2) {
+      const unsigned long long a = sel[j], b = sel[j + 1];
+      rank += (a > e) + ((j + 1 < k) & (b > e));
     }
     if (lane < k) {
-      ids[lane] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(v & 0xffffffffull));
-      if (vals) vals[lane] = key_score(static_cast<uint32_t>(v >> 32));
+      ids[rank] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(e & 0xffffffffull));
+      if (vals) vals[rank] = key_score(static_cast<uint32_t>(e >> 32));
     }
     return;
   }

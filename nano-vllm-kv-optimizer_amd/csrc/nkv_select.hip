@@ -242,29 +242,30 @@ __device__ __forceinline__ void select_row_wave(
 }
 
 
-// One (tile, head) unit of score_kernel, computed by one wavefront.
+// The loaded operands of one (tile, head) unit: the 64 x 256 B tile of
+// representative rows (16 x 16 B per lane) and the query chunks of query 0.
+template <int G>
+struct ScoreTile {
+  uint4 v[16];
+  QueryChunks<G> qc;
+};
+
+// Issues every load of unit `unit` of `layer` (no wait).  The tile is 64 rows
+// x 256 B, read with fully coalesced 16-byte loads; half c8 of chunk c holds
+// rows (64 c + lane) / 16 of dims 64 (c / 8) .. +63.  Rows past nblocks are
+// clamped to the last valid row and zeroed, so every load is issued.
 template <int R, int G>
-__device__ __forceinline__ void score_unit(
-    const uint16_t* __restrict__ q, int64_t q_ls, int nq, int per_query,
-    const uint16_t* __restrict__ reps, int64_t reps_ls, int hkv, int cap,
-    int nblocks, uint32_t* __restrict__ keys, int layer, int unit, int lane, uint4* my) {
+__device__ __forceinline__ void score_load(
+    const uint16_t* __restrict__ q, int64_t q_ls, const uint16_t* __restrict__ reps,
+    int64_t reps_ls, int hkv, int cap, int nblocks, int layer, int unit, int lane, ScoreTile<G>& t) {
   constexpr int TB = kWave / R;  // blocks per tile
-  const int nqo = per_query ? nq : 1;
   const int h = unit % hkv;
   const int b0 = (unit / hkv) * TB;
-  const int b = b0 + lane / R;
-  const int hq = hkv * G;
   const uint16_t* qL = q + static_cast<int64_t>(layer) * q_ls;
   const uint16_t* rL = reps + static_cast<int64_t>(layer) * reps_ls;
-
-  // The tile is 64 rows x 256 B.  All 16 loads are issued up front; the rows
-  // are then staged and consumed in two halves (dims 0-63, then 64-127), so
-  // each wave needs only 8 KiB of LDS.  Half c8 of chunk c: row = (64c+lane)/16.
   const uint4* src = reinterpret_cast<const uint4*>(rL + (static_cast<int64_t>(h) * cap + b0) * R * kHeadDim);
-  QueryChunks<G> qc;
-  qc.load(qL, hq, h, 0, lane);
+  t.qc.load(qL, hkv * G, h, 0, lane);
   const int last_row = (nblocks - b0) * R - 1;  // rows past it belong to blocks >= nblocks
-  uint4 v[16];
 #pragma unroll
   for (int c = 0; c < 16; ++c) {
     // half hf = c / 8 holds row chunks 8 hf .. 8 hf + 7; chunk index within
@@ -272,14 +273,25 @@ __device__ __forceinline__ void score_unit(
     const int i = (c & 7) * 64 + lane;
     const int row = i >> 3;
     const int col = (c >> 3) * 8 + (i & 7);
-    v[c] = and_mask(src[min(row, last_row) * 16 + col], row <= last_row);
+    t.v[c] = and_mask(src[min(row, last_row) * 16 + col], row <= last_row);
   }
+}
 
-  // per query n: dot over both halves in ascending d (half 0 then half 1);
-  // each half is re-staged from registers, so only 8 KiB of LDS per wave.
+// The dots and block maxima of one loaded unit.  Per query n: dot over both
+// halves in ascending d (half 0 then half 1); each half is re-staged from
+// registers through `my` (8 KiB of LDS per wave).
+template <int R, int G>
+__device__ __forceinline__ void score_dots(
+    const uint16_t* __restrict__ q, int64_t q_ls, int nq, int per_query, int hkv, int nblocks,
+    uint32_t* __restrict__ keys, int layer, int unit, int lane, ScoreTile<G>& t, uint4* my) {
+  constexpr int TB = kWave / R;
+  const int nqo = per_query ? nq : 1;
+  const int h = unit % hkv;
+  const int b = (unit / hkv) * TB + lane / R;
+  const uint16_t* qL = q + static_cast<int64_t>(layer) * q_ls;
   float best = -INFINITY;
   for (int n = 0; n < nq; ++n) {
-    if (n > 0) qc.load(qL, hq, h, n, lane);
+    if (n > 0) t.qc.load(qL, hkv * G, h, n, lane);
     float acc[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g] = 0.0f;
@@ -290,13 +302,13 @@ __device__ __forceinline__ void score_unit(
       for (int c = 0; c < 8; ++c) {
         const int i = c * 64 + lane;
         const int row = i >> 3, col = i & 7;
-        my[row * 8 + (col ^ (row & 7))] = v[hf * 8 + c];
+        my[row * 8 + (col ^ (row & 7))] = t.v[hf * 8 + c];
       }
       wave_lds_sync();
 #pragma unroll 1
       for (int c = 0; c < 8; ++c) {
         const uint4 rv = my[lane * 8 + (c ^ (lane & 7))];
-        qc.fma_chunk(rv, hf * 8 + c, acc);
+        t.qc.fma_chunk(rv, hf * 8 + c, acc);
       }
     }
     float m = acc[0];
@@ -315,6 +327,7 @@ __device__ __forceinline__ void score_unit(
     atomicMax(&keys[static_cast<int64_t>(layer) * nblocks + b], score_key(best));
 }
 
+// One (tile, head) unit per wavefront (any nq).
 template <int R, int G>
 __global__ __launch_bounds__(kScoreThreads) void score_kernel(
     const uint16_t* __restrict__ q, int64_t q_ls, int nq, int per_query,
@@ -324,8 +337,10 @@ __global__ __launch_bounds__(kScoreThreads) void score_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int unit = blockIdx.x * kScoreWaves + wave;  // (tile, head) pair
   if (unit >= units) return;
-  score_unit<R, G>(q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, keys, blockIdx.y, unit,
-                   threadIdx.x & 63, stage[wave]);
+  const int lane = threadIdx.x & 63;
+  ScoreTile<G> t;
+  score_load<R, G>(q, q_ls, reps, reps_ls, hkv, cap, nblocks, blockIdx.y, unit, lane, t);
+  score_dots<R, G>(q, q_ls, nq, per_query, hkv, nblocks, keys, blockIdx.y, unit, lane, t, stage[wave]);
 }
 
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(

@@ -351,8 +351,9 @@ class _SparseCore:
 
     def attend(self, q, k_new, v_new, *, n_chunk, write_slot, ids, ids_stride,
                n_hist, allowed, sink_len, ring_base, rec_lo, rec_len, lo=0, ws="", out=None,
-               allowed_stride=0):
+               allowed_stride=0, scale=None):
         cfg = self.cfg
+        scale = cfg.scale if scale is None else scale
         nl, tq = q.shape[0], q.shape[1]
         g = cfg.num_heads // cfg.num_kv_heads
         qpg = min(tq, max(1, 16 // g))
@@ -365,7 +366,7 @@ class _SparseCore:
         part = self._buf("partial" + ws, self.store.attend_workspace_floats(nl, tq, splits), torch.float32)
         self.store.attend(self.layer0 + lo, q, k_new, v_new, n_chunk, write_slot, ids,
                           ids_stride, n_hist, allowed, sink_len, ring_base, rec_lo, rec_len,
-                          cfg.scale, splits, part, out, allowed_stride)
+                          scale, splits, part, out, allowed_stride)
         return out
 
     def decode_attend(self, q, k, v, ids, ids_stride, n_hist, *, lo=0, ws="", out=None,
@@ -409,12 +410,16 @@ class _SparseCore:
         self.ring_start = (self.ring_start + 1) % self.cfg.recent_tokens
         self.valid_len += 1
 
-    def chunk_attend(self, q, k, v, ids, ids_stride, n_hist, allowed=None, allowed_stride=0):
+    def chunk_attend(self, q, k, v, ids, ids_stride, n_hist, allowed=None, allowed_stride=0,
+                     scale=None):
         """[selected | sink | previous recent | chunk (causal)] (m12_runtime.py:592-639, :725-758).
 
         allowed: uint8 [tq, n_hist] shared by the layers, or per layer with
-        layer stride allowed_stride."""
+        layer stride allowed_stride.  scale: softmax scale (default cfg.scale).
+        With nothing stored yet (valid_len 0, n_hist 0) this is plain causal
+        attention within the chunk."""
         cfg = self.cfg
+        scale = cfg.scale if scale is None else float(scale)
         sink_len = min(cfg.sink_tokens, self.valid_len)
         _, off, ln = prefill_recent_slice(self.valid_len, cfg.sink_tokens, cfg.recent_tokens)
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
@@ -429,13 +434,13 @@ class _SparseCore:
                 part = self._buf("pf_partial", self.store.prefill_workspace_floats(self.nl, tq, splits),
                                  torch.float32)
             self.store.prefill_attend(self.layer0, q, k, v, ids, ids_stride, n_hist, allowed,
-                                      sink_len, self.ring_start, off, ln, cfg.scale, out,
+                                      sink_len, self.ring_start, off, ln, scale, out,
                                       allowed_stride, splits, part)
         else:
             out = self.attend(q, k, v, n_chunk=q.shape[1], write_slot=-1, ids=ids,
                               ids_stride=ids_stride, n_hist=n_hist, allowed=allowed,
                               sink_len=sink_len, ring_base=self.ring_start, rec_lo=off,
-                              rec_len=ln, allowed_stride=allowed_stride)
+                              rec_len=ln, allowed_stride=allowed_stride, scale=scale)
         return out, sink_len, ln
 
 
@@ -588,6 +593,24 @@ class M12LayerRuntime:
         assert self.prefill_len == 0, "prefill_first called after history exists"
         self._store_kv(k, v)
         return {"nblocks": self.nblocks_filled, "valid_len": self.valid_len}
+
+    def dense_prefill(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                      scale: float | None = None) -> torch.Tensor:
+        """Causal attention of the first chunk within itself, on this library's kernels.
+
+        The reference runs it through flash_attn_varlen_func(causal=True)
+        before prefill_first (nanovllm/layers/attention.py:79-85); here it is
+        the chunk path with nothing stored yet (no history, sink or recent).
+        Call it before prefill_first.  q [T, Hq, D], k/v [T, Hkv, D] bf16 ->
+        [T, Hq, D] bf16."""
+        assert self.prefill_len == 0 and self.valid_len == 0, "dense_prefill is for the first chunk"
+        q = self._as_bf16(q, "q")
+        k = self._as_bf16(k, "k")
+        v = self._as_bf16(v, "v")
+        no_ids = self._core._buf("no_ids", 1, torch.int32)
+        out, _, _ = self._core.chunk_attend(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0),
+                                            no_ids, 1, 0, scale=scale)
+        return out[0]
 
     # -- selection -------------------------------------------------------------------
     def _select_dev(self, q3: torch.Tensor, requested: int, order: int):

@@ -75,3 +75,104 @@ def test_dynamic_top_k_known_answers():
     for _ in range(50):
         s = torch.sort(torch.randn(32, generator=g) * 3, descending=True).values
         assert f(s, 32, 0.9) == O.dynamic_top_k_from_scores(s.numpy(), 32, 0.9)
+
+
+class _FakeRuntime:
+    """Records which runtime entry point Attention.forward calls."""
+
+    def __init__(self, prefill_len=0):
+        self.enabled = True
+        self.verify_mode = False
+        self.prefill_len = prefill_len
+        self.calls = []
+
+    def _rec(self, name, q):
+        self.calls.append(name)
+        return torch.full((q.shape[0], 1), float(len(self.calls)))
+
+    def dense_prefill(self, q, k, v, scale=None):
+        self.calls.append(("scale", scale))
+        return self._rec("dense_prefill", q)
+
+    def prefill_first(self, q, k, v):
+        self.calls.append("prefill_first")
+        self.prefill_len = q.shape[0]
+        return {}
+
+    def prefill_chunk(self, q, k, v, device=None):
+        return self._rec("prefill_chunk", q)
+
+    def decode(self, q, k, v, device=None):
+        return self._rec("decode", q)
+
+    def verify_tokens(self, q, k, v, device=None):
+        return self._rec("verify_tokens", q)
+
+
+def test_attention_routing_follows_the_reference_order():
+    """nanovllm/layers/attention.py:64-99 sparse branch: verify, first chunk, later chunk, decode."""
+    from nanokv_amd import attention as A
+
+    layer = A.Attention(32, 128, 0.125, 8)
+    fake = _FakeRuntime()
+    layer.sparse_rt = fake
+    q, k, v = torch.zeros(4, 32, 128), torch.zeros(4, 8, 128), torch.zeros(4, 8, 128)
+    try:
+        A.set_context(True, max_seqlen_q=4)
+        layer(q, k, v)
+        assert fake.calls == [("scale", 0.125), "dense_prefill", "prefill_first"]
+        fake.calls.clear()
+        layer(q, k, v)   # history exists now
+        assert fake.calls == ["prefill_chunk"]
+        fake.calls.clear()
+        fake.verify_mode = True
+        A.set_context(False)
+        layer(q, k, v)   # verify ignores is_prefill and the token count
+        assert fake.calls == ["verify_tokens"]
+        fake.calls.clear()
+        fake.verify_mode = False
+        layer(q[:1], k[:1], v[:1])
+        assert fake.calls == ["decode"]
+        with pytest.raises(AssertionError, match="single query token"):
+            layer(q, k, v)
+        A.set_context(False, block_tables=torch.zeros(1, 1))
+        with pytest.raises(AssertionError, match="block tables"):
+            layer(q[:1], k[:1], v[:1])
+        A.set_context(False)
+        layer.k_cache = torch.zeros(3)
+        with pytest.raises(AssertionError, match="zero paged blocks"):
+            layer(q[:1], k[:1], v[:1])
+    finally:
+        A.reset_context()
+
+
+def test_attention_without_runtime_raises():
+    from nanokv_amd import attention as A
+
+    layer = A.Attention(32, 128, 0.125, 8)
+    with pytest.raises(NotImplementedError, match="sparse_rt"):
+        layer(torch.zeros(1, 32, 128), torch.zeros(1, 8, 128), torch.zeros(1, 8, 128))
+    fake = _FakeRuntime()
+    fake.enabled = False
+    layer.sparse_rt = fake
+    with pytest.raises(NotImplementedError):
+        layer(torch.zeros(1, 32, 128), torch.zeros(1, 8, 128), torch.zeros(1, 8, 128))
+
+
+def test_context_mirrors_the_reference_fields():
+    from nanokv_amd import attention as A
+
+    assert list(A.Context.__dataclass_fields__) == [
+        "is_prefill", "cu_seqlens_q", "cu_seqlens_k", "max_seqlen_q", "max_seqlen_k",
+        "slot_mapping", "context_lens", "block_tables"]
+    A.set_context(True, None, None, 7)
+    assert A.get_context().is_prefill and A.get_context().max_seqlen_q == 7
+    A.reset_context()
+    assert A.get_context() == A.Context()
+
+
+def test_attach_requires_attention_modules():
+    from nanokv_amd import attention as A
+
+    with pytest.raises(ValueError, match="no attention modules"):
+        A.attach_m12_runtimes(torch.nn.Linear(2, 2), rt.M12Config(max_model_len=1024))

@@ -343,6 +343,8 @@ def main():
     ap.add_argument("--top-k", type=int, default=32)
     ap.add_argument("--kv-format", choices=["bf16", "int8", "int8_token"], default="bf16")
     ap.add_argument("--splits", type=int, default=None)
+    ap.add_argument("--history", choices=["hbm", "host"], default="hbm",
+                    help="decode: history in HBM (default) or in pinned host memory read in place")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-layers", type=int, default=4)
@@ -396,7 +398,7 @@ def main():
     quant = args.kv_format != "bf16"
     cfg = M12Config(max_model_len=T, top_k_blocks=args.top_k, quant_history=quant,
                     quant_scale_layout="token" if args.kv_format == "int8_token" else "channel_block",
-                    attend_splits=args.splits)
+                    attend_splits=args.splits, history_tier=args.history)
     model = M12ModelRuntime(L, cfg, device=dev, layer_streams=args.layer_streams)
 
     t0 = time.perf_counter()
@@ -483,9 +485,11 @@ def main():
             "workload": (f"sparse decode layer-step, {T}-token history ({nb} blocks) x {L} "
                          f"independent layers, Qwen3-4B attention shape (Hq=32, Hkv=8, D=128), "
                          f"top-{args.top_k} + sink {cfg.sink_tokens} + recent {cfg.recent_tokens}, "
-                         f"r=4, {args.kv_format} history"),
+                         f"r=4, {args.kv_format} history"
+                         + (" in pinned host memory, read in place over the host link"
+                            if args.history == "host" else "")),
             "layers": L, "context": T, "top_k": args.top_k, "kv_format": args.kv_format,
-            "layer_streams": args.layer_streams,
+            "layer_streams": args.layer_streams, "history_tier": args.history,
         },
         "us_per_layer_step": round(us_layer, 4),
         "hbm_gbps": round(step_gbps, 1),

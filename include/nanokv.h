@@ -310,6 +310,21 @@ int nkv_query_summaries(const uint16_t* q, int64_t q_layer_stride, int num_layer
                         int T, int num_heads, int head_dim, int nsegments,
                         uint16_t* out, int64_t out_layer_stride, void* stream);
 
+/*
+ * Device address of pinned host memory, for a history kept in host memory.
+ *
+ * Replaces the reference's host-resident history and its per-step gather +
+ * H2D copy of the selected blocks into pinned staging (m12_runtime.py:185-246
+ * allocation, :1212-1311 decode gather, :560-636 prefill gather): a store
+ * whose hist_k / hist_v point at pinned host memory (allocated by the HIP
+ * runtime: hipHostMalloc, or torch's pin_memory=True) is read in place by
+ * every kernel over the host link, so no staging copy exists.  Put the
+ * returned address (not host_ptr) in nkv_store.hist_k / hist_v.
+ * Returns NKV_ERR_ARG when host_ptr is not pinned host memory of the HIP
+ * runtime or is not mapped for the current device.
+ */
+int nkv_host_device_pointer(const void* host_ptr, void** device_ptr);
+
 #ifdef __cplusplus
 }
 #endif

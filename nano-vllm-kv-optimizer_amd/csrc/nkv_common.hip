@@ -67,4 +67,31 @@ int device_cus() {
 }  // namespace nkv
 
 extern "C" int nkv_abi_version(void) { return NKV_ABI_VERSION; }
+
+extern "C" int nkv_host_device_pointer(const void* host_ptr, void** device_ptr) {
+  NKV_CHECK_ARG(host_ptr != nullptr && device_ptr != nullptr,
+                "nkv_host_device_pointer: host_ptr and device_ptr must be non-NULL");
+  *device_ptr = nullptr;
+  hipPointerAttribute_t attr;
+  hipError_t e = hipPointerGetAttributes(&attr, host_ptr);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();  // an unknown (pageable) pointer is an argument error, not a fault
+    ::nkv::set_error("nkv_host_device_pointer: %p is not memory of the HIP runtime (%s)", host_ptr,
+                     hipGetErrorString(e));
+    return NKV_ERR_ARG;
+  }
+  NKV_CHECK_ARG(attr.type == hipMemoryTypeHost,
+                "nkv_host_device_pointer: %p is not pinned host memory (memory type %d)", host_ptr,
+                static_cast<int>(attr.type));
+  void* d = nullptr;
+  e = hipHostGetDevicePointer(&d, const_cast<void*>(host_ptr), 0);
+  if (e != hipSuccess || d == nullptr) {
+    (void)hipGetLastError();
+    ::nkv::set_error("nkv_host_device_pointer: %p is not mapped for the device (%s)", host_ptr,
+                     hipGetErrorString(e));
+    return NKV_ERR_ARG;
+  }
+  *device_ptr = d;
+  return NKV_OK;
+}
 extern "C" const char* nkv_last_error(void) { return nkv::g_last_error; }

@@ -82,6 +82,7 @@ SIGNATURES = {
     "nkv_build_reps": (_I, [_SP, _I, _I, _P, _I64, _I, _I, _P]),
     "nkv_recent_update": (_I, [_SP, _I, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _P]),
     "nkv_query_summaries": (_I, [_P, _I64, _I, _I, _I, _I, _I, _P, _I64, _P]),
+    "nkv_host_device_pointer": (_I, [_P, ctypes.POINTER(ctypes.c_void_p)]),
 }
 
 _lib = None
@@ -105,6 +106,15 @@ def load():
         raise RuntimeError(f"{LIB_PATH}: ABI version {lib.nkv_abi_version()} != {ABI_VERSION}")
     _lib = lib
     return lib
+
+
+def host_device_pointer(host_ptr: int) -> int:
+    """Device address of pinned host memory (nkv_host_device_pointer)."""
+    lib = load()
+    out = ctypes.c_void_p()
+    check(lib.nkv_host_device_pointer(ctypes.c_void_p(host_ptr), ctypes.byref(out)),
+          "host_device_pointer")
+    return out.value
 
 
 def check(rc: int, what: str) -> None:

@@ -111,7 +111,7 @@ def attach_m12_runtimes(model: nn.Module, cfg: M12Config, device=None) -> list[M
         len(layers), num_heads=cfg.num_heads, num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim,
         block_size=B, r=cfg.r, cap_blocks=(cfg.max_model_len + B - 1) // B,
         sink_tokens=cfg.sink_tokens, recent_tokens=cfg.recent_tokens, kv_format=cfg.kv_format,
-        device=device)
+        device=device, history_tier=cfg.history_tier)
     runtimes = []
     for layer_id, module in enumerate(layers):
         module.layer_id = layer_id

@@ -96,7 +96,10 @@ class M12Config:
     matrix-core kernel, shorter ones the few-query kernel; None = automatic:
     the matrix-core kernel as soon as the chunk's query rows, tokens x heads
     per KV head, exceed the few-query kernel's 16-row group, which it would
-    otherwise split, reading every block once per group).  ``use_index_select``,
+    otherwise split, reading every block once per group), ``history_tier``
+("hbm": the whole history in HBM; "host": hist_k / hist_v in pinned host
+memory, read in place by the same kernels over the host link, the
+reference's offload mode without its gather and H2D copy).  ``use_index_select``,
     ``decode_kv_pipeline`` and ``gather_sort``'s gather-locality purpose
     belong to the host-offload design and do not change the HBM path
     (``gather_sort`` still orders ``last_block_ids`` ascending).
@@ -136,6 +139,7 @@ class M12Config:
     quant_scale_layout: str = "channel_block"
     attend_splits: int | None = None
     mfma_chunk_min_tokens: int | None = None
+    history_tier: str = "hbm"
 
     def __post_init__(self):
         if self.decode_kv_pipeline and not self.use_index_select:
@@ -161,6 +165,8 @@ class M12Config:
             raise ValueError("attend_splits must be in [1, 64]")
         if self.mfma_chunk_min_tokens is not None and self.mfma_chunk_min_tokens < 1:
             raise ValueError("mfma_chunk_min_tokens must be >= 1 or None")
+        if self.history_tier not in ("hbm", "host"):
+            raise ValueError("history_tier must be 'hbm' or 'host'")
 
     @property
     def kv_format(self) -> str:
@@ -465,7 +471,8 @@ class M12LayerRuntime:
             store = SparseKVStore(
                 1, num_heads=cfg.num_heads, num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim,
                 block_size=B, r=cfg.r, cap_blocks=self.max_blocks, sink_tokens=cfg.sink_tokens,
-                recent_tokens=cfg.recent_tokens, kv_format=cfg.kv_format, device=device)
+                recent_tokens=cfg.recent_tokens, kv_format=cfg.kv_format, device=device,
+                history_tier=cfg.history_tier)
             store_layer = 0
         elif store_layer is None:
             store_layer = layer_id
@@ -894,7 +901,8 @@ class M12ModelRuntime:
             num_layers, num_heads=cfg.num_heads, num_kv_heads=cfg.num_kv_heads,
             head_dim=cfg.head_dim, block_size=B, r=cfg.r, cap_blocks=self.max_blocks,
             sink_tokens=cfg.sink_tokens, recent_tokens=cfg.recent_tokens,
-            kv_format=cfg.kv_format, device=device)
+            kv_format=cfg.kv_format, device=device,
+                history_tier=cfg.history_tier)
         self.core = _SparseCore(cfg, self.store, 0, num_layers)
         self.last_ids_dev: torch.Tensor | None = None
         self.last_n_selected = 0

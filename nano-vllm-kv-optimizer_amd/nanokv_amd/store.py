@@ -12,6 +12,13 @@ blocks to the GPU every decode step (nanovllm/sparse/m12_runtime.py:185-246,
 
 Every method enqueues HIP kernels on the current torch stream through the C
 ABI of include/nanokv.h; none of them synchronises.
+
+history_tier="host" keeps hist_k / hist_v (the bulk: 16 KiB per (block, KV
+head) each) in pinned host memory instead, for histories larger than HBM,
+as the reference always does.  Everything else stays in HBM, and the same
+kernels read the selected blocks in place through the device mapping of the
+pinned pages (nkv_host_device_pointer): the reference's per-step gather into
+pinned staging and H2D copy (m12_runtime.py:1212-1311) has no counterpart.
 """
 
 from __future__ import annotations
@@ -45,13 +52,15 @@ class SparseKVStore:
 
     def __init__(self, num_layers: int, *, num_heads: int, num_kv_heads: int, head_dim: int,
                  block_size: int, r: int, cap_blocks: int, sink_tokens: int, recent_tokens: int,
-                 kv_format: str = "bf16", device=None):
+                 kv_format: str = "bf16", device=None, history_tier: str = "hbm"):
         if head_dim != HEAD_DIM:
             raise ValueError(f"head_dim must be {HEAD_DIM} for the gfx950 kernels (got {head_dim})")
         if block_size != BLOCK_SIZE:
             raise ValueError(f"block_size must be {BLOCK_SIZE} for the gfx950 kernels (got {block_size})")
         if kv_format not in KV_FORMATS:
             raise ValueError(f"unknown kv_format {kv_format!r}")
+        if history_tier not in ("hbm", "host"):
+            raise ValueError(f"history_tier must be 'hbm' or 'host' (got {history_tier!r})")
         self.lib = _lib.load()
         dev = torch.device(device if device is not None else "cuda")
         L, H, S, R, B, D = num_layers, num_kv_heads, sink_tokens, recent_tokens, block_size, head_dim
@@ -60,9 +69,19 @@ class SparseKVStore:
         self.cap_blocks, self.sink_tokens, self.recent_tokens = cap_blocks, S, R
         self.kv_format = kv_format
         self.device = dev
+        self.history_tier = history_tier
         hdt = torch.bfloat16 if kv_format == "bf16" else torch.int8
-        self.hist_k = torch.zeros(L, H, cap_blocks, B, D, dtype=hdt, device=dev)
-        self.hist_v = torch.zeros_like(self.hist_k)
+        if history_tier == "host":
+            # new pinned allocations (the HIP runtime maps them for the device)
+            self.hist_k = torch.zeros(L, H, cap_blocks, B, D, dtype=hdt, pin_memory=True)
+            self.hist_v = torch.zeros(L, H, cap_blocks, B, D, dtype=hdt, pin_memory=True)
+            with torch.cuda.device(dev):
+                hist_k_addr = _lib.host_device_pointer(self.hist_k.data_ptr())
+                hist_v_addr = _lib.host_device_pointer(self.hist_v.data_ptr())
+        else:
+            self.hist_k = torch.zeros(L, H, cap_blocks, B, D, dtype=hdt, device=dev)
+            self.hist_v = torch.zeros_like(self.hist_k)
+            hist_k_addr, hist_v_addr = self.hist_k.data_ptr(), self.hist_v.data_ptr()
         self.reps = torch.zeros(L, H, cap_blocks, r, D, dtype=torch.bfloat16, device=dev)
         self.sink_k = torch.zeros(L, H, max(S, 1), D, dtype=torch.bfloat16, device=dev)
         self.sink_v = torch.zeros_like(self.sink_k)
@@ -76,7 +95,7 @@ class SparseKVStore:
             self.k_tscale = torch.zeros(L, H, cap_blocks * B, dtype=torch.float16, device=dev)
             self.v_tscale = torch.zeros_like(self.k_tscale)
         self.desc = _lib.NkvStore(
-            _ptr(self.hist_k).value, _ptr(self.hist_v).value, _ptr(self.reps).value,
+            hist_k_addr, hist_v_addr, _ptr(self.reps).value,
             _ptr(self.sink_k).value, _ptr(self.sink_v).value,
             _ptr(self.recent_k).value, _ptr(self.recent_v).value,
             _ptr(self.k_scale).value, _ptr(self.v_scale).value,

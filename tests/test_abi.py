@@ -139,3 +139,11 @@ def test_attend_rejects_a_short_allowed_layer_stride():
     rc = lib.nkv_attend(ctypes.byref(st), 0, 2, d, 6 * 32 * 128, 6, d, d, 6 * 8 * 128, 6, -1, d, 10, 10,
                         d, 59, 64, 0, 0, 511, 1.0, 1, None, d, None)
     assert rc == _lib.NKV_ERR_ARG and b"allowed_layer_stride" in lib.nkv_last_error()
+
+
+def test_host_device_pointer_rejects_null_without_device_work():
+    lib = _lib.load()
+    out = ctypes.c_void_p(1234)
+    assert lib.nkv_host_device_pointer(None, ctypes.byref(out)) == _lib.NKV_ERR_ARG
+    assert b"non-NULL" in lib.nkv_last_error()
+    assert lib.nkv_host_device_pointer(ctypes.c_void_p(8), None) == _lib.NKV_ERR_ARG

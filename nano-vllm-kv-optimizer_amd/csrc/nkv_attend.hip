@@ -22,11 +22,16 @@
 //    keys are widened to bf16 exactly; the per-(head, dim) K scale is folded
 //    into the bf16 query operand of history segments.
 //  * softmax: fp32, exp2 with the scale folded in.
-//  * P.V on the vector ALUs in fp32: lane (r, c) owns dims 8c..8c+7 of keys
-//    4j + r; p comes from LDS.  The int8 V scale (per block or per token) is
-//    folded into p.  With 4 query rows (decode) V loads are issued together
-//    with the K loads, so a segment's 32 KiB are in flight at once; wider
-//    accumulators issue them right after the MFMAs, overlapping the softmax.
+//  * P.V, 4 query rows (decode): on the matrix cores.  V (int8 widened to
+//    bf16 exactly) goes to the wave's LDS tile and is read back transposed
+//    (ds_read_b64_tr_b16) as the A operand; P^T comes straight from the
+//    Q.K^T output registers as bf16 hi + lo parts, so P.V keeps fp32
+//    accuracy.  V loads are issued together with the K loads, so a
+//    segment's 32 KiB (bf16) are in flight at once.
+//  * P.V, 8 or 16 query rows (verify): on the vector ALUs in fp32: lane
+//    (r, c) owns dims 8c..8c+7 of keys 4j + r; p comes from LDS.  V loads are
+//    issued right after the MFMAs, overlapping the softmax.
+//    In both forms the int8 V scale (per block or per token) is folded into p.
 //  * the 4 wavefronts merge through LDS; with splits > 1 each workgroup
 //    writes a partial (m, l, acc[128]) per query row and a second kernel
 //    merges them (stream order makes the partials visible).
@@ -39,6 +44,7 @@
 #include <type_traits>
 
 #include "nkv_attend_common.h"
+#include "nkv_stage.h"
 
 namespace nkv {
 namespace {
@@ -76,10 +82,25 @@ constexpr int attend_lds_floats() {
              : 2 * kAttendWaves * kMaxRows + kAttendWaves * M * kHeadDim;
 }
 
+// The 4-row (decode) variants run P.V on the matrix cores: the vector-ALU
+// form costs 512 fp32 FMAs per lane and segment, which with the int8
+// dequantisation no longer hides under the loads (36-layer 32K step: bf16
+// attention 86.6 -> 83.2 us, int8 77.0 -> 74.2, int8 per-token 84.6 -> 79.2).
+// The wider variants keep fp32 P.V on the vector ALUs (their accumulators
+// would not fit beside the V tiles).
+template <int FMT, int M>
+constexpr bool attend_mfma_pv() {
+  return M == 4;
+}
+constexpr int kVTileBytes = kBlock * kHeadDim * 2;   // one bf16 V tile in LDS
+static_assert(2 * kAttendWaves * kMaxRows + kAttendWaves * 4 * kHeadDim <= kAttendWaves * kVTileBytes / 4,
+              "the cross-wave merge fits in the V tiles");
+
 template <int FMT, int M>
 __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 1) void attend_kernel(const AttendParams p) {
-  __shared__ __attribute__((aligned(16))) float s_lds[attend_lds_floats<M>()];
-  __shared__ float s_alpha[kAttendWaves][kMaxRows];
+  constexpr bool kMfmaPV = attend_mfma_pv<FMT, M>();
+  __shared__ __attribute__((aligned(16))) float s_lds[kMfmaPV ? kAttendWaves * kVTileBytes / 4 : attend_lds_floats<M>()];
+  __shared__ float s_alpha[kMfmaPV ? 1 : kAttendWaves][kMaxRows];
 
   const int split = blockIdx.x;
   const int h = blockIdx.y;
@@ -139,13 +160,27 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
 
   float m_run = -INFINITY;   // per query row (lane & 15); equal across lane groups
   float l_run = 0.0f;        // partial over this lane group's keys
-  float acc[M][8];
+  float acc[M][8];           // vector-ALU P.V: dims 8 ln .. +8 of row n, keys = lg mod 4
+  f32x4 oacc[8];             // matrix-core P.V: O^T, oacc[dt][i] = dim 16 dt + 4 lg + i of row ln
 #pragma unroll
   for (int n = 0; n < M; ++n)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[n][e] = 0.0f;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) oacc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   float* my_p = s_lds + wave * kBlock * kPRow;
+  // matrix-core P.V: this wave's V tile in LDS, key-major with chunk c of key
+  // k at position c ^ 2 (k & 3); V register (key 4 j + lg, chunk ln) lands at
+  // j * 1024 + vw.  The transposing reads (ds_read_b64_tr_b16) give lane ln
+  // keys 4 lg + (ln >> 2) (+ 32 k2, + 16 for the high half), dims 16 dt +
+  // 4 (ln & 3) + 0..3; vtr[dt & 3] is that lane's offset, dt & 4 adds 128.
+  char* my_v = reinterpret_cast<char*>(s_lds) + wave * kVTileBytes;
+  const int vw = lg * 256 + ((ln ^ (2 * lg)) << 4);
+  int vtr[4];
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4)
+    vtr[q4] = (4 * lg + (ln >> 2)) * 256 + ((2 * (q4 ^ (ln >> 2)) + ((ln & 3) >> 1)) << 4) + 8 * (ln & 1);
   const int nwaves = p.splits * kAttendWaves;
   // One segment of this wavefront.  int8 history segments (always the first
   // n_hist segments) and bf16 segments are two instantiations of the body, run
@@ -275,11 +310,56 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
         if (FMT == NKV_KV_INT8_TOKEN && int8_seg)
           pv *= f16_bits_to_f32(p.v_tscale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap * kBlock +
                                            static_cast<int64_t>(g.blk) * kBlock + tk]);
-        my_p[tk * kPRow + ln] = pv;
+        if (kMfmaPV)
+          x[i][e] = pv;
+        else
+          my_p[tk * kPRow + ln] = pv;
       }
     }
     l_run = l_run * alpha + lsum;
     m_run = m_new;
+
+    if constexpr (kMfmaPV) {
+      // ---- O^T += V^T . P^T on the matrix cores -----------------------------
+      // V (int8 widened to bf16 exactly) -> LDS; P^T from registers: key
+      // 32 k2 + 4 lg + e is x[2 k2][e], key 32 k2 + 16 + 4 lg + e is
+      // x[2 k2 + 1][e], the same order the transposing reads give V^T.  P
+      // enters as bf16 hi + lo parts (about 16 significant bits), so P.V
+      // keeps fp32 accuracy.
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) oacc[dt] *= alpha;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint4 vb = int8_seg ? i8x8_to_bf16x8(va[j].x, va[j].y) : va[j];
+        *reinterpret_cast<uint4*>(my_v + j * 1024 + vw) = vb;
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const float v8[8] = {x[2 * k2][0], x[2 * k2][1], x[2 * k2][2], x[2 * k2][3],
+                             x[2 * k2 + 1][0], x[2 * k2 + 1][1], x[2 * k2 + 1][2], x[2 * k2 + 1][3]};
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          hw[i] = stage::pack_bf16(v8[2 * i], v8[2 * i + 1]);
+          lw[i] = stage::pack_bf16(v8[2 * i] - __uint_as_float(hw[i] << 16),
+                                   v8[2 * i + 1] - __uint_as_float(hw[i] & 0xffff0000u));
+        }
+        const bf16x8 bp = as_bf16x8(make_uint4(hw[0], hw[1], hw[2], hw[3]));
+        const bf16x8 bl = as_bf16x8(make_uint4(lw[0], lw[1], lw[2], lw[3]));
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const char* vp = my_v + vtr[dt & 3] + (dt >> 2) * 128 + k2 * 8192;
+          const stage::i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((stage::lds_i16x4*)(vp));
+          const stage::i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((stage::lds_i16x4*)(vp + 4096));
+          const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp, oacc[dt], 0, 0, 0);
+          oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bl, oacc[dt], 0, 0, 0);
+        }
+      }
+      wave_lds_sync();   // the next segment overwrites the V tile
+      return;
+    }
     if (lane < kMaxRows) s_alpha[wave][lane] = alpha;
     wave_lds_sync();
 
@@ -325,13 +405,15 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
   // ---- reduce the wave's state across lane groups --------------------------
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
+  if constexpr (!kMfmaPV) {
 #pragma unroll
-  for (int n = 0; n < M; ++n)
+    for (int n = 0; n < M; ++n)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      acc[n][e] += __shfl_xor(acc[n][e], 16);
-      acc[n][e] += __shfl_xor(acc[n][e], 32);
-    }
+      for (int e = 0; e < 8; ++e) {
+        acc[n][e] += __shfl_xor(acc[n][e], 16);
+        acc[n][e] += __shfl_xor(acc[n][e], 32);
+      }
+  }
 
   // ---- merge the 4 wavefronts in LDS (reusing the p tiles) -----------------
   __syncthreads();
@@ -342,7 +424,14 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
     s_m[wave * kMaxRows + lane] = m_run;
     s_l[wave * kMaxRows + lane] = l_run;
   }
-  if (lg == 0) {
+  if constexpr (kMfmaPV) {
+    if (ln < M) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s_acc[(wave * M + ln) * kHeadDim + 16 * dt + 4 * lg + i] = oacc[dt][i];
+    }
+  } else if (lg == 0) {
 #pragma unroll
     for (int n = 0; n < M; ++n)
 #pragma unroll

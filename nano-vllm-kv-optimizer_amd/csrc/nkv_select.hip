@@ -10,14 +10,14 @@
 // (nanovllm/sparse/m12_runtime.py:999-1003).
 //
 // Mapping: a wavefront owns one (16-block tile, KV head) unit = 64 rows of
-// r representatives.  It streams that 16 KiB tile with fully coalesced 16-byte
+// r representatives; the 4 waves of a workgroup take 4 consecutive tiles of
+// one KV head.  A wave streams its 16 KiB tile with fully coalesced 16-byte
 // loads (lane i reads bytes [1024*c + 16*i, +16)), transposes it through LDS
 // with an XOR swizzle (conflict-free ds_read_b128), and then every lane dots
-// its own row with the G query rows of that head.  The query rows arrive with
-// one vector load issued beside the tile's and are read back as wave-uniform
-// scalars (v_readlane), so no chain of scalar-cache misses sits between the
-// tile's arrival and the wave's exit.  Every load is unconditional (rows past
-// nblocks are clamped and masked), so the waits count exactly.  Block maxima across the
+// its own row with the G query rows of that head, whose values come from
+// scalar loads (wave-uniform) after one warm-up touch of their cache lines.
+// Every vector load is unconditional (rows past nblocks are clamped and
+// masked), so the waits count exactly.  Block maxima across the
 // r rows use lane shuffles; the maximum across KV heads is an atomicMax on
 // the order-preserving uint32 key of the score, which kernel 2 consumes and
 // resets to zero.
@@ -55,23 +55,23 @@ __device__ __forceinline__ uint4 and_mask(uint4 x, bool keep) {
   return make_uint4(x.x & m, x.y & m, x.z & m, x.w & m);
 }
 
-// The G query rows of one (query, KV head) as 16 G chunks of 8 bf16, held in
-// vector registers: lane j of set s holds chunk 64 s + j (row (64 s + j) / 16,
-// dims 8 ((64 s + j) % 16) .. +8).  One vector load fetches them together
-// with the tile; the dot loop reads each chunk back as wave-uniform scalars
-// (v_readlane), so no scalar-cache round trip sits on the critical path.
+// The G query rows of one (query, KV head): 16 G chunks of 8 bf16 at a
+// wave-uniform address, read with scalar loads straight into the
+// `v_fmac_f32 v, s, v` operand (no vector-ALU broadcast).  load() first touches
+// every 64-byte line of the rows once, so the per-chunk scalar loads hit the
+// scalar cache instead of queueing one line miss after another; the four
+// waves of a workgroup score the same KV head, so they share those lines.
 template <int G>
 struct QueryChunks {
-  static constexpr int kSets = (16 * G + kWave - 1) / kWave;
-  uint4 r[kSets];
+  const uint4* qh;   // the G rows of query n, KV head h: 16 G chunks of 16 bytes (uniform)
 
   __device__ __forceinline__ void load(const uint16_t* qL, int hq, int h, int n, int lane) {
-    const uint4* qh = reinterpret_cast<const uint4*>(qL + (static_cast<int64_t>(n) * hq + h * G) * kHeadDim);
+    qh = reinterpret_cast<const uint4*>(qL + (static_cast<int64_t>(n) * hq + h * G) * kHeadDim);
+    // bring every 64-byte line of the rows into the scalar cache at once
+    uint32_t x = 0;
 #pragma unroll
-    for (int s = 0; s < kSets; ++s) {
-      const int j = s * kWave + lane;
-      r[s] = and_mask(qh[min(j, 16 * G - 1)], j < 16 * G);
-    }
+    for (int l = 0; l < 4 * G; ++l) x ^= reinterpret_cast<const uint32_t*>(qh)[l * 16];
+    asm volatile("" ::"s"(x));
   }
 
   // acc[g] += q[g][8 c + e] * rv[e] for e = 0..7 in ascending order
@@ -80,14 +80,9 @@ struct QueryChunks {
                          bf16_lo(rv.z), bf16_hi(rv.z), bf16_lo(rv.w), bf16_hi(rv.w)};
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const uint4& src = r[g >> 2];
-      const int ln = ((g & 3) << 4) + c;
-      const uint32_t q0 = __builtin_amdgcn_readlane(src.x, ln);
-      const uint32_t q1 = __builtin_amdgcn_readlane(src.y, ln);
-      const uint32_t q2 = __builtin_amdgcn_readlane(src.z, ln);
-      const uint32_t q3 = __builtin_amdgcn_readlane(src.w, ln);
-      const float qf[8] = {bf16_lo(q0), bf16_hi(q0), bf16_lo(q1), bf16_hi(q1),
-                           bf16_lo(q2), bf16_hi(q2), bf16_lo(q3), bf16_hi(q3)};
+      const uint4 qv = qh[g * 16 + c];
+      const float qf[8] = {bf16_lo(qv.x), bf16_hi(qv.x), bf16_lo(qv.y), bf16_hi(qv.y),
+                           bf16_lo(qv.z), bf16_hi(qv.z), bf16_lo(qv.w), bf16_hi(qv.w)};
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[g] = __builtin_fmaf(qf[e], rf[e], acc[g]);
     }
@@ -264,7 +259,6 @@ __device__ __forceinline__ void score_load(
   const uint16_t* qL = q + static_cast<int64_t>(layer) * q_ls;
   const uint16_t* rL = reps + static_cast<int64_t>(layer) * reps_ls;
   const uint4* src = reinterpret_cast<const uint4*>(rL + (static_cast<int64_t>(h) * cap + b0) * R * kHeadDim);
-  t.qc.load(qL, hkv * G, h, 0, lane);
   const int last_row = (nblocks - b0) * R - 1;  // rows past it belong to blocks >= nblocks
 #pragma unroll
   for (int c = 0; c < 16; ++c) {
@@ -275,6 +269,7 @@ __device__ __forceinline__ void score_load(
     const int col = (c >> 3) * 8 + (i & 7);
     t.v[c] = and_mask(src[min(row, last_row) * 16 + col], row <= last_row);
   }
+  t.qc.load(qL, hkv * G, h, 0, lane);
 }
 
 // The dots and block maxima of one loaded unit.  Per query n: dot over both
@@ -335,7 +330,10 @@ __global__ __launch_bounds__(kScoreThreads) void score_kernel(
     int nblocks, int units, uint32_t* __restrict__ keys) {
   __shared__ uint4 stage[kScoreWaves][64 * 8];  // per wave: 64 rows x 8 chunks (one half), swizzled
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int unit = blockIdx.x * kScoreWaves + wave;  // (tile, head) pair
+  // the 4 waves of a workgroup take 4 consecutive tiles of one KV head
+  const int hh = blockIdx.x % hkv;
+  const int tile = (blockIdx.x / hkv) * kScoreWaves + wave;
+  const int unit = tile * hkv + hh;  // (tile, head) pair
   if (unit >= units) return;
   const int lane = threadIdx.x & 63;
   ScoreTile<G> t;
@@ -646,7 +644,7 @@ extern "C" int nkv_select(const nkv_store* st, int layer0, int num_layers, const
   const int64_t reps_ls = static_cast<int64_t>(st->num_kv_heads) * st->cap_blocks * R * kHeadDim;
   const uint16_t* reps = static_cast<const uint16_t*>(st->reps) + layer0 * reps_ls;
   const int units = ((nblocks + TB - 1) / TB) * st->num_kv_heads;
-  dim3 grid((units + kScoreWaves - 1) / kScoreWaves, num_layers);
+  dim3 grid(((units / st->num_kv_heads + kScoreWaves - 1) / kScoreWaves) * st->num_kv_heads, num_layers);
   int bad = 0;
   switch (R) {
     case 1: bad = dispatch_g<1>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;

@@ -273,6 +273,39 @@ def dynamic_top_k_from_scores(top_scores, max_k: int, target_mass: float) -> int
     return max_k
 
 
+def relative_threshold_select(scores, protected, requested: int, a: float, scale: float,
+                              max_blocks: int, union: bool):
+    """Relative-threshold decode selection (m12_runtime.py:1015-1031).
+
+    Protected -> -inf; threshold = max score + ln(a) / scale; among the first
+    cap = min(max_blocks, max(1, avail)) blocks in (score desc, id asc) order,
+    keep those with score >= threshold (with ``union``: also the first k of
+    them); if none is kept, the first k.  Returns (ids int64, values f32) in
+    score order.  k = effective_k(...).  Pinned by hand-computed known answers
+    in tests/test_oracle_pins.py.
+    """
+    s = np.array(scores, dtype=F32, copy=True)
+    nb = s.shape[0]
+    prot = [p for p in protected if 0 <= p < nb]
+    if prot:
+        s[np.asarray(sorted(prot))] = F32(-np.inf)
+    avail = nb - len(prot)
+    k = effective_k(nb, protected, requested)
+    cap = min(int(max_blocks), max(1, avail))
+    key = orderable_key(s).astype(np.int64)
+    order = np.lexsort((np.arange(nb), -key))
+    threshold = float(s.max()) + math.log(a) / scale
+    cand = order[:cap]
+    keep = s[cand] >= threshold
+    if union:
+        keep = keep | (np.arange(cand.shape[0]) < k)
+    if not keep.any():
+        ids = order[:k]
+    else:
+        ids = cand[keep]
+    return ids.astype(np.int64), s[ids]
+
+
 # ---------------------------------------------------------------------------
 # Representatives -- m12_runtime.py:354-395
 # ---------------------------------------------------------------------------
@@ -448,6 +481,11 @@ class OracleConfig:
     num_kv_heads: int = 8
     head_dim: int = 128
     scale: float = 128.0 ** -0.5
+    # decode selection policies (m12_runtime.py:98-166 fields, :1176-1195, :1015-1031)
+    decode_relative_a: float | None = None
+    decode_relative_max_blocks: int = 48
+    decode_relative_union: bool = False
+    decode_query_window: int = 1
 
 
 @dataclass
@@ -480,6 +518,7 @@ class M12Oracle:
         self.protected_blocks: set = set()
         self.last_block_ids = None
         self.pending = None
+        self.q_window: list = []   # decode routing queries (m12_runtime.py:1181-1184)
 
     def reset(self):
         """m12_runtime.py:322-349: lengths cleared, buffers (and their contents) kept."""
@@ -490,6 +529,7 @@ class M12Oracle:
         self.k_scale = None
         self.last_block_ids = None
         self.pending = None
+        self.q_window = []
 
     # -- store (m12_runtime.py:420-513) ------------------------------------
     def store_kv(self, k, v, with_reps: bool = True):
@@ -613,7 +653,23 @@ class M12Oracle:
         self.recent_v[:-1] = self.recent_v[1:].copy()
         self.recent_k[-1] = np.asarray(k, F32)[0]
         self.recent_v[-1] = np.asarray(v, F32)[0]
-        ids, vals = self.select(q[0], c.decode_top_k_blocks if budget is None else budget)
+        # routing query: the mean of the last decode_query_window queries
+        # (m12_runtime.py:1176-1189); attention below uses the current q
+        q_route = q[0]
+        if c.decode_query_window > 1:
+            self.q_window.append(q[0].copy())
+            del self.q_window[:-c.decode_query_window]
+            if len(self.q_window) > 1:
+                q_route = query_summaries(np.stack(self.q_window), 1)[0]
+        req = c.top_k_blocks if (budget is None and c.decode_top_k_blocks is None) else (
+            c.decode_top_k_blocks if budget is None else budget)
+        if c.decode_relative_a is not None:
+            scores = block_scores(q_route[None], self.reps, self.nblocks_filled, c.num_kv_heads)
+            ids, vals = relative_threshold_select(scores, self.protected_blocks, req, c.decode_relative_a,
+                                                  c.scale, c.decode_relative_max_blocks,
+                                                  c.decode_relative_union)
+        else:
+            ids, vals = self.select(q_route, req)
         hk, hv = self.history_blocks(ids)
         sink_len = min(c.sink_tokens, self.valid_len)
         recent_len = min(c.recent_tokens, self.valid_len + 1)

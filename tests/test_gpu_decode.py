@@ -23,18 +23,18 @@ pytestmark = pytest.mark.gpu
 
 
 def _make(T, steps, seed, *, quant=False, layout="channel_block", recent=512, sink=64,
-          top_k=32, planted=3, gather_sort=False, decode_budget=None):
+          top_k=32, planted=3, gather_sort=False, decode_budget=None, **policy):
     from nanokv_amd import workload
     from nanokv_amd.sparse import M12Config, M12LayerRuntime
     cfg = M12Config(max_model_len=T + 64, quant_history=quant, quant_scale_layout=layout,
                     recent_tokens=recent, sink_tokens=sink, top_k_blocks=top_k,
-                    gather_sort=gather_sort, decode_top_k_blocks=decode_budget)
+                    gather_sort=gather_sort, decode_top_k_blocks=decode_budget, **policy)
     rt = M12LayerRuntime(0, cfg)
     k, v, q, planted_ids = workload.history(T, seed, num_planted=planted, recent_tokens=recent)
     rt.prefill_first(None, k.cuda(), v.cuda())
     ocfg = O.OracleConfig(recent_tokens=recent, sink_tokens=sink, top_k_blocks=top_k,
                           quant_history=quant and layout == "channel_block",
-                          decode_top_k_blocks=decode_budget)
+                          decode_top_k_blocks=decode_budget, **policy)
     ob = O.M12Oracle(ocfg)
     ob.store_kv(to_np(k), to_np(v), with_reps=False)
     nb = rt.nblocks_filled
@@ -105,6 +105,32 @@ def test_decode_short_history_and_small_windows():
 def test_decode_gather_sort_and_budget():
     rt, ob, _, _, inputs = _make(16384, 3, 22, gather_sort=True, decode_budget=24)
     _run_steps(rt, ob, inputs, 3)
+
+
+@pytest.mark.parametrize("a,cap,union", [(0.97, 48, False), (0.97, 12, True), (0.5, 20, False)])
+def test_decode_relative_threshold_policy(a, cap, union):
+    """decode_relative_a (m12_runtime.py:1015-1031): the kept blocks and the
+    attention over them match the oracle at every step; the count varies."""
+    rt, ob, _, _, inputs = _make(16384, 6, 24, decode_relative_a=a, decode_relative_max_blocks=cap,
+                                 decode_relative_union=union)
+    counts = []
+    qs, ks, vs = inputs
+    for s in range(6):
+        out = rt.decode(qs[s, 0].cuda(), ks[s, 0].cuda(), vs[s, 0].cuda())
+        ids_or, _, o_ref = ob.decode(to_np(qs[s, 0]), to_np(ks[s, 0]), to_np(vs[s, 0]))
+        assert rt.last_block_ids.tolist() == ids_or.tolist(), f"step {s}: ids differ"
+        assert_close_bf16(to_np(out), o_ref)
+        counts.append(len(ids_or))
+    print(f"[relative a={a} cap={cap} union={union}] kept blocks per step: {counts}", flush=True)
+    assert max(counts) <= max(cap, 32 if union else 0)
+
+
+@pytest.mark.parametrize("window", [2, 4])
+def test_decode_query_window_policy(window):
+    """decode_query_window (m12_runtime.py:1176-1189): routing on the mean of
+    the last W decode queries, attention on the current one."""
+    rt, ob, _, _, inputs = _make(8192, 7, 25, decode_query_window=window)
+    _run_steps(rt, ob, inputs, 7)
 
 
 def test_decode_many_steps_ring_wraps():

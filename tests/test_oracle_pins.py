@@ -342,3 +342,52 @@ def test_bf16_probability_rounding_sizes_the_prefill_tolerance():
     assert not (err > PREFILL_TOL["rel"] * np.abs(exact) + PREFILL_TOL["abs_tol"]).any()
     # and with P exact the same comparison is within one bf16 ulp
     assert np.abs(O.bf16_round(exact.astype(np.float32)) - exact).max() <= 2.0 ** -8 * np.abs(exact).max()
+
+
+# ---- relative-threshold decode selection (m12_runtime.py:1015-1031) --------------
+
+@pytest.mark.parametrize("scores,prot,req,a,scale,cap,union,want", [
+    # threshold 5 + ln 0.5 = 4.307: blocks 0 (5.0) and 4 (4.9) pass, in score order
+    ([5.0, 4.0, 1.0, 0.0, 4.9], [], 2, 0.5, 1.0, 48, False, [0, 4]),
+    # union with the first k = 3 by score adds block 1 (4.0)
+    ([5.0, 4.0, 1.0, 0.0, 4.9], [], 3, 0.5, 1.0, 48, True, [0, 4, 1]),
+    # block 0 protected: max 4.9, threshold 4.207 keeps block 4 only
+    ([5.0, 4.0, 1.0, 0.0, 4.9], [0], 2, 0.5, 1.0, 48, False, [4]),
+    # cap 1: only the best candidate can be kept
+    ([5.0, 4.0, 1.0, 0.0, 4.9], [], 2, 0.5, 1.0, 1, False, [0]),
+    # scale 0.5 doubles the margin: 5 + 2 ln 0.5 = 3.614 also keeps block 1
+    ([5.0, 4.0, 1.0, 0.0, 4.9], [], 2, 0.5, 0.5, 48, False, [0, 4, 1]),
+    # exact ties pass together, lower ids first
+    ([3.0, 3.0, 3.0], [], 1, 0.9, 1.0, 48, False, [0, 1, 2]),
+    # every block protected: k = cap = 1 and the -inf threshold keeps block 0
+    ([1.0, 2.0, 3.0], [0, 1, 2], 4, 0.5, 1.0, 48, False, [0]),
+])
+def test_relative_threshold_select_known_answers(scores, prot, req, a, scale, cap, union, want):
+    ids, vals = O.relative_threshold_select(np.array(scores, np.float32), prot, req, a, scale, cap, union)
+    assert ids.tolist() == want
+    s = np.array(scores, np.float32)
+    s[prot] = -np.inf
+    assert np.array_equal(vals, s[ids])
+
+
+def test_relative_threshold_matches_brute_force():
+    """Random cases against a direct statement: every kept block is within the
+    margin and among the first cap by (score desc, id asc); every block within
+    the margin among those first cap is kept."""
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        nb = int(rng.integers(1, 40))
+        s = (rng.standard_normal(nb) * 2).astype(np.float32)
+        prot = sorted(set(rng.integers(0, nb, int(rng.integers(0, 4))).tolist()))
+        a, scale = float(rng.uniform(0.05, 0.95)), float(rng.uniform(0.05, 1.0))
+        cap, req = int(rng.integers(1, 20)), int(rng.integers(1, 20))
+        ids, _ = O.relative_threshold_select(s, prot, req, a, scale, cap, False)
+        sm = s.copy()
+        sm[prot] = -np.inf
+        ranked = sorted(range(nb), key=lambda b: (-float(sm[b]), b))
+        avail = nb - len(prot)
+        first = ranked[:min(cap, max(1, avail))]
+        thr = np.float32(float(sm.max()) + np.log(a) / scale)
+        within = [b for b in first if sm[b] >= thr]
+        k = min(req, max(1, avail))
+        assert ids.tolist() == (within if within else ranked[:k])

@@ -340,11 +340,23 @@ class _SparseCore:
     def _splits(self, nseg: int, nqg: int) -> int:
         if self.cfg.attend_splits is not None:
             return self.cfg.attend_splits
-        # ~900 workgroups per launch (about 3.5 per CU on 256 CUs) measured
-        # best for the 36-layer 32K decode step; never more than one segment
-        # per wavefront.
-        want = max(1, round(900 / (self.store.num_kv_heads * self.nl * nqg)))
-        return max(1, min(-(-nseg // 4), want, 64))
+        # Workgroups per launch measured best on the 36-layer 32K decode step
+        # (tok/s): bf16 ~1440 (5 splits 8850 vs 3 splits 8620), int8_token
+        # ~1440 (8770 vs 8660); per-block int8, whose segments carry half
+        # the bytes and no per-token scales, ~900 (3 splits 9040 vs 5
+        # splits 8730).  Never more than one segment per wavefront.
+        # Workgroups go round-robin over the 8 XCDs with the split index
+        # fastest, so a split count with a factor 4 in common with 8 pins
+        # the splits that carry an extra segment to the same XCDs (4 and 8
+        # splits measured 5% and 14% slower than 5 in bf16): such counts
+        # move up by one.
+        target = 900 if self.cfg.kv_format == "int8" else 1440
+        want = max(1, round(target / (self.store.num_kv_heads * self.nl * nqg)))
+        cap = max(1, min(-(-nseg // 4), 64))
+        s = min(want, cap)
+        if s > 1 and s % 4 == 0:
+            s = s + 1 if s < cap else s - 1
+        return s
 
     def _prefill_splits(self, tq: int, nseg: int) -> int:
         """Split-K for the matrix-core kernel: about 1024 workgroups per launch

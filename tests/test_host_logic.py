@@ -47,6 +47,26 @@ def test_kv_format_mapping():
     assert rt.M12Config(quant_history=True, quant_scale_layout="token").kv_format == "int8_token"
 
 
+def _split_choice(nseg, layers=36, kv_heads=8, nqg=1, **cfg):
+    from types import SimpleNamespace
+    me = SimpleNamespace(cfg=rt.M12Config(**cfg), store=SimpleNamespace(num_kv_heads=kv_heads), nl=layers)
+    return rt._SparseCore._splits(me, nseg, nqg)
+
+
+def test_decode_split_choice():
+    # 36 layers x 8 KV heads, top-32 + sink + 8 recent pieces = 41 segments
+    assert _split_choice(41) == 5                              # ~1440 workgroups
+    assert _split_choice(41, quant_history=True) == 3          # per-block int8: ~900
+    assert _split_choice(41, quant_history=True, quant_scale_layout="token") == 5
+    assert _split_choice(41, attend_splits=8) == 8             # explicit choice kept
+    for layers in range(1, 80):
+        for nseg in (1, 5, 16, 41, 300):
+            s = _split_choice(nseg, layers=layers)
+            assert 1 <= s <= max(1, min(-(-nseg // 4), 64))    # at most one segment per wavefront
+            assert s == 1 or s % 4 != 0                          # never a multiple of 4
+    assert _split_choice(16, layers=4) == 3                    # cap 4 is a multiple of 4: one less
+
+
 @pytest.mark.parametrize("bad", [
     {"dtype": torch.float32}, {"head_dim": 64}, {"block_size": 32}, {"num_heads": 24}, {"r": 3},
 ])

@@ -200,6 +200,33 @@ int64_t nkv_decode_step_workspace_floats(int num_layers, int num_kv_heads, int n
                                          int splits, int nstreams);
 
 /*
+ * The steady-state decode layer-step (recent window full) with the ring
+ * position in device memory, so that every argument is the same from one
+ * step to the next and the call can be captured in a HIP graph and replayed.
+ *
+ * Same work as nkv_decode_step with one range (nkv_select, then nkv_attend
+ * over [selected | sink | the R - 1 recent tokens | the new token]), for
+ * M12LayerRuntime.decode (nanovllm/sparse/m12_runtime.py:1141-1346) once
+ * valid_len >= R - 1.
+ * ring_start : int32 [num_layers] device array: each layer's ring start, the
+ *              physical slot of its oldest recent token, which this step's
+ *              new token overwrites (the attended ring part starts one slot
+ *              after it).  Values are taken mod R.  After the attention a
+ *              one-workgroup kernel on the same stream advances each entry by
+ *              one slot (mod R).
+ * score_keys : as nkv_select, [num_layers][nblocks].
+ * partial_ws : >= nkv_attend_workspace_floats(num_layers, Hkv, Hq, 1, splits)
+ *              floats (splits > 1).
+ * Other arguments as nkv_decode_step.
+ */
+int nkv_decode_step_ring(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
+                         const uint16_t* k_new, const uint16_t* v_new, int nblocks,
+                         const int32_t* protected_ids, int n_protected, int k, int n_hist,
+                         int sink_len, int32_t* ring_start, float scale, int splits,
+                         uint32_t* score_keys, int32_t* out_ids, float* partial_ws, uint16_t* out,
+                         void* stream);
+
+/*
  * Union of per-query selections, for lossless speculative verify.
  *
  * Replaces the host-side union + mask of M12LayerRuntime._gpu_select_per_query
@@ -324,6 +351,43 @@ int nkv_query_summaries(const uint16_t* q, int64_t q_layer_stride, int num_layer
  * runtime or is not mapped for the current device.
  */
 int nkv_host_device_pointer(const void* host_ptr, void** device_ptr);
+
+/* ------------------------------------------------------------------------
+ * Fused elementwise ops of the Qwen3 decoder that calls the layer-step
+ * (nanovllm/models/qwen3.py).  bf16 tensors, contiguous rows, device
+ * pointers; each call is one launch on `stream`.
+ * ---------------------------------------------------------------------- */
+
+/*
+ * RMSNorm of `rows` rows of n elements, optionally after a residual add
+ * (RMSNorm.forward, nanovllm/layers/layernorm.py:17-44):
+ *   s = x (+ residual) in fp32; residual_out = bf16(s) (if non-NULL);
+ *   out = bf16(bf16(s * rsqrt(mean(s^2) + eps)) * weight).
+ * n: a multiple of 8, at most 8192; buffers 16-byte aligned.
+ */
+int nkv_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16_t* weight, uint16_t* out,
+                uint16_t* residual_out, int rows, int n, float eps, void* stream);
+
+/*
+ * Qwen3Attention's q/k RMSNorm and RoPE (nanovllm/models/qwen3.py:99-110,
+ * nanovllm/layers/rotary_embedding.py:6-50) on the fused projection output
+ * qkv [rows][Hq + 2 Hkv][128]: per head of q and k, RMSNorm over the 128 dims
+ * with q_weight / k_weight, then rotate-half RoPE in fp32 with
+ * cos/sin_table [max_position][64] at positions[row] (int64; clamped to
+ * [0, max_position)); v is copied.  Outputs q [rows][Hq][128], k and v
+ * [rows][Hkv][128].
+ */
+int nkv_qk_norm_rope(const uint16_t* qkv, int rows, int num_heads, int num_kv_heads, const uint16_t* q_weight,
+                     const uint16_t* k_weight, const float* cos_table, const float* sin_table, int max_position,
+                     const int64_t* positions, float eps, uint16_t* q, uint16_t* k, uint16_t* v, void* stream);
+
+/*
+ * SiLU-and-mul (nanovllm/layers/activation.py:6-11) of gate_up
+ * [rows][2 intermediate] (gate, then up) -> out [rows][intermediate]:
+ * out = bf16(bf16(g / (1 + e^-g)) * u).  intermediate: a multiple of 8;
+ * buffers 16-byte aligned.
+ */
+int nkv_silu_mul(const uint16_t* gate_up, uint16_t* out, int rows, int intermediate, void* stream);
 
 #ifdef __cplusplus
 }

@@ -114,16 +114,24 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
   const int q0 = qg * p.qpg;
   const int rows = min(p.qpg, p.tq - q0) * p.G;
 
+  // The ring position: the call's, or this layer's ring start in device
+  // memory (reduced mod R, so any stored value addresses a ring slot).
+  int write_slot = p.write_slot, ring_base = p.ring_base;
+  if (p.ring_start != nullptr) {
+    write_slot = static_cast<int>(static_cast<uint32_t>(p.ring_start[layer]) % static_cast<uint32_t>(p.R));
+    ring_base = write_slot + 1 == p.R ? 0 : write_slot + 1;
+  }
+
   // decode's shift+append: the new token (chunk token 0) also goes into the
   // freed ring slot, which no workgroup of this launch reads.
-  if (p.write_slot >= 0 && split == 0 && qg == 0 && wave == 0 && lane < 32) {
+  if (write_slot >= 0 && split == 0 && qg == 0 && wave == 0 && lane < 32) {
     const int which = lane >> 4;
     const int c = lane & 15;
     const uint4* src = reinterpret_cast<const uint4*>(
         (which ? p.v_new : p.k_new) + p.kv_ls * layer + static_cast<int64_t>(h) * kHeadDim);
     uint4* dst = reinterpret_cast<uint4*>(
         (which ? p.rec_v : p.rec_k) + p.rec_ls * layer +
-        (static_cast<int64_t>(h) * p.R + p.write_slot) * kHeadDim);
+        (static_cast<int64_t>(h) * p.R + write_slot) * kHeadDim);
     dst[c] = src[c];
   }
 
@@ -277,7 +285,7 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
         float v = c[i][e];
         bool ok = row_ok && tk < g.vlen && seg_allowed;
         if (g.type == kSegRecent) {
-          int lp = g.off + tk - p.ring_base;
+          int lp = g.off + tk - ring_base;
           if (lp < 0) lp += p.R;
           ok = ok && static_cast<unsigned>(lp - p.rec_lo) < static_cast<unsigned>(p.rec_len);
         } else if (g.type == kSegChunk) {
@@ -502,6 +510,16 @@ __global__ __launch_bounds__(kHeadDim) void attend_merge_kernel(const AttendPara
   p.out[p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d] = f32_to_bf16(A / L);
 }
 
+// Device-ring decode: every layer's ring start moves one slot (mod R) once
+// the step's attention has read it; the next launch on the stream sees it.
+__global__ __launch_bounds__(kWave) void ring_advance_kernel(int32_t* ring_start, int n, int R) {
+  const int i = blockIdx.x * kWave + threadIdx.x;
+  if (i < n) {
+    const int v = static_cast<int>(static_cast<uint32_t>(ring_start[i]) % static_cast<uint32_t>(R));
+    ring_start[i] = v + 1 == R ? 0 : v + 1;
+  }
+}
+
 template <int FMT>
 int launch_fmt(int M, dim3 grid, hipStream_t s, const AttendParams& p) {
   switch (M) {
@@ -530,6 +548,28 @@ void group_shape(int tq, int G, int* qpg, int* M) {
   *qpg = per;
   const int rows = per * G;
   *M = rows <= 4 ? 4 : (rows <= 8 ? 8 : 16);
+}
+
+// The few-query kernel over (split, KV head, layer x query group), then the
+// split merge.
+int launch_grouped(const nkv_store* st, int num_layers, int tq, AttendParams& p, hipStream_t s) {
+  int qpg, M;
+  group_shape(tq, p.G, &qpg, &M);
+  p.qpg = qpg;
+  p.nqg = (tq + qpg - 1) / qpg;
+  dim3 grid(p.splits, st->num_kv_heads, num_layers * p.nqg);
+  int bad = 0;
+  switch (st->kv_format) {
+    case NKV_KV_BF16: bad = launch_fmt<NKV_KV_BF16>(M, grid, s, p); break;
+    case NKV_KV_INT8_CHANNEL: bad = launch_fmt<NKV_KV_INT8_CHANNEL>(M, grid, s, p); break;
+    case NKV_KV_INT8_TOKEN: bad = launch_fmt<NKV_KV_INT8_TOKEN>(M, grid, s, p); break;
+    default: bad = -1;
+  }
+  NKV_CHECK_SUPPORTED(bad == 0, "nkv_attend: unsupported row count %d", M);
+  if (p.splits > 1)
+    hipLaunchKernelGGL(attend_merge_kernel, dim3(st->num_kv_heads, num_layers * p.nqg, qpg * p.G), dim3(kHeadDim),
+                       0, s, p);
+  return NKV_OK;
 }
 
 }  // namespace
@@ -640,6 +680,7 @@ int fill_attend_params(const char* who, const nkv_store* st, int layer0, int num
   p.n_hist = n_hist;
   p.sink_len = sink_len;
   p.ring_base = ring_base;
+  p.ring_start = nullptr;
   p.rec_lo = rec_lo;
   p.rec_len = rec_len;
   p.n_sink_seg = n_sink_seg;
@@ -673,21 +714,42 @@ extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const
     ps.splits = 1;
     if (launch_attend_stream(ps, num_layers, s) == 0) return launch_status("nkv_attend");
   }
-  int qpg, M;
-  group_shape(tq, p.G, &qpg, &M);
-  p.qpg = qpg;
-  p.nqg = (tq + qpg - 1) / qpg;
+  const int lrc = launch_grouped(st, num_layers, tq, p, s);
+  return lrc != NKV_OK ? lrc : launch_status("nkv_attend");
+}
 
-  dim3 grid(splits, st->num_kv_heads, num_layers * p.nqg);
-  int bad = 0;
-  switch (st->kv_format) {
-    case NKV_KV_BF16: bad = launch_fmt<NKV_KV_BF16>(M, grid, s, p); break;
-    case NKV_KV_INT8_CHANNEL: bad = launch_fmt<NKV_KV_INT8_CHANNEL>(M, grid, s, p); break;
-    case NKV_KV_INT8_TOKEN: bad = launch_fmt<NKV_KV_INT8_TOKEN>(M, grid, s, p); break;
-    default: bad = -1;
-  }
-  NKV_CHECK_SUPPORTED(bad == 0, "nkv_attend: unsupported row count %d", M);
-  if (splits > 1)
-    hipLaunchKernelGGL(attend_merge_kernel, dim3(st->num_kv_heads, num_layers * p.nqg, qpg * p.G), dim3(kHeadDim), 0, s, p);
-  return launch_status("nkv_attend");
+extern "C" int nkv_decode_step_ring(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
+                                    const uint16_t* k_new, const uint16_t* v_new, int nblocks,
+                                    const int32_t* protected_ids, int n_protected, int k, int n_hist,
+                                    int sink_len, int32_t* ring_start, float scale, int splits,
+                                    uint32_t* score_keys, int32_t* out_ids, float* partial_ws, uint16_t* out,
+                                    void* stream) {
+  int rc = check_store(st, layer0, num_layers);
+  if (rc != NKV_OK) return rc;
+  NKV_CHECK_ARG(q != nullptr && k_new != nullptr && v_new != nullptr && score_keys != nullptr &&
+                    out_ids != nullptr && out != nullptr && ring_start != nullptr,
+                "nkv_decode_step_ring: q, k_new, v_new, score_keys, out_ids, out and ring_start must be non-NULL");
+  NKV_CHECK_ARG(n_hist >= 1 && n_hist <= k, "nkv_decode_step_ring: n_hist must be in [1, k] (got %d, k=%d)", n_hist,
+                k);
+  const int R = st->recent_tokens;
+  NKV_CHECK_ARG(R >= 2, "nkv_decode_step_ring: needs a recent window of at least 2 tokens");
+  const int64_t q_ls = static_cast<int64_t>(st->num_heads) * kHeadDim;
+  const int64_t kv_ls = static_cast<int64_t>(st->num_kv_heads) * kHeadDim;
+  rc = nkv_select(st, layer0, num_layers, q, q_ls, 1, 0, nblocks, protected_ids, n_protected, k,
+                  NKV_ORDER_SCORE_DESC, score_keys, nullptr, out_ids, nullptr, stream);
+  if (rc != NKV_OK) return rc;
+  // The full window: the R - 1 recent tokens before the write slot, then the
+  // new token.  Write slot 0 / base 1 stand in for the host checks; the
+  // kernel reads each layer's ring start from device memory.
+  AttendParams p;
+  rc = fill_attend_params("nkv_decode_step_ring", st, layer0, num_layers, q, q_ls, 1, k_new, v_new, kv_ls, 1, 0,
+                          out_ids, k, n_hist, nullptr, 0, sink_len, 1, 0, R - 1, scale, splits, partial_ws, out, &p);
+  if (rc != NKV_OK) return rc;
+  p.ring_start = ring_start;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  rc = launch_grouped(st, num_layers, 1, p, s);
+  if (rc != NKV_OK) return rc;
+  hipLaunchKernelGGL(ring_advance_kernel, dim3((num_layers + kWave - 1) / kWave), dim3(kWave), 0, s, ring_start,
+                     num_layers, R);
+  return launch_status("nkv_decode_step_ring");
 }

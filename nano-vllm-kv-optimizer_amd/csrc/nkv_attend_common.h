@@ -52,6 +52,9 @@ struct AttendParams {
   int tq, qpg, nqg;
   int n_chunk, write_slot;
   int n_hist, sink_len, ring_base, rec_lo, rec_len;
+  // non-null: per-layer ring starts in device memory, used instead of
+  // write_slot / ring_base (write slot = start, ring base = start + 1 mod R)
+  const int32_t* ring_start;
   int n_sink_seg, n_rec_seg, nseg;
   int splits;
   float scale_log2;

@@ -19,7 +19,7 @@ CSRC = os.path.join(ROOT, "csrc")
 LIB_PATH = os.path.join(PKG_DIR, "libnanokv.so")
 OBJ_DIR = os.path.join(ROOT, "_build")
 SOURCES = ["nkv_common.hip", "nkv_select.hip", "nkv_attend.hip", "nkv_store.hip", "nkv_prefill.hip",
-           "nkv_decode.hip", "nkv_step.hip"]
+           "nkv_decode.hip", "nkv_step.hip", "nkv_model.hip"]
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

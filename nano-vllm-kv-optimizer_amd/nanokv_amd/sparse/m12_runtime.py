@@ -216,6 +216,8 @@ class _SparseCore:
         self._prot_key = None
         self._prot_dev = None
         self._ws: dict[str, torch.Tensor] = {}
+        self._ring_dev = None       # int32 [nl]: ring starts in device memory (device-ring decode)
+        self._ring_dev_pos = None   # the value every entry of _ring_dev holds
 
     # -- workspaces ---------------------------------------------------------
     def _buf(self, name: str, numel: int, dtype) -> torch.Tensor:
@@ -428,6 +430,49 @@ class _SparseCore:
         self.ring_start = (self.ring_start + 1) % self.cfg.recent_tokens
         self.valid_len += 1
 
+    # -- device-ring decode (capturable in a HIP graph) ----------------------------
+    def decode_ring_ready(self) -> bool:
+        """Steady decode: sink and recent window full, so every argument of a
+        decode step except the ring position repeats from step to step."""
+        return (self.nblocks_filled > 0 and self.valid_len + 1 >= self.cfg.recent_tokens
+                and self.valid_len >= self.cfg.sink_tokens)
+
+    def decode_ring(self, q, k, v, requested: int, *, out=None):
+        """The decode step through nkv_decode_step_ring: q [nl,1,Hq,D], k/v [nl,1,Hkv,D].
+
+        The ring start lives in a device array that the call advances, so the
+        enqueued work is the same every step and can be captured and
+        replayed; advance_ring() is the host side of each replay.  Returns
+        (out, ids [nl,1,requested], n_hist, window)."""
+        if not self.decode_ring_ready():
+            raise RuntimeError("device-ring decode needs a full sink and recent window")
+        if self._ring_dev is None:
+            self._ring_dev = torch.empty(self.nl, dtype=torch.int32, device=self.device)
+            self._ring_dev_pos = None
+        if self._ring_dev_pos != self.ring_start:   # the host moved the ring since (or never synced)
+            self._ring_dev.fill_(self.ring_start)
+            self._ring_dev_pos = self.ring_start
+        nb = self.nblocks_filled
+        n_hist = self.effective_k(requested)
+        w = self.decode_window()
+        splits = self.decode_splits(n_hist)
+        prot, n_prot = self.protected_dev()
+        keys = self._zeroed_keys(self.nl * nb, "/ring")
+        ids = self._buf("ids/ring", self.nl * requested, torch.int32).view(self.nl, 1, requested)
+        part = self._buf("partial/ring", self.store.attend_workspace_floats(self.nl, 1, splits), torch.float32)
+        if out is None:
+            out = torch.empty_like(q)
+        self.store.decode_step_ring(self.layer0, q.contiguous(), k.contiguous(), v.contiguous(), nb, prot, n_prot,
+                                    requested, n_hist, w["sink_len"], self._ring_dev, self.cfg.scale, splits, keys,
+                                    ids, part, out)
+        self.advance_ring()
+        return out, ids, n_hist, w
+
+    def advance_ring(self) -> None:
+        """Host bookkeeping of one device-ring decode step (the device array moved itself)."""
+        self.advance_decode()
+        self._ring_dev_pos = self.ring_start
+
     def chunk_attend(self, q, k, v, ids, ids_stride, n_hist, allowed=None, allowed_stride=0,
                      scale=None):
         """[selected | sink | previous recent | chunk (causal)] (m12_runtime.py:592-639, :725-758).
@@ -503,6 +548,11 @@ class M12LayerRuntime:
         self.q_history: list[torch.Tensor] = []
         self.verify_mode = False
         self.verify_lossless = False
+        # decode through nkv_decode_step_ring once the window is full (same
+        # results; the ring position lives on the device, so a decode step can
+        # be captured in a HIP graph and replayed); host-side selection rules,
+        # gather_sort and query windows keep the regular path
+        self.device_ring = False
         self.last_verify_timings: dict = {}
         self.selector_graph_setup_ms = 0.0
         self.selector_graph_builds = 0
@@ -762,6 +812,8 @@ class M12LayerRuntime:
             q_route = q
         requested = cfg.top_k_blocks if cfg.decode_top_k_blocks is None else cfg.decode_top_k_blocks
         host_rule = cfg.decode_relative_a is not None or (cfg.dynamic_top_k)
+        if self.device_ring and self.device_ring_ready():
+            return self._decode_ring(q, k, v, requested, t0)
         if host_rule:
             ids_cpu, info = self._gpu_select(q_route, dynamic=cfg.dynamic_top_k, budget=requested,
                                              use_relative=cfg.decode_relative_a is not None)
@@ -794,6 +846,50 @@ class M12LayerRuntime:
             "packed_attn_ms": attn_ms,
             "selected_tokens": sel_tokens,
             "total_attend_tokens": sel_tokens + sink_len + rec_len,
+        }
+        o = out[0]
+        if cfg.check_finite_outputs and not bool(torch.isfinite(o).all()):
+            raise RuntimeError("M12 sparse decode output is non-finite")
+        return o
+
+    # -- replaying a captured device-ring decode step -----------------------------
+    def device_ring_ready(self) -> bool:
+        """Whether decode() would take the device-ring entry with device_ring set."""
+        cfg = self.cfg
+        return (cfg.decode_relative_a is None and not cfg.dynamic_top_k and not cfg.gather_sort
+                and cfg.decode_query_window <= 1 and self._core.decode_ring_ready())
+
+    def decode_state(self) -> tuple:
+        """(ring start, valid length, device ring value): the host state a decode step moves."""
+        c = self._core
+        return c.ring_start, c.valid_len, c._ring_dev_pos
+
+    def restore_decode_state(self, state: tuple) -> None:
+        """Undo the host side of a decode step that was captured, not run."""
+        c = self._core
+        c.ring_start, c.valid_len, c._ring_dev_pos = state
+
+    def ring_replayed(self) -> None:
+        """Host side of one replay of a captured device-ring decode step: the
+        ring and length move as in decode(); the ids are re-read on demand."""
+        self._core.advance_ring()
+        self._last_ids_cpu = None
+
+    def _decode_ring(self, q, k, v, requested: int, t0: float) -> torch.Tensor:
+        """decode() through the device-ring entry (same kernels and results)."""
+        cfg = self.cfg
+        out, ids_dev, n_hist, w = self._core.decode_ring(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0),
+                                                         requested)
+        self._set_last_ids(ids_dev[0, 0, :n_hist])
+        if self.record_ids:
+            self.ids_history.append(self.last_block_ids.tolist())
+        ms = (perf_counter() - t0) * 1000.0
+        sel_tokens = n_hist * cfg.block_size
+        self.timings = {
+            "selector_ms": 0.0, "selector_enqueue_ms": 0.0, "d2h_ms": 0.0, "cpu_gather_ms": 0.0,
+            "h2d_pack_ms": 0.0, "h2d_event_spans_cpu_gather": False, "recent_ms": 0.0,
+            "packed_attn_ms": ms, "selected_tokens": sel_tokens,
+            "total_attend_tokens": sel_tokens + w["sink_len"] + w["rec_len"] + 1,
         }
         o = out[0]
         if cfg.check_finite_outputs and not bool(torch.isfinite(o).all()):

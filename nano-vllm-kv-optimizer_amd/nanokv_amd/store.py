@@ -226,6 +226,28 @@ class SparseKVStore:
             _ptr(score_keys), _ptr(out_ids), _ptr(partial_ws), _ptr(out), len(streams), arr),
             "decode_step")
 
+    def decode_step_ring(self, layer0: int, q, k_new, v_new, nblocks: int, prot_dev, n_prot: int, k: int,
+                         n_hist: int, sink_len: int, ring_start, scale: float, splits: int, score_keys, out_ids,
+                         partial_ws, out) -> None:
+        """nkv_decode_step_ring: the steady-state decode step of q.shape[0] layers with
+        their ring starts in `ring_start` (int32 [L] on the device, advanced by the call)."""
+        self._bf16(q, "q")
+        self._bf16(out, "out")
+        nl = q.shape[0]
+        if not (q.is_contiguous() and k_new.is_contiguous() and v_new.is_contiguous()
+                and out.is_contiguous() and out_ids.is_contiguous()):
+            raise ValueError("decode_step_ring: q, k_new, v_new, out and out_ids must be contiguous")
+        if q.shape[1] != 1 or k_new.shape[:2] != (nl, 1) or out.shape != q.shape:
+            raise ValueError("decode_step_ring: expects q/out [L, 1, Hq, D] and k/v [L, 1, Hkv, D]")
+        if out_ids.numel() < nl * k or score_keys.numel() < nl * nblocks:
+            raise ValueError("decode_step_ring: out_ids or score_keys too small")
+        if ring_start.dtype != torch.int32 or ring_start.numel() < nl or ring_start.device != q.device:
+            raise ValueError("decode_step_ring: ring_start must be int32 with one entry per layer, on q's device")
+        _lib.check(self.lib.nkv_decode_step_ring(
+            self._desc_ref, layer0, nl, _ptr(q), _ptr(k_new), _ptr(v_new), nblocks, _ptr(prot_dev), n_prot, k,
+            n_hist, sink_len, _ptr(ring_start), float(scale), splits, _ptr(score_keys), _ptr(out_ids),
+            _ptr(partial_ws), _ptr(out), _stream()), "decode_step_ring")
+
     def decode_step_workspace_floats(self, nl: int, splits: int, nstreams: int) -> int:
         return int(self.lib.nkv_decode_step_workspace_floats(nl, self.num_kv_heads, self.num_heads,
                                                              splits, nstreams))

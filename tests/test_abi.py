@@ -147,3 +147,20 @@ def test_host_device_pointer_rejects_null_without_device_work():
     assert lib.nkv_host_device_pointer(None, ctypes.byref(out)) == _lib.NKV_ERR_ARG
     assert b"non-NULL" in lib.nkv_last_error()
     assert lib.nkv_host_device_pointer(ctypes.c_void_p(8), None) == _lib.NKV_ERR_ARG
+
+
+def test_model_ops_reject_bad_sizes_without_device_work():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(256)     # never dereferenced: the size checks come first
+    assert lib.nkv_rmsnorm(fake, None, fake, fake, None, 1, 12, 1e-6, None) == _lib.NKV_ERR_ARG
+    assert b"multiple of 8" in lib.nkv_last_error()
+    assert lib.nkv_rmsnorm(fake, None, fake, fake, None, 1, 16384, 1e-6, None) == _lib.NKV_ERR_ARG
+    assert lib.nkv_rmsnorm(fake, None, fake, fake, None, 0, 64, 1e-6, None) == _lib.NKV_ERR_ARG
+    assert lib.nkv_rmsnorm(ctypes.c_void_p(258), None, fake, fake, None, 1, 64, 1e-6, None) == _lib.NKV_ERR_ARG
+    assert b"aligned" in lib.nkv_last_error()
+    assert lib.nkv_silu_mul(fake, fake, 1, 12, None) == _lib.NKV_ERR_ARG
+    assert lib.nkv_silu_mul(None, fake, 1, 16, None) == _lib.NKV_ERR_ARG
+    assert lib.nkv_qk_norm_rope(fake, 0, 32, 8, fake, fake, fake, fake, 10, fake, 1e-6, fake, fake, fake,
+                                None) == _lib.NKV_ERR_ARG
+    assert lib.nkv_qk_norm_rope(None, 1, 32, 8, fake, fake, fake, fake, 10, fake, 1e-6, fake, fake, fake,
+                                None) == _lib.NKV_ERR_ARG

@@ -1,0 +1,85 @@
+"""The decoder's fused elementwise kernels against the tensor-op formulas
+they replace (nanovllm/layers/layernorm.py:17-44,
+nanovllm/layers/rotary_embedding.py:6-50, nanovllm/models/qwen3.py:99-110,
+nanovllm/layers/activation.py:6-11), computed with torch on the same GPU.
+
+Copies and sums that do not depend on a reduction order (v, the residual
+output bf16(x + r)) must match bit for bit.  Results after a sum of squares
+may differ from torch's reduction by an fp32 rounding of the mean, which can
+move a bf16 output by one unit in the last place: those are checked to within
+one bf16 ulp (2^-7 relative), with most elements equal.  SiLU uses the same
+exp and division as torch's kernel.  The RoPE formula of the CPU path is
+pinned separately by known answers (tests/test_qwen3_host.py).
+"""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+ULP = 2.0 ** -7
+
+
+def _close(out, ref, min_equal=0.95):
+    o, r = out.float(), ref.float()
+    rel = ((o - r).abs() / r.abs().clamp_min(1e-30)).max().item()
+    eq = (o == r).float().mean().item()
+    assert rel <= ULP, f"max rel diff {rel:.3e}"
+    assert eq >= min_equal, f"only {eq:.3f} of the elements equal"
+
+
+def _rms_ref(x, w, eps, res=None):
+    s = x.float() if res is None else x.float() + res.float()
+    y = (s * torch.rsqrt(s.pow(2).mean(-1, keepdim=True) + eps)).to(torch.bfloat16) * w
+    return y, s.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("n,rows", [(2560, 7), (4096, 1), (8192, 3), (136, 2)])
+def test_rmsnorm_with_and_without_residual(n, rows):
+    from nanokv_amd.qwen3 import rmsnorm_dev
+
+    g = torch.Generator(device="cuda").manual_seed(n + rows)
+    x = (torch.randn(rows, n, generator=g, device="cuda") * 3).bfloat16()
+    r = torch.randn(rows, n, generator=g, device="cuda").bfloat16()
+    w = (1 + 0.1 * torch.randn(n, generator=g, device="cuda")).bfloat16()
+    ref, _ = _rms_ref(x, w, 1e-6)
+    _close(rmsnorm_dev(x, w, 1e-6), ref)
+    out, res = rmsnorm_dev(x, w, 1e-6, r)
+    ref, ref_res = _rms_ref(x, w, 1e-6, r)
+    assert torch.equal(res, ref_res)
+    _close(out, ref)
+
+
+def test_qk_norm_rope_and_v_copy():
+    from nanokv_amd.qwen3 import _rope_table, qk_norm_rope_dev
+
+    T, hq, hkv, D, P = 9, 32, 8, 128, 4096
+    g = torch.Generator(device="cuda").manual_seed(1)
+    qkv = torch.randn(T, (hq + 2 * hkv) * D, generator=g, device="cuda").bfloat16()
+    qw = (1 + 0.1 * torch.randn(D, generator=g, device="cuda")).bfloat16()
+    kw = (1 + 0.1 * torch.randn(D, generator=g, device="cuda")).bfloat16()
+    pos = torch.tensor([0, 1, 2, 63, 64, 1000, 4095, 17, 3000], device="cuda")
+    cos, sin = _rope_table(D, 1e6, P, "cuda")
+    q, k, v = qk_norm_rope_dev(qkv, pos, hq, hkv, qw, kw, 1e-6, cos, sin)
+
+    def ref(x, w):
+        xf = x.float()
+        y = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16) * w
+        c, s = cos[pos].unsqueeze(1), sin[pos].unsqueeze(1)
+        a, b = y.float().chunk(2, dim=-1)
+        return torch.cat((a * c - b * s, b * c + a * s), dim=-1).to(torch.bfloat16)
+
+    x = qkv.view(T, hq + 2 * hkv, D)
+    _close(q, ref(x[:, :hq], qw))
+    _close(k, ref(x[:, hq:hq + hkv], kw))
+    assert torch.equal(v, x[:, hq + hkv:])
+    assert q.is_contiguous() and k.is_contiguous() and v.is_contiguous()
+
+
+def test_silu_mul_matches_torch():
+    from nanokv_amd.qwen3 import silu_mul_dev
+
+    g = torch.Generator(device="cuda").manual_seed(2)
+    gu = (torch.randn(5, 2 * 9728, generator=g, device="cuda") * 4).bfloat16()
+    ref = torch.nn.functional.silu(gu[:, :9728]) * gu[:, 9728:]
+    _close(silu_mul_dev(gu), ref, min_equal=0.999)

@@ -211,9 +211,9 @@ int64_t nkv_decode_step_workspace_floats(int num_layers, int num_kv_heads, int n
  * ring_start : int32 [num_layers] device array: each layer's ring start, the
  *              physical slot of its oldest recent token, which this step's
  *              new token overwrites (the attended ring part starts one slot
- *              after it).  Values are taken mod R.  After the attention a
- *              one-workgroup kernel on the same stream advances each entry by
- *              one slot (mod R).
+ *              after it).  Values are taken mod R.  After the attention the
+ *              split merge (with splits = 1, a one-workgroup kernel) advances
+ *              each entry by one slot (mod R).
  * score_keys : as nkv_select, [num_layers][nblocks].
  * partial_ws : >= nkv_attend_workspace_floats(num_layers, Hkv, Hq, 1, splits)
  *              floats (splits > 1).
@@ -388,6 +388,14 @@ int nkv_qk_norm_rope(const uint16_t* qkv, int rows, int num_heads, int num_kv_he
  * buffers 16-byte aligned.
  */
 int nkv_silu_mul(const uint16_t* gate_up, uint16_t* out, int rows, int intermediate, void* stream);
+
+/*
+ * y [m][n] = x [m][k] . weight [n][k]^T (nn.Linear without bias, the decode-
+ * time projections of nanovllm/layers/linear.py) for 1 <= m <= 4 rows:
+ * fp32 accumulation, bf16 output.  k: a multiple of 8; weight and x 16-byte
+ * aligned.
+ */
+int nkv_gemv(const uint16_t* weight, const uint16_t* x, uint16_t* y, int m, int n, int k, void* stream);
 
 #ifdef __cplusplus
 }

@@ -508,6 +508,13 @@ __global__ __launch_bounds__(kHeadDim) void attend_merge_kernel(const AttendPara
   const int t = q0 + n / p.G;
   const int hh = h * p.G + n % p.G;
   p.out[p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d] = f32_to_bf16(A / L);
+  // device-ring decode: the attention has read this layer's ring start, so
+  // one thread of the layer's first merge workgroup moves it one slot
+  if (p.ring_start != nullptr && h == 0 && qg == 0 && n == 0 && d == 0) {
+    int32_t* rs = const_cast<int32_t*>(p.ring_start) + layer;
+    const int v = static_cast<int>(static_cast<uint32_t>(*rs) % static_cast<uint32_t>(p.R));
+    *rs = v + 1 == p.R ? 0 : v + 1;
+  }
 }
 
 // Device-ring decode: every layer's ring start moves one slot (mod R) once
@@ -747,9 +754,10 @@ extern "C" int nkv_decode_step_ring(const nkv_store* st, int layer0, int num_lay
   if (rc != NKV_OK) return rc;
   p.ring_start = ring_start;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  rc = launch_grouped(st, num_layers, 1, p, s);
+  rc = launch_grouped(st, num_layers, 1, p, s);   // with splits > 1 the merge advances the ring
   if (rc != NKV_OK) return rc;
-  hipLaunchKernelGGL(ring_advance_kernel, dim3((num_layers + kWave - 1) / kWave), dim3(kWave), 0, s, ring_start,
-                     num_layers, R);
+  if (splits == 1)
+    hipLaunchKernelGGL(ring_advance_kernel, dim3((num_layers + kWave - 1) / kWave), dim3(kWave), 0, s, ring_start,
+                       num_layers, R);
   return launch_status("nkv_decode_step_ring");
 }

@@ -14,6 +14,9 @@
 //    fused projection output so that q, k and v are contiguous;
 //  * silu_mul_kernel: SiLU(gate) * up (nanovllm/layers/activation.py:6-11),
 //    bf16(bf16(g / (1 + e^-g)) * u).
+//  * gemv_kernel: the decode-time projections (nn.Linear without bias on
+//    1-4 rows, nanovllm/layers/linear.py) as an HBM-bound matrix-vector
+//    product, fp32 accumulation, bf16 output.
 // The sums of squares are taken in a fixed order of this kernel's own, so
 // a result can differ from a tensor library's reduction by an fp32 rounding.
 #include "nkv_common.h"
@@ -153,6 +156,109 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
   reinterpret_cast<uint4*>(out + row * inter)[c] = pack8(o);
 }
 
+// y[m][r] = sum_k x[m][k] w[r][k] (nn.Linear without bias) for up to 4 rows
+// of x.  A wavefront owns 4 weight rows; each lane streams 16-byte chunks of
+// the 4 rows along k, up to 8 chunks per row in flight per iteration, with
+// the matching x chunks (L1 / L2 hits); fp32 fma accumulation, then a
+// wavefront sum.  SPLITK: the 4 wavefronts of a workgroup share the same 4
+// rows and take a quarter of k each (long rows: more loads in flight per
+// row), summed through LDS; otherwise each wavefront has its own 4 rows.
+// HBM-bound: the weight matrix is read once.
+constexpr int kGemvRows = 4;
+constexpr int kGemvUnroll = 8;
+
+__device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float acc) {
+  float fa[8], fb[8];
+  unpack8(a, fa);
+  unpack8(b, fb);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(fa[e], fb[e], acc);
+  return acc;
+}
+
+template <int MR, bool SPLITK>
+__global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x,
+                                                   uint16_t* __restrict__ y, int n, int k) {
+  __shared__ float s_red[SPLITK ? 4 : 1][MR][kGemvRows];
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int r0 = (SPLITK ? blockIdx.x : blockIdx.x * 4 + wave) * kGemvRows;
+  if (!SPLITK && r0 >= n) return;   // no workgroup barrier on this path
+  const int nc = k >> 3;
+  int cbeg = 0, cend = nc;
+  if (SPLITK) {
+    cbeg = static_cast<int>(static_cast<int64_t>(nc) * wave / 4);
+    cend = static_cast<int>(static_cast<int64_t>(nc) * (wave + 1) / 4);
+  }
+  const uint4* wr[kGemvRows];
+#pragma unroll
+  for (int j = 0; j < kGemvRows; ++j) {
+    const int r = min(r0 + j, n - 1);   // rows past n re-read the last row (not stored)
+    wr[j] = reinterpret_cast<const uint4*>(w + static_cast<int64_t>(r) * k);
+  }
+  const uint4* xv = reinterpret_cast<const uint4*>(x);
+  float acc[MR][kGemvRows];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int j = 0; j < kGemvRows; ++j) acc[m][j] = 0.0f;
+  const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
+  for (int c0 = cbeg + lane; c0 < cend; c0 += kWave * kGemvUnroll) {
+    uint4 a[kGemvUnroll][kGemvRows];
+#pragma unroll
+    for (int u = 0; u < kGemvUnroll; ++u) {
+      const int c = c0 + u * kWave;
+#pragma unroll
+      for (int j = 0; j < kGemvRows; ++j) a[u][j] = c < cend ? wr[j][c] : zero;
+    }
+#pragma unroll
+    for (int u = 0; u < kGemvUnroll; ++u) {
+      const int c = c0 + u * kWave;
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const uint4 xm = c < cend ? xv[static_cast<int64_t>(m) * nc + c] : zero;
+#pragma unroll
+        for (int j = 0; j < kGemvRows; ++j) acc[m][j] = dot8(a[u][j], xm, acc[m][j]);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int j = 0; j < kGemvRows; ++j)
+#pragma unroll
+      for (int o = kWave / 2; o > 0; o >>= 1) acc[m][j] += __shfl_xor(acc[m][j], o);
+  if (SPLITK) {
+    if (lane == 0)
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int j = 0; j < kGemvRows; ++j) s_red[SPLITK ? wave : 0][m][j] = acc[m][j];
+    __syncthreads();
+    if (threadIdx.x < MR * kGemvRows) {
+      const int m = threadIdx.x / kGemvRows, j = threadIdx.x % kGemvRows;
+      const float v = s_red[0][m][j] + s_red[SPLITK ? 1 : 0][m][j] + s_red[SPLITK ? 2 : 0][m][j] +
+                      s_red[SPLITK ? 3 : 0][m][j];
+      if (r0 + j < n) y[static_cast<int64_t>(m) * n + r0 + j] = f32_to_bf16(v);
+    }
+  } else if (lane == 0) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int j = 0; j < kGemvRows; ++j)
+        if (r0 + j < n) y[static_cast<int64_t>(m) * n + r0 + j] = f32_to_bf16(acc[m][j]);
+  }
+}
+
+template <int MR>
+void launch_gemv(const uint16_t* w, const uint16_t* x, uint16_t* y, int n, int k, hipStream_t s) {
+  if (k >= 4096)
+    hipLaunchKernelGGL((gemv_kernel<MR, true>), dim3((n + kGemvRows - 1) / kGemvRows), dim3(256), 0, s, w, x, y, n, k);
+  else
+    hipLaunchKernelGGL((gemv_kernel<MR, false>), dim3((n + 4 * kGemvRows - 1) / (4 * kGemvRows)), dim3(256), 0, s, w,
+                       x, y, n, k);
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -199,4 +305,19 @@ extern "C" int nkv_silu_mul(const uint16_t* gate_up, uint16_t* out, int rows, in
   hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), gate_up, out, chunks, intermediate);
   return launch_status("nkv_silu_mul");
+}
+
+extern "C" int nkv_gemv(const uint16_t* weight, const uint16_t* x, uint16_t* y, int m, int n, int k, void* stream) {
+  NKV_CHECK_ARG(weight != nullptr && x != nullptr && y != nullptr, "nkv_gemv: weight, x and y must be non-NULL");
+  NKV_CHECK_ARG(m >= 1 && m <= 4, "nkv_gemv: m must be in [1, 4] (got %d)", m);
+  NKV_CHECK_ARG(n >= 1 && k >= 8 && k % 8 == 0, "nkv_gemv: n >= 1 and k a positive multiple of 8 (got %d, %d)", n, k);
+  NKV_CHECK_ARG(aligned16(weight) && aligned16(x), "nkv_gemv: weight and x must be 16-byte aligned");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (m) {
+    case 1: launch_gemv<1>(weight, x, y, n, k, s); break;
+    case 2: launch_gemv<2>(weight, x, y, n, k, s); break;
+    case 3: launch_gemv<3>(weight, x, y, n, k, s); break;
+    default: launch_gemv<4>(weight, x, y, n, k, s); break;
+  }
+  return launch_status("nkv_gemv");
 }

@@ -16,8 +16,9 @@ Qwen3MLP, Qwen3DecoderLayer, Qwen3Model, Qwen3ForCausalLM) on one GPU:
 Attention is ``nanokv_amd.attention.Attention``: the M12 runtime on this
 library's kernels, routed by the per-step context.  On the GPU the
 elementwise chains are this library's fused kernels (nkv_rmsnorm,
-nkv_qk_norm_rope, nkv_silu_mul: one launch each, same rounding points); the
-tensor-op formulas below are the CPU path of the same modules.
+nkv_qk_norm_rope, nkv_silu_mul: one launch each, same rounding points) and
+the decode-step projections its HBM-bound GEMV (nkv_gemv); the tensor-op
+formulas below are the CPU path of the same modules.
 
 Weights come from a local checkpoint directory (config.json + *.safetensors
 with the Hugging Face Qwen3 parameter names, packed into the fused
@@ -78,6 +79,31 @@ def qk_norm_rope_dev(qkv: torch.Tensor, positions: torch.Tensor, hq: int, hkv: i
                                             _ptr(pos), float(eps), _ptr(q), _ptr(k), _ptr(v), _stream()),
                "qk_norm_rope")
     return q, k, v
+
+
+def gemv_dev(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """nkv_gemv: x [m, k] (1 <= m <= 4) . weight [n, k]^T -> [m, n]."""
+    x = x.contiguous()
+    m, k = x.shape
+    n = weight.shape[0]
+    y = torch.empty(m, n, dtype=x.dtype, device=x.device)
+    _lib.check(_lib.load().nkv_gemv(_ptr(weight), _ptr(x), _ptr(y), m, n, k, _stream()), "gemv")
+    return y
+
+
+def _gemv_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    return (_fused(x) and x.dim() == 2 and 1 <= x.shape[0] <= 4 and x.shape[1] % 8 == 0
+            and weight.dtype == torch.bfloat16 and weight.is_contiguous())
+
+
+class Linear(nn.Linear):
+    """nn.Linear whose products of 1-4 rows on the GPU (decode steps) run on
+    nkv_gemv; longer inputs (prefill) stay on the library GEMM."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.bias is None and _gemv_ok(x, self.weight):
+            return gemv_dev(x, self.weight)
+        return F.linear(x, self.weight, self.bias)
 
 
 def silu_mul_dev(gate_up: torch.Tensor) -> torch.Tensor:
@@ -196,8 +222,8 @@ class Qwen3Attention(nn.Module):
         self.head_dim = cfg.head_dim
         self.q_size = self.num_heads * self.head_dim
         self.kv_size = self.num_kv_heads * self.head_dim
-        self.qkv_proj = nn.Linear(cfg.hidden_size, self.q_size + 2 * self.kv_size, bias=cfg.attention_bias)
-        self.o_proj = nn.Linear(self.q_size, cfg.hidden_size, bias=False)
+        self.qkv_proj = Linear(cfg.hidden_size, self.q_size + 2 * self.kv_size, bias=cfg.attention_bias)
+        self.o_proj = Linear(self.q_size, cfg.hidden_size, bias=False)
         self.qk_norm = not cfg.attention_bias
         if self.qk_norm:
             self.q_norm = RMSNorm(self.head_dim, cfg.rms_norm_eps)
@@ -229,8 +255,8 @@ class Qwen3MLP(nn.Module):
     def __init__(self, cfg: Qwen3Config):
         super().__init__()
         self.intermediate_size = cfg.intermediate_size
-        self.gate_up_proj = nn.Linear(cfg.hidden_size, 2 * cfg.intermediate_size, bias=False)
-        self.down_proj = nn.Linear(cfg.intermediate_size, cfg.hidden_size, bias=False)
+        self.gate_up_proj = Linear(cfg.hidden_size, 2 * cfg.intermediate_size, bias=False)
+        self.down_proj = Linear(cfg.intermediate_size, cfg.hidden_size, bias=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         gu = self.gate_up_proj(x)
@@ -299,6 +325,8 @@ class Qwen3ForCausalLM(nn.Module):
         return self.model(input_ids, positions)
 
     def compute_logits(self, h: torch.Tensor) -> torch.Tensor:
+        if _gemv_ok(h, self.lm_head_weight):
+            return gemv_dev(h, self.lm_head_weight)
         return F.linear(h, self.lm_head_weight)
 
     # -- sparse runtime wiring and one-sequence driving -------------------------

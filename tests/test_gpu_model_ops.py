@@ -83,3 +83,20 @@ def test_silu_mul_matches_torch():
     gu = (torch.randn(5, 2 * 9728, generator=g, device="cuda") * 4).bfloat16()
     ref = torch.nn.functional.silu(gu[:, :9728]) * gu[:, 9728:]
     _close(silu_mul_dev(gu), ref, min_equal=0.999)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 6144, 2560), (1, 2560, 9728), (3, 1001, 4096), (4, 19456, 2560), (1, 7, 8)])
+def test_gemv_against_float64(m, n, k):
+    """|y - x.W^T| <= 2^-8 |x.W^T| (bf16 output rounding) + 2^-22 sum |x||W|
+    (fp32 accumulation over at most 16384 terms, generous)."""
+    from nanokv_amd.qwen3 import gemv_dev
+
+    g = torch.Generator(device="cuda").manual_seed(m * n + k)
+    x = torch.randn(m, k, generator=g, device="cuda").bfloat16()
+    w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).bfloat16()
+    y = gemv_dev(x, w).double()
+    ref = x.double() @ w.double().T
+    mag = x.double().abs() @ w.double().abs().T
+    err = (y - ref).abs()
+    bound = 2.0 ** -8 * ref.abs() + 2.0 ** -22 * mag + 1e-30
+    assert bool((err <= bound).all()), f"worst err / bound {float((err / bound).max()):.3f}"

@@ -397,6 +397,16 @@ int nkv_silu_mul(const uint16_t* gate_up, uint16_t* out, int rows, int intermedi
  */
 int nkv_gemv(const uint16_t* weight, const uint16_t* x, uint16_t* y, int m, int n, int k, void* stream);
 
+/*
+ * Qwen3MLP's gate|up projection and SiLU-and-mul in one launch for 1 <= m <= 4
+ * rows (nanovllm/models/qwen3.py:125-130, nanovllm/layers/activation.py:6-11):
+ * gate_up_weight [2 intermediate][k] (gate rows, then up rows), x [m][k] ->
+ * y [m][intermediate] = bf16(bf16(silu(g)) * u) with g, u the bf16-rounded
+ * products, the rounding points of nkv_gemv followed by nkv_silu_mul.
+ */
+int nkv_gemv_silu_mul(const uint16_t* gate_up_weight, const uint16_t* x, uint16_t* y, int m, int intermediate,
+                      int k, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -176,13 +176,17 @@ __device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float acc)
   return acc;
 }
 
-template <int MR, bool SPLITK>
+// SILU: w is the fused gate|up weight [2 n][k]; the wave's 4 rows are gate
+// rows r, r + 1 and up rows n + r, n + 1 + r, and the epilogue writes
+// bf16(bf16(silu(bf16 g)) * bf16 u) for rows r, r + 1 of y [m][n] (the
+// rounding points of a bf16 GEMM followed by nkv_silu_mul).
+template <int MR, bool SPLITK, bool SILU = false>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x,
                                                    uint16_t* __restrict__ y, int n, int k) {
   __shared__ float s_red[SPLITK ? 4 : 1][MR][kGemvRows];
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  const int r0 = (SPLITK ? blockIdx.x : blockIdx.x * 4 + wave) * kGemvRows;
+  const int r0 = (SPLITK ? blockIdx.x : blockIdx.x * 4 + wave) * (SILU ? kGemvRows / 2 : kGemvRows);
   if (!SPLITK && r0 >= n) return;   // no workgroup barrier on this path
   const int nc = k >> 3;
   int cbeg = 0, cend = nc;
@@ -193,7 +197,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   const uint4* wr[kGemvRows];
 #pragma unroll
   for (int j = 0; j < kGemvRows; ++j) {
-    const int r = min(r0 + j, n - 1);   // rows past n re-read the last row (not stored)
+    // rows past n re-read the last row (not stored)
+    const int r = SILU ? min(r0 + (j & 1), n - 1) + (j >> 1) * n : min(r0 + j, n - 1);
     wr[j] = reinterpret_cast<const uint4*>(w + static_cast<int64_t>(r) * k);
   }
   const uint4* xv = reinterpret_cast<const uint4*>(x);
@@ -243,11 +248,29 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
     }
   } else if (lane == 0) {
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
+    for (int m = 0; m < MR; ++m) {
+      if constexpr (SILU) {
 #pragma unroll
-      for (int j = 0; j < kGemvRows; ++j)
-        if (r0 + j < n) y[static_cast<int64_t>(m) * n + r0 + j] = f32_to_bf16(acc[m][j]);
+        for (int j = 0; j < 2; ++j) {
+          if (r0 + j >= n) continue;
+          const float g = round_bf16(acc[m][j]);
+          const float u = round_bf16(acc[m][2 + j]);
+          y[static_cast<int64_t>(m) * n + r0 + j] = f32_to_bf16(round_bf16(g / (1.0f + expf(-g))) * u);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kGemvRows; ++j)
+          if (r0 + j < n) y[static_cast<int64_t>(m) * n + r0 + j] = f32_to_bf16(acc[m][j]);
+      }
+    }
   }
+}
+
+template <int MR>
+void launch_gemv_silu(const uint16_t* w, const uint16_t* x, uint16_t* y, int n, int k, hipStream_t s) {
+  const int rows_per_wg = 4 * (kGemvRows / 2);
+  hipLaunchKernelGGL((gemv_kernel<MR, false, true>), dim3((n + rows_per_wg - 1) / rows_per_wg), dim3(256), 0, s, w, x,
+                     y, n, k);
 }
 
 template <int MR>
@@ -320,4 +343,22 @@ extern "C" int nkv_gemv(const uint16_t* weight, const uint16_t* x, uint16_t* y, 
     default: launch_gemv<4>(weight, x, y, n, k, s); break;
   }
   return launch_status("nkv_gemv");
+}
+
+extern "C" int nkv_gemv_silu_mul(const uint16_t* gate_up_weight, const uint16_t* x, uint16_t* y, int m,
+                                 int intermediate, int k, void* stream) {
+  NKV_CHECK_ARG(gate_up_weight != nullptr && x != nullptr && y != nullptr,
+                "nkv_gemv_silu_mul: gate_up_weight, x and y must be non-NULL");
+  NKV_CHECK_ARG(m >= 1 && m <= 4, "nkv_gemv_silu_mul: m must be in [1, 4] (got %d)", m);
+  NKV_CHECK_ARG(intermediate >= 1 && k >= 8 && k % 8 == 0,
+                "nkv_gemv_silu_mul: intermediate >= 1 and k a positive multiple of 8 (got %d, %d)", intermediate, k);
+  NKV_CHECK_ARG(aligned16(gate_up_weight) && aligned16(x), "nkv_gemv_silu_mul: weight and x must be 16-byte aligned");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (m) {
+    case 1: launch_gemv_silu<1>(gate_up_weight, x, y, intermediate, k, s); break;
+    case 2: launch_gemv_silu<2>(gate_up_weight, x, y, intermediate, k, s); break;
+    case 3: launch_gemv_silu<3>(gate_up_weight, x, y, intermediate, k, s); break;
+    default: launch_gemv_silu<4>(gate_up_weight, x, y, intermediate, k, s); break;
+  }
+  return launch_status("nkv_gemv_silu_mul");
 }

@@ -78,6 +78,7 @@ SIGNATURES = {
     "nkv_qk_norm_rope": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _F, _P, _P, _P, _P]),
     "nkv_silu_mul": (_I, [_P, _P, _I, _I, _P]),
     "nkv_gemv": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "nkv_gemv_silu_mul": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "nkv_decode_step_ring": (_I, [_SP, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _F, _I, _P, _P, _P,
                                   _P, _P]),
     "nkv_prefill_attend": (_I, [_SP, _I, _I, _P, _I64, _I, _P, _P, _I64, _P, _I64, _I, _P, _I64,

@@ -91,6 +91,17 @@ def gemv_dev(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     return y
 
 
+def gemv_silu_mul_dev(x: torch.Tensor, gate_up_weight: torch.Tensor) -> torch.Tensor:
+    """nkv_gemv_silu_mul: x [m, k] (1 <= m <= 4), gate|up weight [2 I, k] -> SiLU(gate) * up [m, I]."""
+    x = x.contiguous()
+    m, k = x.shape
+    inter = gate_up_weight.shape[0] // 2
+    y = torch.empty(m, inter, dtype=x.dtype, device=x.device)
+    _lib.check(_lib.load().nkv_gemv_silu_mul(_ptr(gate_up_weight), _ptr(x), _ptr(y), m, inter, k, _stream()),
+               "gemv_silu_mul")
+    return y
+
+
 def _gemv_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:
     return (_fused(x) and x.dim() == 2 and 1 <= x.shape[0] <= 4 and x.shape[1] % 8 == 0
             and weight.dtype == torch.bfloat16 and weight.is_contiguous())
@@ -259,6 +270,8 @@ class Qwen3MLP(nn.Module):
         self.down_proj = Linear(cfg.intermediate_size, cfg.hidden_size, bias=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.gate_up_proj.bias is None and _gemv_ok(x, self.gate_up_proj.weight):
+            return self.down_proj(gemv_silu_mul_dev(x, self.gate_up_proj.weight))   # one launch for both
         gu = self.gate_up_proj(x)
         if _fused(gu) and self.intermediate_size % 8 == 0:
             return self.down_proj(silu_mul_dev(gu))

@@ -100,3 +100,20 @@ def test_gemv_against_float64(m, n, k):
     err = (y - ref).abs()
     bound = 2.0 ** -8 * ref.abs() + 2.0 ** -22 * mag + 1e-30
     assert bool((err <= bound).all()), f"worst err / bound {float((err / bound).max()):.3f}"
+
+
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_gemv_silu_mul_equals_gemv_then_silu_mul(m):
+    """The fused gate|up projection + SiLU-and-mul rounds where the two
+    launches do, so it matches them bit for bit."""
+    from nanokv_amd.qwen3 import gemv_dev, gemv_silu_mul_dev, silu_mul_dev
+
+    g = torch.Generator(device="cuda").manual_seed(31 + m)
+    inter, k = 9728, 2560
+    x = torch.randn(m, k, generator=g, device="cuda").bfloat16()
+    w = (torch.randn(2 * inter, k, generator=g, device="cuda") * 0.05).bfloat16()
+    assert torch.equal(gemv_silu_mul_dev(x, w), silu_mul_dev(gemv_dev(x, w)))
+    # an odd intermediate size (the last row pair is half empty) against torch's SiLU
+    w2 = w[: 2 * 1001].contiguous()
+    gate, up = gemv_dev(x, w2[:1001]), gemv_dev(x, w2[1001:])
+    _close(gemv_silu_mul_dev(x, w2), torch.nn.functional.silu(gate) * up, min_equal=0.99)

@@ -376,6 +376,63 @@ __global__ __launch_bounds__(kStoreThreads) void query_mean_kernel(
   out[out_ls * layer + static_cast<int64_t>(s) * nelem + e] = f64_to_bf16(sum / static_cast<double>(hi - lo));
 }
 
+// The same means with 16-byte loads: a workgroup owns 16 chunks of 8
+// elements and splits the segment's tokens over 16 thread groups, each with 8
+// rows in flight; the groups' fp64 partial sums meet in LDS.  The sums are
+// exact in fp64 (bf16 values of any realistic exponent spread), so the result
+// does not depend on the order and equals query_mean_kernel's.
+constexpr int kQmChunks = 16;
+constexpr int kQmGroups = kStoreThreads / kQmChunks;
+constexpr int kQmUnroll = 8;
+__global__ __launch_bounds__(kStoreThreads) void query_mean8_kernel(
+    const uint16_t* __restrict__ q, int64_t q_ls, int T, int nelem, int nseg,
+    uint16_t* __restrict__ out, int64_t out_ls) {
+  __shared__ double s_part[kQmGroups][kQmChunks * 8];
+  const int cl = threadIdx.x % kQmChunks;
+  const int grp = threadIdx.x / kQmChunks;
+  const int nc = nelem >> 3;
+  const int c = blockIdx.x * kQmChunks + cl;
+  const int s = blockIdx.y;
+  const int layer = blockIdx.z;
+  const int base = T / nseg, extra = T % nseg;
+  const int lo = s * base + min(s, extra);
+  const int hi = lo + base + (s < extra ? 1 : 0);
+  double acc[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+  auto add = [&](const uint4& v) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[2 * i] += static_cast<double>(bf16_lo(w[i]));
+      acc[2 * i + 1] += static_cast<double>(bf16_hi(w[i]));
+    }
+  };
+  if (c < nc) {
+    const uint4* ql = reinterpret_cast<const uint4*>(q + q_ls * layer);
+    int t = lo + grp;
+    for (; t + (kQmUnroll - 1) * kQmGroups < hi; t += kQmUnroll * kQmGroups) {
+      uint4 v[kQmUnroll];
+#pragma unroll
+      for (int u = 0; u < kQmUnroll; ++u) v[u] = ql[static_cast<int64_t>(t + u * kQmGroups) * nc + c];
+#pragma unroll
+      for (int u = 0; u < kQmUnroll; ++u) add(v[u]);
+    }
+    for (; t < hi; t += kQmGroups) add(ql[static_cast<int64_t>(t) * nc + c]);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s_part[grp][cl * 8 + e] = acc[e];
+  __syncthreads();
+  if (threadIdx.x < kQmChunks * 8) {
+    const int c2 = blockIdx.x * kQmChunks + threadIdx.x / 8;
+    if (c2 < nc) {
+      double sum = 0.0;
+#pragma unroll
+      for (int g = 0; g < kQmGroups; ++g) sum += s_part[g][threadIdx.x];
+      out[out_ls * layer + static_cast<int64_t>(s) * nelem + c2 * 8 + threadIdx.x % 8] =
+          f64_to_bf16(sum / static_cast<double>(hi - lo));
+    }
+  }
+}
+
 }  // namespace
 }  // namespace nkv
 
@@ -472,8 +529,15 @@ extern "C" int nkv_query_summaries(const uint16_t* q, int64_t q_layer_stride, in
   NKV_CHECK_SUPPORTED(head_dim == kHeadDim, "nkv_query_summaries: head_dim must be %d", kHeadDim);
   const int nseg = nsegments < T ? nsegments : T;
   const int nelem = num_heads * head_dim;
-  hipLaunchKernelGGL(query_mean_kernel, dim3((nelem + kStoreThreads - 1) / kStoreThreads, nseg, num_layers),
-                     dim3(kStoreThreads), 0, reinterpret_cast<hipStream_t>(stream), q, q_layer_stride, T,
-                     nelem, nseg, out, out_layer_stride);
+  if ((reinterpret_cast<uintptr_t>(q) & 15u) == 0 && q_layer_stride % 8 == 0) {
+    const int nc = nelem / 8;
+    hipLaunchKernelGGL(query_mean8_kernel, dim3((nc + kQmChunks - 1) / kQmChunks, nseg, num_layers),
+                       dim3(kStoreThreads), 0, reinterpret_cast<hipStream_t>(stream), q, q_layer_stride, T, nelem,
+                       nseg, out, out_layer_stride);
+  } else {
+    hipLaunchKernelGGL(query_mean_kernel, dim3((nelem + kStoreThreads - 1) / kStoreThreads, nseg, num_layers),
+                       dim3(kStoreThreads), 0, reinterpret_cast<hipStream_t>(stream), q, q_layer_stride, T,
+                       nelem, nseg, out, out_layer_stride);
+  }
   return launch_status("nkv_query_summaries");
 }

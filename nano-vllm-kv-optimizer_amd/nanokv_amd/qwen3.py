@@ -6,7 +6,8 @@ Qwen3MLP, Qwen3DecoderLayer, Qwen3Model, Qwen3ForCausalLM) on one GPU:
 * fused q/k/v and gate/up projections (plain bf16 GEMMs);
 * per-head RMSNorm of q and k when the projections carry no bias;
 * rotate-half RoPE over the whole head in fp32
-  (nanovllm/layers/rotary_embedding.py:6-50);
+  (nanovllm/layers/rotary_embedding.py:6-50), with YaRN scaling when the
+  config asks for it (rotary_embedding.py:52-185);
 * RMSNorm computed in fp32, with the residual add fused as in
   nanovllm/layers/layernorm.py:17-44 (the bf16 sum becomes the next
   residual);
@@ -33,6 +34,7 @@ from __future__ import annotations
 
 import glob
 import json
+import math
 import os
 from dataclasses import dataclass, fields
 
@@ -151,11 +153,24 @@ class Qwen3Config:
             raise ValueError(f"hidden_act {self.hidden_act!r} is not supported (silu only)")
         if isinstance(self.rope_scaling, dict):
             kind = self.rope_scaling.get("rope_type", self.rope_scaling.get("type"))
-            if kind not in (None, "default"):
-                raise ValueError(f"rope_scaling type {kind!r} is not supported (plain RoPE only)")
+            if kind not in (None, "default", "yarn"):
+                raise ValueError(f"rope_scaling type {kind!r} is not supported (plain RoPE or yarn)")
             self.rope_theta = float(self.rope_scaling.get("rope_theta", self.rope_theta))
         if self.num_attention_heads % self.num_key_value_heads:
             raise ValueError("num_attention_heads must be a multiple of num_key_value_heads")
+
+    @property
+    def yarn(self) -> tuple | None:
+        """(factor, original max positions, beta_fast, beta_slow, attention factor, truncate)
+        for a YaRN config, else None."""
+        r = self.rope_scaling
+        if not isinstance(r, dict) or r.get("rope_type", r.get("type")) != "yarn":
+            return None
+        factor = float(r.get("factor", 1.0))
+        att = r.get("attention_factor")
+        return (factor, int(r.get("original_max_position_embeddings", self.max_position_embeddings)),
+                float(r.get("beta_fast", 32.0)), float(r.get("beta_slow", 1.0)),
+                yarn_attention_factor(factor) if att is None else float(att), bool(r.get("truncate", True)))
 
     @classmethod
     def from_dir(cls, path: str) -> "Qwen3Config":
@@ -191,15 +206,54 @@ class RMSNorm(nn.Module):
 _ROPE_TABLES: dict = {}
 
 
-def _rope_table(head_dim: int, base: float, max_position: int, device) -> tuple:
-    """cos / sin [max_position, head_dim / 2] fp32 on `device`, shared by every
-    layer (built once per shape and device)."""
-    key = (head_dim, float(base), max_position, str(torch.device(device)))
+def yarn_attention_factor(factor: float) -> float:
+    """YaRN's cos/sin scale: 0.1 ln(s) + 1 for s > 1 (Peng et al., 2023)."""
+    return 1.0 if factor <= 1.0 else 0.1 * math.log(factor) + 1.0
+
+
+def yarn_inv_freq(head_dim: int, base: float, factor: float, original_max: int, beta_fast: float = 32.0,
+                  beta_slow: float = 1.0, truncate: bool = True) -> torch.Tensor:
+    """YaRN inverse frequencies (Peng et al., 2023, "YaRN: Efficient Context
+    Window Extension of Large Language Models"): dimension pair i rotates at
+    base^(-2i/D) (extrapolation) for the fast pairs, at that over `factor`
+    (interpolation) for the slow ones, and a linear ramp in between.  The
+    ramp runs over the pairs whose wavelength at `original_max` positions
+    makes between beta_fast and beta_slow turns: the pair index that turns
+    `rot` times is D ln(original_max / (2 pi rot)) / (2 ln base)."""
+    pos_freq = base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim)
+    extrap = 1.0 / pos_freq
+    interp = 1.0 / (factor * pos_freq)
+
+    def pair_for(rot: float) -> float:
+        return head_dim * math.log(original_max / (2.0 * math.pi * rot)) / (2.0 * math.log(base))
+
+    lo, hi = pair_for(beta_fast), pair_for(beta_slow)
+    if truncate:
+        lo, hi = math.floor(lo), math.ceil(hi)
+    lo, hi = max(lo, 0), min(hi, head_dim - 1)
+    if lo == hi:
+        hi += 0.001
+    ramp = ((torch.arange(head_dim // 2, dtype=torch.float32) - lo) / (hi - lo)).clamp(0.0, 1.0)
+    return interp * ramp + extrap * (1.0 - ramp)
+
+
+def _rope_table(head_dim: int, base: float, max_position: int, device, yarn: tuple | None = None) -> tuple:
+    """cos / sin [max_position, head_dim / 2] fp32 on `device` (times YaRN's
+    attention factor with `yarn`), shared by every layer (built once per shape,
+    scaling and device)."""
+    key = (head_dim, float(base), max_position, yarn, str(torch.device(device)))
     t = _ROPE_TABLES.get(key)
     if t is None:
-        inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+        if yarn is None:
+            inv_freq, att = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim)), 1.0
+        else:
+            factor, orig, bf, bs, att, trunc = yarn
+            inv_freq = yarn_inv_freq(head_dim, base, factor, orig, bf, bs, trunc)
         ang = torch.arange(max_position, dtype=torch.float32)[:, None] * inv_freq[None, :]
-        t = _ROPE_TABLES[key] = (ang.cos().to(device), ang.sin().to(device))
+        cos, sin = ang.cos(), ang.sin()
+        if att != 1.0:
+            cos, sin = cos * att, sin * att
+        t = _ROPE_TABLES[key] = (cos.to(device), sin.to(device))
     return t
 
 
@@ -209,12 +263,15 @@ class RotaryEmbedding(nn.Module):
     (nanovllm/layers/rotary_embedding.py:6-50).  The tables are not module
     state, so casting the model to bf16 leaves them fp32."""
 
-    def __init__(self, head_dim: int, base: float, max_position: int):
+    def __init__(self, head_dim: int, base: float, max_position: int, yarn: tuple | None = None):
         super().__init__()
-        self.head_dim, self.base, self.max_position = head_dim, base, max_position
+        self.head_dim, self.base, self.max_position, self.yarn = head_dim, base, max_position, yarn
+
+    def table(self, device) -> tuple:
+        return _rope_table(self.head_dim, self.base, self.max_position, device, self.yarn)
 
     def forward(self, positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor):
-        cos, sin = _rope_table(self.head_dim, self.base, self.max_position, positions.device)
+        cos, sin = self.table(positions.device)
         cos = cos[positions].unsqueeze(1)   # [T, 1, D/2]
         sin = sin[positions].unsqueeze(1)
         return _rotate(q, cos, sin), _rotate(k, cos, sin)
@@ -239,14 +296,13 @@ class Qwen3Attention(nn.Module):
         if self.qk_norm:
             self.q_norm = RMSNorm(self.head_dim, cfg.rms_norm_eps)
             self.k_norm = RMSNorm(self.head_dim, cfg.rms_norm_eps)
-        self.rotary_emb = RotaryEmbedding(self.head_dim, cfg.rope_theta, max_position)
+        self.rotary_emb = RotaryEmbedding(self.head_dim, cfg.rope_theta, max_position, cfg.yarn)
         self.attn = Attention(self.num_heads, self.head_dim, self.head_dim ** -0.5, self.num_kv_heads)
 
     def forward(self, positions: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
         qkv = self.qkv_proj(h)
         if self.qk_norm and self.head_dim == 128 and _fused(qkv):
-            r = self.rotary_emb
-            cos, sin = _rope_table(r.head_dim, r.base, r.max_position, qkv.device)
+            cos, sin = self.rotary_emb.table(qkv.device)
             q, k, v = qk_norm_rope_dev(qkv, positions, self.num_heads, self.num_kv_heads, self.q_norm.weight,
                                        self.k_norm.weight, self.q_norm.eps, cos, sin)
             return self.o_proj(self.attn(q, k, v).flatten(1))
@@ -323,6 +379,8 @@ class Qwen3ForCausalLM(nn.Module):
         super().__init__()
         self.config = cfg
         self.max_position = max(max_position or 0, cfg.max_position_embeddings)
+        if cfg.yarn is not None:   # the extended context YaRN is configured for
+            self.max_position = max(self.max_position, int(cfg.yarn[1] * cfg.yarn[0]))
         self.model = Qwen3Model(cfg, self.max_position)
         if cfg.tie_word_embeddings:
             self.lm_head_weight = self.model.embed_tokens.weight

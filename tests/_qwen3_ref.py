@@ -31,10 +31,21 @@ class RefQwen3:
 
     def _rope(self, x, pos):
         d = self.c.head_dim
-        inv = self.c.rope_theta ** (-torch.arange(0, d, 2, dtype=torch.float64) / d)
+        att = 1.0
+        if self.c.yarn is None:
+            inv = self.c.rope_theta ** (-torch.arange(0, d, 2, dtype=torch.float64) / d)
+        else:   # Hugging Face's YaRN frequencies and attention factor
+            from transformers import Qwen3Config as HFQwen3Config
+            from transformers.modeling_rope_utils import ROPE_INIT_FUNCTIONS
+            hf = HFQwen3Config(rope_scaling=dict(self.c.rope_scaling, rope_theta=self.c.rope_theta),
+                               rope_theta=self.c.rope_theta, head_dim=d,
+                               max_position_embeddings=self.c.max_position_embeddings)
+            inv, att = ROPE_INIT_FUNCTIONS["yarn"](hf, "cpu")
+            inv = inv.double()
         ang = pos.double()[:, None, None] * inv          # [T, 1, D/2]
+        c, s = ang.cos() * att, ang.sin() * att
         a, b = x[..., : d // 2], x[..., d // 2:]
-        return torch.cat((a * ang.cos() - b * ang.sin(), b * ang.cos() + a * ang.sin()), dim=-1)
+        return torch.cat((a * c - b * s, b * c + a * s), dim=-1)
 
     def forward(self, ids: torch.Tensor, phase: str) -> torch.Tensor:
         """ids [T]; phase 'first' | 'chunk' | 'decode'; returns logits [T, vocab] float64."""

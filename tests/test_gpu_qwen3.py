@@ -34,12 +34,18 @@ def _rel(a, b):
     return float(np.linalg.norm(np.asarray(a, np.float64) - b) / np.linalg.norm(b))
 
 
-def test_qwen3_prefill_and_decode_match_float64_reference():
+@pytest.mark.parametrize("rope_scaling", [None, {"rope_type": "yarn", "factor": 8.0,
+                                                  "original_max_position_embeddings": 256}])
+def test_qwen3_prefill_and_decode_match_float64_reference(rope_scaling):
+    """rope_scaling: plain RoPE, or YaRN with the 1027 positions of the test
+    well past its original 256 (the reference restatement takes Hugging
+    Face's YaRN frequencies)."""
     from nanokv_amd.qwen3 import Qwen3Config, Qwen3ForCausalLM, init_random_
     from nanokv_amd.sparse import M12Config
 
     cfg = Qwen3Config(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
-                      num_attention_heads=8, num_key_value_heads=2, max_position_embeddings=4096)
+                      num_attention_heads=8, num_key_value_heads=2,
+                      max_position_embeddings=256 if rope_scaling else 4096, rope_scaling=rope_scaling)
     m12 = M12Config(max_model_len=2048, num_heads=8, num_kv_heads=2)
     model = Qwen3ForCausalLM(cfg)
     init_random_(model, 7)

@@ -114,7 +114,7 @@ def test_config_from_dir_and_unsupported_variants(tmp_path):
     cfg = Qwen3Config.from_dir(str(tmp_path))
     assert cfg.hidden_size == 256 and cfg.rope_theta == 5e5 and cfg.tie_word_embeddings
     with pytest.raises(ValueError, match="rope_scaling"):
-        Qwen3Config(rope_scaling={"rope_type": "yarn", "factor": 4.0})
+        Qwen3Config(rope_scaling={"rope_type": "longrope", "factor": 4.0})
     assert Qwen3Config(rope_scaling={"rope_type": "default", "rope_theta": 7.0}).rope_theta == 7.0
     with pytest.raises(ValueError, match="silu"):
         Qwen3Config(hidden_act="gelu")
@@ -167,3 +167,36 @@ def test_reference_model_detects_a_decode_position_off_by_one():
     assert rel(runs[1][0], runs[0][0]) > 2 * 0.025
     for a, b in zip(runs[1][1], runs[0][1]):
         assert rel(torch.from_numpy(a), torch.from_numpy(b)) > 0.02
+
+
+@pytest.mark.parametrize("factor,orig,theta,extra", [(4.0, 32768, 1e6, {}), (2.0, 4096, 1e4, {}),
+                                                      (8.0, 8192, 5e5, {"beta_fast": 16, "beta_slow": 2}),
+                                                      (4.0, 32768, 1e6, {"truncate": False})])
+def test_yarn_matches_the_transformers_implementation(factor, orig, theta, extra):
+    """YaRN inverse frequencies and attention factor against Hugging Face's
+    own implementation (an independent restatement of the same paper)."""
+    from transformers import Qwen3Config as HFQwen3Config
+    from transformers.modeling_rope_utils import ROPE_INIT_FUNCTIONS
+
+    from nanokv_amd.qwen3 import yarn_attention_factor, yarn_inv_freq
+
+    scaling = {"rope_type": "yarn", "factor": factor, "original_max_position_embeddings": orig, **extra}
+    hf = HFQwen3Config(rope_scaling=dict(scaling, rope_theta=theta), rope_theta=theta, head_dim=128,
+                       max_position_embeddings=int(orig * factor))
+    inv_ref, att_ref = ROPE_INIT_FUNCTIONS["yarn"](hf, "cpu")
+    inv = yarn_inv_freq(128, theta, factor, orig, float(extra.get("beta_fast", 32)),
+                        float(extra.get("beta_slow", 1)), bool(extra.get("truncate", True)))
+    assert torch.allclose(inv, inv_ref.float(), rtol=1e-6, atol=0)
+    assert abs(yarn_attention_factor(factor) - att_ref) < 1e-12
+    cfg = Qwen3Config(rope_theta=theta, rope_scaling=scaling, max_position_embeddings=orig)
+    assert cfg.yarn[0] == factor and cfg.yarn[4] == pytest.approx(att_ref)
+    assert Qwen3ForCausalLM(Qwen3Config(**dict(TINY, rope_scaling=scaling,
+                                                max_position_embeddings=orig))).max_position >= orig * factor
+
+
+def test_yarn_with_factor_one_is_plain_rope():
+    from nanokv_amd.qwen3 import _rope_table
+
+    plain = _rope_table(128, 1e6, 64, "cpu")
+    yarn = _rope_table(128, 1e6, 64, "cpu", (1.0, 4096, 32.0, 1.0, 1.0, True))
+    assert torch.allclose(plain[0], yarn[0], atol=1e-6) and torch.allclose(plain[1], yarn[1], atol=1e-6)

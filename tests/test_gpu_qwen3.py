@@ -126,3 +126,53 @@ def test_qwen3_decode_graph_replays_match_eager_decode():
     assert [rt.valid_len for rt in graphed.runtimes] == [rt.valid_len for rt in eager.runtimes] == [1032] * 2
     graphed.reset()
     assert graphed._graph is None and not graphed.runtimes[0].device_ring
+
+
+def test_from_pretrained_loads_a_local_checkpoint(tmp_path):
+    """A checkpoint directory in the Hugging Face layout (config.json, two
+    safetensors shards, separate q/k/v and gate/up tensors) through
+    from_pretrained: prefill and decode logits equal those of the model built
+    in memory from the same weights."""
+    import json
+
+    from safetensors.torch import save_file
+
+    from nanokv_amd.qwen3 import Qwen3Config, Qwen3ForCausalLM, from_pretrained, init_random_
+    from nanokv_amd.sparse import M12Config
+
+    raw = dict(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+               num_attention_heads=8, num_key_value_heads=2, head_dim=128, max_position_embeddings=4096,
+               tie_word_embeddings=True, architectures=["Qwen3ForCausalLM"], torch_dtype="bfloat16")
+    (tmp_path / "config.json").write_text(json.dumps(raw))
+    cfg = Qwen3Config.from_dir(str(tmp_path))
+    ref = Qwen3ForCausalLM(cfg)
+    init_random_(ref, 21)
+    ref = ref.to(torch.bfloat16)
+    q, kv, inter = 8 * 128, 2 * 128, 1024
+    tensors = {"model.embed_tokens.weight": ref.model.embed_tokens.weight, "model.norm.weight": ref.model.norm.weight}
+    for i, layer in enumerate(ref.model.layers):
+        p = f"model.layers.{i}."
+        qkv = layer.self_attn.qkv_proj.weight
+        gu = layer.mlp.gate_up_proj.weight
+        tensors.update({p + "self_attn.q_proj.weight": qkv[:q], p + "self_attn.k_proj.weight": qkv[q:q + kv],
+                        p + "self_attn.v_proj.weight": qkv[q + kv:], p + "mlp.gate_proj.weight": gu[:inter],
+                        p + "mlp.up_proj.weight": gu[inter:],
+                        p + "self_attn.o_proj.weight": layer.self_attn.o_proj.weight,
+                        p + "self_attn.q_norm.weight": layer.self_attn.q_norm.weight,
+                        p + "self_attn.k_norm.weight": layer.self_attn.k_norm.weight,
+                        p + "mlp.down_proj.weight": layer.mlp.down_proj.weight,
+                        p + "input_layernorm.weight": layer.input_layernorm.weight,
+                        p + "post_attention_layernorm.weight": layer.post_attention_layernorm.weight})
+    names = sorted(tensors)
+    for j, part in enumerate((names[: len(names) // 2], names[len(names) // 2:])):
+        save_file({n: tensors[n].contiguous() for n in part}, str(tmp_path / f"model-{j}.safetensors"))
+
+    m12 = M12Config(max_model_len=2048, num_heads=8, num_kv_heads=2)
+    loaded = from_pretrained(str(tmp_path), m12)
+    ref = ref.to("cuda")
+    ref.attach(m12)
+    prompt = torch.randint(0, 512, (700,), generator=torch.Generator().manual_seed(9)).cuda()
+    la, lb = loaded.prefill(prompt, chunk=512), ref.prefill(prompt, chunk=512)
+    assert torch.equal(la, lb)
+    tok = la.argmax().view(1)
+    assert torch.equal(loaded.decode(tok, 700), ref.decode(tok, 700))

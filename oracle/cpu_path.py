@@ -1,4 +1,4 @@
-"""CPU restatement of the reference's decode layer-step op sequence (TEST / BASELINE ONLY).
+"""CPU restatement of the reference's decode layer-step op sequence (for the tests and the CPU-baseline timing only).
 
 Used by bench.py's ``cpu_baseline`` leg to time the reference's algorithm on
 the host cores of the GPU box; never part of the shipped path.  It performs

@@ -1,0 +1,70 @@
+"""Seeded sweep of decode configurations against the oracle.
+
+Beyond the Qwen3-4B attention shape of the other decode tests: GQA ratios
+1-16, r = 1, 2, 4, 8 representatives, budgets 1-200 (including more than the
+history offers, and more than one wavefront's 64 lanes), explicit attention
+split counts (a multiple of 4, and more splits than segments, so some
+workgroups attend nothing), ragged histories, bf16 and int8 history.
+
+Per decode step: selected ids bit-exact against the oracle, outputs within
+the bf16 bar (tests/_util.assert_close_bf16).  The representatives are the
+GPU's (the rep builder is pinned on its own), so each case checks the
+layer-step itself.
+"""
+
+import pytest
+import torch
+
+from oracle import nkv_oracle as O
+from tests._util import assert_close_bf16, to_np
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+
+# (Hq, Hkv, r, T, top_k, attend_splits, int8, seed)
+CASES = [
+    (16, 16, 4, 3000, 16, 3, False, 1),     # G = 1
+    (32, 16, 2, 5000, 32, 5, False, 2),     # G = 2, r = 2
+    (64, 8, 8, 2500, 8, 2, False, 3),       # G = 8, r = 8
+    (64, 4, 1, 4100, 64, 7, False, 4),      # G = 16, r = 1, a full wavefront of ids
+    (32, 8, 4, 700, 1, 1, False, 5),        # top-1, one split
+    (32, 8, 4, 300, 32, 8, False, 6),       # short history, more splits than segments
+    (32, 8, 4, 9000, 48, 4, False, 7),      # an explicit multiple of 4
+    (32, 4, 4, 6000, 20, None, True, 8),    # int8, G = 8
+    (16, 8, 2, 2049, 32, 6, True, 9),       # int8, ragged last block
+    (32, 8, 4, 20000, 128, None, False, 10),  # k > 64: the sorting-network path
+    (8, 8, 4, 1500, 12, 2, False, 11),      # Hq = Hkv = 8
+    (32, 8, 4, 64 * 40, 200, None, False, 12),  # budget above the 31 selectable blocks
+]
+
+
+@pytest.mark.parametrize("hq,hkv,r,T,top_k,splits,int8,seed", CASES)
+def test_decode_sweep_against_oracle(hq, hkv, r, T, top_k, splits, int8, seed):
+    from nanokv_amd.sparse import M12Config, M12LayerRuntime
+
+    print(f"case Hq={hq} Hkv={hkv} r={r} T={T} k={top_k} splits={splits} int8={int8}", flush=True)
+    cfg = M12Config(max_model_len=T + 64, num_heads=hq, num_kv_heads=hkv, r=r, top_k_blocks=top_k,
+                    attend_splits=splits, quant_history=int8)
+    rt = M12LayerRuntime(0, cfg)
+    g = torch.Generator().manual_seed(seed)
+    k = (torch.randn(T, hkv, D, generator=g) * D ** -0.5).bfloat16()
+    v = (torch.randn(T, hkv, D, generator=g) * D ** -0.5).bfloat16()
+    rt.prefill_first(None, k.cuda(), v.cuda())
+
+    ob = O.M12Oracle(O.OracleConfig(num_heads=hq, num_kv_heads=hkv, r=r, top_k_blocks=top_k,
+                                    quant_history=int8))
+    ob.store_kv(to_np(k), to_np(v), with_reps=False)
+    nb = rt.nblocks_filled
+    assert nb == ob.nblocks_filled
+    ob.reps[:, :nb] = to_np(rt.reps_gpu[:, :nb])
+
+    for step in range(2):
+        q = torch.randn(1, hq, D, generator=g).bfloat16()
+        kn = (torch.randn(1, hkv, D, generator=g) * D ** -0.5).bfloat16()
+        vn = (torch.randn(1, hkv, D, generator=g) * D ** -0.5).bfloat16()
+        out = rt.decode(q.cuda(), kn.cuda(), vn.cuda())
+        ids_or, _, o_ref = ob.decode(to_np(q), to_np(kn), to_np(vn))
+        assert rt.last_block_ids.tolist() == ids_or.tolist(), f"step {step}: ids differ"
+        assert_close_bf16(to_np(out), o_ref)
+        assert rt.valid_len == ob.valid_len

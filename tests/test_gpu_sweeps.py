@@ -1,4 +1,4 @@
-"""Seeded sweep of decode configurations against the oracle.
+"""Seeded sweeps of decode and chunked-prefill configurations against the oracle.
 
 Beyond the Qwen3-4B attention shape of the other decode tests: GQA ratios
 1-16, r = 1, 2, 4, 8 representatives, budgets 1-200 (including more than the
@@ -68,3 +68,46 @@ def test_decode_sweep_against_oracle(hq, hkv, r, T, top_k, splits, int8, seed):
         assert rt.last_block_ids.tolist() == ids_or.tolist(), f"step {step}: ids differ"
         assert_close_bf16(to_np(out), o_ref)
         assert rt.valid_len == ob.valid_len
+
+
+# (Hq, Hkv, r, history T, chunk lengths, top_k, int8, seed)
+PREFILL_CASES = [
+    (16, 16, 4, 1800, (40, 300), 16, False, 21),     # G = 1: 128 tokens per query tile
+    (64, 4, 2, 2500, (17, 130), 32, False, 22),      # G = 16: 8 tokens per query tile
+    (32, 16, 8, 3100, (9, 257), 12, True, 23),       # G = 2, r = 8, int8
+    (8, 8, 1, 900, (2, 64, 65), 8, False, 24),       # two-token chunk, block-aligned and ragged
+]
+
+
+@pytest.mark.parametrize("hq,hkv,r,T,chunks,top_k,int8,seed", PREFILL_CASES)
+def test_prefill_sweep_against_oracle(hq, hkv, r, T, chunks, top_k, int8, seed):
+    """Later prefill chunks (query summaries, selection, [selected | sink |
+    previous recent | causal chunk]) on both attention kernels (few-query
+    kernel for short chunks, matrix cores for long ones) against the oracle:
+    ids bit-exact, outputs within the bf16-probability bar of the prefill
+    tests."""
+    from nanokv_amd.sparse import M12Config, M12LayerRuntime
+    from tests._util import PREFILL_TOL
+
+    print(f"case Hq={hq} Hkv={hkv} r={r} T={T} chunks={chunks} k={top_k} int8={int8}", flush=True)
+    blocks = -(-T // 64) + sum(-(-n // 64) for n in chunks)   # every stored chunk starts a block
+    cfg = M12Config(max_model_len=64 * blocks, num_heads=hq, num_kv_heads=hkv, r=r,
+                    top_k_blocks=top_k, quant_history=int8)
+    rt = M12LayerRuntime(0, cfg)
+    ob = O.M12Oracle(O.OracleConfig(num_heads=hq, num_kv_heads=hkv, r=r, top_k_blocks=top_k,
+                                    quant_history=int8))
+    g = torch.Generator().manual_seed(seed)
+    k = (torch.randn(T, hkv, D, generator=g) * 0.09).bfloat16()
+    v = (torch.randn(T, hkv, D, generator=g) * 0.09).bfloat16()
+    rt.prefill_first(None, k.cuda(), v.cuda())
+    ob.store_kv(to_np(k), to_np(v), with_reps=False)
+    for i, n in enumerate(chunks):
+        nb = rt.nblocks_filled
+        ob.reps[:, :nb] = to_np(rt.reps_gpu[:, :nb])
+        q = torch.randn(n, hq, D, generator=g).bfloat16()
+        kc = (torch.randn(n, hkv, D, generator=g) * 0.09).bfloat16()
+        vc = (torch.randn(n, hkv, D, generator=g) * 0.09).bfloat16()
+        out = rt.prefill_chunk(q.cuda(), kc.cuda(), vc.cuda())
+        ids_or, o_ref = ob.prefill_chunk(to_np(q), to_np(kc), to_np(vc))
+        assert rt.last_prefill_block_ids.tolist() == ids_or.tolist(), f"chunk {i}: ids differ"
+        assert_close_bf16(to_np(out), o_ref, **PREFILL_TOL)

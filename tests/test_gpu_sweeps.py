@@ -1,4 +1,4 @@
-"""Seeded sweeps of decode and chunked-prefill configurations against the oracle.
+"""Seeded sweeps of decode, chunked-prefill and verify configurations against the oracle.
 
 Beyond the Qwen3-4B attention shape of the other decode tests: GQA ratios
 1-16, r = 1, 2, 4, 8 representatives, budgets 1-200 (including more than the
@@ -111,3 +111,49 @@ def test_prefill_sweep_against_oracle(hq, hkv, r, T, chunks, top_k, int8, seed):
         ids_or, o_ref = ob.prefill_chunk(to_np(q), to_np(kc), to_np(vc))
         assert rt.last_prefill_block_ids.tolist() == ids_or.tolist(), f"chunk {i}: ids differ"
         assert_close_bf16(to_np(out), o_ref, **PREFILL_TOL)
+
+
+# (Hq, Hkv, r, history T, draft tokens, top_k, lossless, seed)
+VERIFY_CASES = [
+    (16, 16, 4, 5000, 2, 16, False, 31),   # G = 1, 2 queries
+    (64, 4, 2, 6000, 8, 32, True, 32),     # G = 16: 8 queries = 128 rows, matrix cores, per-query masks
+    (32, 16, 8, 4000, 5, 24, True, 33),    # G = 2, r = 8: 10 rows on the few-query kernel
+]
+
+
+@pytest.mark.parametrize("hq,hkv,r,T,tq,top_k,lossless,seed", VERIFY_CASES)
+def test_verify_sweep_against_oracle(hq, hkv, r, T, tq, top_k, lossless, seed):
+    """Speculative verify (shared or lossless per-query selection), a partial
+    commit, then one decode step, against the oracle."""
+    from nanokv_amd.sparse import M12Config, M12LayerRuntime
+    from tests._util import PREFILL_TOL
+
+    print(f"case Hq={hq} Hkv={hkv} r={r} T={T} tq={tq} k={top_k} lossless={lossless}", flush=True)
+    cfg = M12Config(max_model_len=T + 64, num_heads=hq, num_kv_heads=hkv, r=r, top_k_blocks=top_k)
+    rt = M12LayerRuntime(0, cfg)
+    ob = O.M12Oracle(O.OracleConfig(num_heads=hq, num_kv_heads=hkv, r=r, top_k_blocks=top_k))
+    g = torch.Generator().manual_seed(seed)
+    k = (torch.randn(T, hkv, D, generator=g) * 0.09).bfloat16()
+    v = (torch.randn(T, hkv, D, generator=g) * 0.09).bfloat16()
+    rt.prefill_first(None, k.cuda(), v.cuda())
+    ob.store_kv(to_np(k), to_np(v), with_reps=False)
+    nb = rt.nblocks_filled
+    ob.reps[:, :nb] = to_np(rt.reps_gpu[:, :nb])
+    rt.verify_lossless = lossless
+    q = torch.randn(tq, hq, D, generator=g).bfloat16()
+    kc = (torch.randn(tq, hkv, D, generator=g) * 0.09).bfloat16()
+    vc = (torch.randn(tq, hkv, D, generator=g) * 0.09).bfloat16()
+    out = rt.verify_tokens(q.cuda(), kc.cuda(), vc.cuda())
+    ids_or, o_ref = ob.verify_tokens(to_np(q), to_np(kc), to_np(vc), lossless=lossless)
+    assert rt.last_verify_block_ids.tolist() == ids_or.tolist()
+    assert_close_bf16(to_np(out), o_ref, **PREFILL_TOL)
+    rt.commit_verified(tq - 1)
+    ob.commit_verified(tq - 1)
+    assert rt.valid_len == ob.valid_len
+    q = torch.randn(1, hq, D, generator=g).bfloat16()
+    kn = (torch.randn(1, hkv, D, generator=g) * 0.09).bfloat16()
+    vn = (torch.randn(1, hkv, D, generator=g) * 0.09).bfloat16()
+    out = rt.decode(q.cuda(), kn.cuda(), vn.cuda())
+    ids_or, _, o_ref = ob.decode(to_np(q), to_np(kn), to_np(vn))
+    assert rt.last_block_ids.tolist() == ids_or.tolist()
+    assert_close_bf16(to_np(out), o_ref)

@@ -579,7 +579,12 @@ def from_pretrained(path: str, m12: M12Config | None = None, device="cuda",
     cfg = Qwen3Config.from_dir(path)
     m12 = m12 or M12Config(num_heads=cfg.num_attention_heads, num_kv_heads=cfg.num_key_value_heads,
                            head_dim=cfg.head_dim)
-    model = Qwen3ForCausalLM(cfg, m12.max_model_len)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(dtype)      # built in the target dtype: half the host memory of fp32
+    try:
+        model = Qwen3ForCausalLM(cfg, m12.max_model_len)
+    finally:
+        torch.set_default_dtype(prev)
     load_checkpoint(model, path)
     model.to(device=device, dtype=dtype)
     model.attach(m12, device)

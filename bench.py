@@ -102,6 +102,18 @@ class DeviceEvents:
         self.ev = []
 
 
+def _cpu_model():
+    """The host CPU's model name (lscpu's "Model name", read from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(model, args, qs, ks, vs, seconds):
     """The reference's host-side op sequence timed on this box's cores (bounded sample)."""
     import torch
@@ -141,6 +153,10 @@ def cpu_baseline(model, args, qs, ks, vs, seconds):
         "unit": "tokens/s",
         "us_per_layer_step": round(med_us, 1),
         "cores": torch.get_num_threads(),
+        "torch_threads": torch.get_num_threads(),
+        "host_cpus": os.cpu_count(),
+        "cpus_in_affinity": len(os.sched_getaffinity(0)),
+        "cpu_model": _cpu_model(),
         "kind": "port",
         "sample": (f"{len(times)} layer-steps of the 32K workload ({n_sample} distinct layers, "
                    f"~{seconds:.0f} s): torch-CPU einsum scorer + topk + index_select gather + "
@@ -444,7 +460,7 @@ def main():
                     help="decode: history in HBM (default) or in pinned host memory read in place")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--cpu-layers", type=int, default=4)
+    ap.add_argument("--cpu-layers", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--layer-streams", type=int, default=1,
                     help="streams the decode step's layer ranges are spread over")

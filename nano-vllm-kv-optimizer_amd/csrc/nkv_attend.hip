@@ -39,8 +39,6 @@
 // Same result as the reference's gather + pack + fp32 einsum attention
 // (nanovllm/sparse/m12_runtime.py:1212-1320 and :845-896) up to fp32
 // summation order.
-#include <stdlib.h>
-
 #include <type_traits>
 
 #include "nkv_attend_common.h"
@@ -537,17 +535,6 @@ int launch_fmt(int M, dim3 grid, hipStream_t s, const AttendParams& p) {
   }
 }
 
-// NANOKV_ATTEND_STREAM=1 routes eligible calls to the streaming kernel
-// (measured slower than the per-group kernel on the 32K decode step so far,
-// hence opt-in).
-bool stream_enabled() {
-  static const bool on = [] {
-    const char* e = getenv("NANOKV_ATTEND_STREAM");
-    return e != nullptr && e[0] == '1';
-  }();
-  return on;
-}
-
 // Query rows per group and the template row count for a given (tq, G).
 void group_shape(int tq, int G, int* qpg, int* M) {
   int per = kMaxRows / G;          // queries that fit one MFMA tile
@@ -590,14 +577,7 @@ extern "C" int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads,
   int qpg, M;
   group_shape(tq, num_heads / num_kv_heads, &qpg, &M);
   const int64_t nqg = (tq + qpg - 1) / qpg;
-  const int64_t grouped = static_cast<int64_t>(num_layers) * num_kv_heads * nqg * splits * kMaxRows * kPartStride;
-  // the streaming kernel's partial records (one per pair and workgroup range)
-  const int64_t rows = static_cast<int64_t>(tq) * (num_heads / num_kv_heads);
-  int64_t streamed = 0;
-  if (rows <= kMaxRows)
-    streamed = (static_cast<int64_t>(num_layers) * num_kv_heads + 4 * kMaxStreamWorkgroups - 1) * kMaxRows *
-               kPartStride;
-  return grouped > streamed ? grouped : streamed;
+  return static_cast<int64_t>(num_layers) * num_kv_heads * nqg * splits * kMaxRows * kPartStride;
 }
 
 namespace nkv {
@@ -714,13 +694,6 @@ extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const
                                     rec_len, scale, splits, partial_ws, out, &p);
   if (rc != NKV_OK) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  // bf16 history without a per-query mask: the streaming kernel (whatever
-  // `splits`; partial_ws is sized for it by nkv_attend_workspace_floats)
-  if (st->kv_format == NKV_KV_BF16 && allowed == nullptr && partial_ws != nullptr && stream_enabled()) {
-    AttendParams ps = p;
-    ps.splits = 1;
-    if (launch_attend_stream(ps, num_layers, s) == 0) return launch_status("nkv_attend");
-  }
   const int lrc = launch_grouped(st, num_layers, tq, p, s);
   return lrc != NKV_OK ? lrc : launch_status("nkv_attend");
 }

@@ -164,16 +164,6 @@ __device__ __forceinline__ Seg make_seg(const AttendParams& p, int layer, int h,
 
 }  // namespace attend_detail
 
-// Streaming few-query attention (nkv_decode.hip): persistent wavefronts over
-// the flat (layer, KV head, segment) tile list.  Launches and returns 0, or
-// returns -1 when the call is outside its cases (the caller then uses the
-// per-group kernel).  Its partial records need
-// (layers x Hkv + 4 stream_workgroups(...) - 1) x kMaxRows x kPartStride
-// floats of partial_ws.
-constexpr int kMaxStreamWorkgroups = 1024;
-int launch_attend_stream(const attend_detail::AttendParams& p, int num_layers, hipStream_t s);
-int stream_workgroups(int num_layers, int num_kv_heads);
-
 // Validates the arguments shared by nkv_attend and nkv_prefill_attend and
 // fills the launch parameters (everything except the query grouping, which
 // each kernel chooses).  Returns NKV_OK or an error code with the message set.

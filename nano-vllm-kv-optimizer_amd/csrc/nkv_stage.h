@@ -1,7 +1,7 @@
-// Staging of attention segments through LDS on gfx950, shared by the
-// many-query (nkv_prefill.hip) and the streaming decode (nkv_decode.hip)
-// kernels: the stage-buffer layout, direct global -> LDS copies of a bf16
-// segment, and branch-free visibility bounds.
+// Staging of attention segments through LDS on gfx950, used by the
+// many-query kernel (nkv_prefill.hip) and the few-query kernel's matrix-core
+// P.V (nkv_attend.hip): the stage-buffer layout, direct global -> LDS copies
+// of a bf16 segment, bf16 packing and branch-free visibility bounds.
 #pragma once
 
 #include "nkv_attend_common.h"

@@ -19,7 +19,7 @@ CSRC = os.path.join(ROOT, "csrc")
 LIB_PATH = os.path.join(PKG_DIR, "libnanokv.so")
 OBJ_DIR = os.path.join(ROOT, "_build")
 SOURCES = ["nkv_common.hip", "nkv_select.hip", "nkv_attend.hip", "nkv_store.hip", "nkv_prefill.hip",
-           "nkv_decode.hip", "nkv_step.hip", "nkv_model.hip"]
+           "nkv_step.hip", "nkv_model.hip"]
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -38,7 +38,7 @@ CFLAGS = [
 # Per-source additions.  The prefill kernel's max / min over MFMA results need
 # no signalling-NaN quieting (NaN inputs still reach the output through exp2
 # and the P.V product), which saves a canonicalisation per logit.
-EXTRA_FLAGS = {"nkv_prefill.hip": ["-fno-honor-nans"], "nkv_decode.hip": ["-fno-honor-nans"]}
+EXTRA_FLAGS = {"nkv_prefill.hip": ["-fno-honor-nans"]}
 
 
 def _compile(src: str) -> str:

@@ -83,9 +83,22 @@ def qk_norm_rope_dev(qkv: torch.Tensor, positions: torch.Tensor, hq: int, hkv: i
     return q, k, v
 
 
+def _check_gemv_operands(x: torch.Tensor, weight: torch.Tensor, who: str) -> None:
+    """The GEMV kernels read weight as a dense [n, k] bf16 matrix on x's device."""
+    if x.dim() != 2 or not 1 <= x.shape[0] <= 4 or x.shape[1] % 8:
+        raise ValueError(f"{who}: x must be [m, k] with 1 <= m <= 4 and k a multiple of 8 (got {tuple(x.shape)})")
+    if weight.dim() != 2 or weight.shape[1] != x.shape[1]:
+        raise ValueError(f"{who}: weight must be [n, {x.shape[1]}] (got {tuple(weight.shape)})")
+    if weight.device != x.device or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError(f"{who}: x and weight must be bfloat16 tensors on one device")
+    if not weight.is_contiguous():
+        raise ValueError(f"{who}: weight must be contiguous")
+
+
 def gemv_dev(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """nkv_gemv: x [m, k] (1 <= m <= 4) . weight [n, k]^T -> [m, n]."""
     x = x.contiguous()
+    _check_gemv_operands(x, weight, "gemv")
     m, k = x.shape
     n = weight.shape[0]
     y = torch.empty(m, n, dtype=x.dtype, device=x.device)
@@ -96,6 +109,9 @@ def gemv_dev(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
 def gemv_silu_mul_dev(x: torch.Tensor, gate_up_weight: torch.Tensor) -> torch.Tensor:
     """nkv_gemv_silu_mul: x [m, k] (1 <= m <= 4), gate|up weight [2 I, k] -> SiLU(gate) * up [m, I]."""
     x = x.contiguous()
+    _check_gemv_operands(x, gate_up_weight, "gemv_silu_mul")
+    if gate_up_weight.shape[0] % 2:
+        raise ValueError("gemv_silu_mul: the gate|up weight needs an even number of rows")
     m, k = x.shape
     inter = gate_up_weight.shape[0] // 2
     y = torch.empty(m, inter, dtype=x.dtype, device=x.device)
@@ -106,7 +122,28 @@ def gemv_silu_mul_dev(x: torch.Tensor, gate_up_weight: torch.Tensor) -> torch.Te
 
 def _gemv_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:
     return (_fused(x) and x.dim() == 2 and 1 <= x.shape[0] <= 4 and x.shape[1] % 8 == 0
+            and weight.dim() == 2 and weight.shape[1] == x.shape[1] and weight.device == x.device
             and weight.dtype == torch.bfloat16 and weight.is_contiguous())
+
+
+def prefill_chunk_bounds(n: int, chunk: int) -> list:
+    """[(start, end)] of the prefill chunks of an n-token prompt, none shorter
+    than 2 tokens (the store appends chunks of at least two tokens,
+    m12_runtime.py:420-431): a 1-token tail takes one token from the chunk
+    before it (chunks of 2 merge into one of 3).  Raises ValueError for
+    prompts of fewer than 2 tokens, before anything runs."""
+    if chunk < 2:
+        raise ValueError(f"the prefill chunk must be at least 2 tokens (got {chunk})")
+    if n < 2:
+        raise ValueError(f"a prompt needs at least 2 tokens (got {n})")
+    ends = list(range(chunk, n, chunk)) + [n]
+    if len(ends) > 1 and ends[-1] - ends[-2] == 1:
+        if chunk > 2:
+            ends[-2] -= 1
+        else:
+            del ends[-2]
+    starts = [0] + ends[:-1]
+    return list(zip(starts, ends))
 
 
 class Linear(nn.Linear):
@@ -326,7 +363,8 @@ class Qwen3MLP(nn.Module):
         self.down_proj = Linear(cfg.intermediate_size, cfg.hidden_size, bias=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.gate_up_proj.bias is None and _gemv_ok(x, self.gate_up_proj.weight):
+        if (self.gate_up_proj.bias is None and _gemv_ok(x, self.gate_up_proj.weight)
+                and self.gate_up_proj.weight.shape[0] % 2 == 0):
             return self.down_proj(gemv_silu_mul_dev(x, self.gate_up_proj.weight))   # one launch for both
         gu = self.gate_up_proj(x)
         if _fused(gu) and self.intermediate_size % 8 == 0:
@@ -436,10 +474,11 @@ class Qwen3ForCausalLM(nn.Module):
         n = input_ids.numel()
         if n > self.max_position:
             raise ValueError(f"prompt of {n} tokens exceeds the RoPE table ({self.max_position})")
+        bounds = prefill_chunk_bounds(n, chunk)
         h = None
-        for s in range(0, n, chunk):
-            ids = input_ids[s:s + chunk]
-            pos = torch.arange(s, s + ids.numel(), device=ids.device)
+        for s, e in bounds:
+            ids = input_ids[s:e]
+            pos = torch.arange(s, e, device=ids.device)
             set_context(True, max_seqlen_q=ids.numel(), max_seqlen_k=s + ids.numel())
             h = self(ids, pos)
         return self.compute_logits(h[-1:]).float()[0]

@@ -1,0 +1,63 @@
+"""The exact launch the decode benchmark times, checked against the oracle.
+
+M12ModelRuntime over 36 layers of 32768-token histories (512 blocks each)
+decodes through nkv_decode_step with the automatic attention split count
+(5 for bf16, 3 for the reference int8 scheme), the same seeds and inputs as
+bench.py's default line.  On four sampled layers the selected ids must equal
+the oracle's (value and order) and the outputs must match the fp64 oracle to
+about one bf16 ulp at every step (m12_runtime.py:1141-1346).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import nkv_oracle as O
+from tests._util import assert_close_bf16, to_np
+
+pytestmark = pytest.mark.gpu
+
+L, T, SEED, STEPS = 36, 32768, 2024, 3
+SAMPLED = (0, 13, 26, 35)
+
+
+@pytest.mark.parametrize("quant,splits_expected,rel,abs_tol", [
+    (False, 5, 2.0 ** -7, 2e-5),
+    (True, 3, 2.0 ** -6, 2e-4),
+])
+def test_headline_36_layer_32k_step_matches_oracle(quant, splits_expected, rel, abs_tol):
+    from nanokv_amd import workload
+    from nanokv_amd.sparse import M12Config, M12ModelRuntime
+
+    dev = torch.device("cuda:0")
+    cfg = M12Config(max_model_len=T, top_k_blocks=32, quant_history=quant)
+    model = M12ModelRuntime(L, cfg, device=dev)
+    kh = torch.empty(L, T, 8, 128, dtype=torch.bfloat16, device=dev)
+    vh = torch.empty_like(kh)
+    for i in range(L):
+        k, v, _, _ = workload.history(T, SEED + i, device=dev)
+        kh[i].copy_(k)
+        vh[i].copy_(v)
+    model.prefill(kh, vh)
+    nb = model.nblocks_filled
+    assert nb == 512
+    oracles = {}
+    for i in SAMPLED:
+        ob = O.M12Oracle(O.OracleConfig(quant_history=quant))
+        ob.store_kv(to_np(kh[i]), to_np(vh[i]), with_reps=False)
+        ob.reps[:, :nb] = to_np(model.store.reps[i, :, :nb])
+        oracles[i] = ob
+    del kh, vh
+    n = model.core.effective_k(32)
+    assert model.core.decode_splits(n) == splits_expected
+    qs, ks, vs = workload.decode_inputs(STEPS, SEED, device=dev, layers=L)
+    worst = 0.0
+    for s in range(STEPS):
+        out = model.decode(qs[s], ks[s], vs[s])
+        ids = model.last_ids_dev[:, 0, :model.last_n_selected].cpu()
+        for i, ob in oracles.items():
+            ids_or, _, o_ref = ob.decode(to_np(qs[s, i]), to_np(ks[s, i]), to_np(vs[s, i]))
+            assert ids[i].tolist() == ids_or.tolist(), f"step {s} layer {i}: ids differ"
+            worst = max(worst, assert_close_bf16(to_np(out[i]), o_ref, rel=rel, abs_tol=abs_tol))
+    print(f"[headline 36L x 32K {'int8' if quant else 'bf16'}, {splits_expected} splits] "
+          f"max |err| {worst:.3e}", flush=True)

@@ -391,3 +391,165 @@ def test_relative_threshold_matches_brute_force():
         within = [b for b in first if sm[b] >= thr]
         k = min(req, max(1, avail))
         assert ids.tolist() == (within if within else ranked[:k])
+
+
+# ---- recent window: carry, commit and short-history decode -------------------------
+#
+# Token t (1-based) is tagged by the value t in every K dimension and by the
+# one-hot vector e_t in V, so buffer contents read back as token ids (0 = a
+# slot never written) and, with q = 0, the attention output is the mean of
+# the attended one-hot rows: o[t] = (times token t is attended) / (keys).
+
+def _tiny_cfg(R=4, S=2):
+    return O.OracleConfig(block_size=2, r=1, recent_tokens=R, sink_tokens=S, top_k_blocks=1,
+                          num_heads=2, num_kv_heads=1, head_dim=16, scale=1.0)
+
+
+def _tagged(ids):
+    ids = list(ids)
+    k = np.zeros((len(ids), 1, 16), np.float32)
+    v = np.zeros_like(k)
+    for i, t in enumerate(ids):
+        k[i, 0, :] = t
+        v[i, 0, t] = 1.0
+    return k, v
+
+
+def _recent_tags(ob):
+    return ob.recent_k[:, 0, 0].astype(int).tolist()
+
+
+def _decode_tagged(ob, t):
+    k, v = _tagged([t])
+    _, _, o = ob.decode(np.zeros((1, 2, 16), np.float32), k, v)
+    return o[0, 0]
+
+
+def _counts_vector(counts, n_keys):
+    want = np.zeros(16)
+    for t, c in counts.items():
+        want[t] = c / n_keys
+    return want
+
+
+@pytest.mark.parametrize("chunks,want", [
+    ([[1, 2, 3], [4, 5]], [2, 3, 4, 5]),          # carry 2 from a 3-token window
+    ([[1, 2], [3, 4, 5]], [2, 3, 4, 5]),          # carry 1 from a 2-token window
+    ([[1, 2], [3, 4]], [1, 2, 3, 4]),             # carry the whole 2-token window
+    ([[1, 2], [3, 4, 5, 6, 7]], [4, 5, 6, 7]),    # T >= R: the chunk's last 4
+    ([[1, 2, 3, 4, 5, 6], [7, 8]], [5, 6, 7, 8]),
+    ([[1, 2]], [1, 2, 0, 0]),                     # short window: tail never written
+])
+def test_store_recent_window_known_answers(chunks, want):
+    """Hand-derived from m12_runtime.py:482-503: recent_len = min(R, valid + T);
+    T >= recent_len copies the chunk's last recent_len tokens, else carry =
+    recent_len - T tokens move from recent[old - carry:old] to the front."""
+    ob = O.M12Oracle(_tiny_cfg())
+    for c in chunks:
+        k, v = _tagged(c)
+        ob.store_kv(k, v)
+    assert _recent_tags(ob) == want
+    assert ob.valid_len == sum(len(c) for c in chunks)
+
+
+@pytest.mark.parametrize("pending,n,want", [
+    ([4, 5], 1, [1, 2, 3, 4]),                    # carry 3
+    ([4, 5, 6], 2, [2, 3, 4, 5]),                 # carry 2 from a 3-token window
+    ([4, 5, 6, 7, 8], 5, [5, 6, 7, 8]),           # n >= R: the accepted prefix's last 4
+    ([4, 5], 0, [1, 2, 3, 0]),                    # nothing accepted
+])
+def test_commit_known_answers(pending, n, want):
+    """m12_runtime.py:777-803 on a 3-token window [1, 2, 3, _]."""
+    ob = O.M12Oracle(_tiny_cfg())
+    ob.store_kv(*_tagged([1, 2, 3]))
+    ob.pending = _tagged(pending)
+    ob.commit_verified(n)
+    assert _recent_tags(ob) == want
+    assert ob.valid_len == 3 + max(n, 0) and ob.pending is None
+
+
+def test_short_history_decode_attends_the_shifted_stale_slots():
+    """valid_len + 1 < R: decode shifts the left-aligned window left and reads
+    its last valid_len + 1 slots (m12_runtime.py:1164-1172, :1290-1292), so
+    the prefill tokens slide out of view and never-written slots are attended.
+    R = 4, sink 2, blocks of 2: store [1, 2]; history = block 0 (protected,
+    but k = max(1, 0) = 1 still selects it, the lowest id)."""
+    ob = O.M12Oracle(_tiny_cfg())
+    ob.store_kv(*_tagged([1, 2]))
+    o = _decode_tagged(ob, 3)
+    assert _recent_tags(ob) == [2, 0, 0, 3]
+    assert ob.last_block_ids.tolist() == [0]
+    # keys: block 0 [1, 2] | sink [1, 2] | recent[1:] = [0, 0, 3]
+    assert np.allclose(o, _counts_vector({1: 2, 2: 2, 3: 1}, 7))
+    o = _decode_tagged(ob, 4)
+    assert _recent_tags(ob) == [0, 0, 3, 4]
+    # full-length read now: recent[0:4] = [0, 0, 3, 4]
+    assert np.allclose(o, _counts_vector({1: 2, 2: 2, 3: 1, 4: 1}, 8))
+
+
+def test_decode_then_commit_on_a_short_window():
+    """Decode (right end) then commit (left-aligned carry) while valid_len < R:
+    store [1, 2] -> [1, 2, 0, 0]; decode 3 -> [2, 0, 0, 3] (valid 3); commit
+    one of [4, 5]: old = 3, new = 4, carry 3 -> [2, 0, 0, 4]; decode 6 ->
+    [0, 0, 4, 6].  Committing two instead: carry 2 -> [0, 0, 4, 5]."""
+    for n, after_commit, after_decode in ((1, [2, 0, 0, 4], [0, 0, 4, 6]),
+                                          (2, [0, 0, 4, 5], [0, 4, 5, 6])):
+        ob = O.M12Oracle(_tiny_cfg())
+        ob.store_kv(*_tagged([1, 2]))
+        _decode_tagged(ob, 3)
+        ob.pending = _tagged([4, 5])
+        ob.commit_verified(n)
+        assert _recent_tags(ob) == after_commit
+        o = _decode_tagged(ob, 6)
+        assert _recent_tags(ob) == after_decode
+        counts = {1: 2, 2: 2}
+        for t in after_decode:
+            if t:
+                counts[t] = counts.get(t, 0) + 1
+        assert np.allclose(o, _counts_vector(counts, 8))
+
+
+def test_store_and_commit_keep_the_last_tokens_left_aligned():
+    """Closed form over random store / commit sequences with no decode: after
+    every call recent[:min(R, valid_len)] is the last min(R, valid_len) tokens
+    of the concatenated stream."""
+    rng = np.random.default_rng(11)
+    for _ in range(300):
+        R = int(rng.choice([2, 3, 4, 5, 8]))
+        ob = O.M12Oracle(_tiny_cfg(R=R))
+        stream = []
+        nxt = 1
+        for op in range(int(rng.integers(1, 7))):
+            if op == 0 or rng.random() < 0.5:
+                T = int(rng.integers(2, 2 * R + 2))
+                ids = list(range(nxt, nxt + T))
+                ob.store_kv(*_tagged([t % 15 + 1 for t in ids]))
+                stream += ids
+            else:
+                tq = int(rng.integers(1, 2 * R + 1))
+                n = int(rng.integers(0, tq + 1))
+                ids = list(range(nxt, nxt + tq))
+                ob.pending = _tagged([t % 15 + 1 for t in ids])
+                ob.commit_verified(n)
+                stream += ids[:n]
+                T = tq
+            nxt += T
+            m = min(R, ob.valid_len)
+            assert ob.valid_len == len(stream)
+            assert _recent_tags(ob)[:m] == [t % 15 + 1 for t in stream[len(stream) - m:]]
+
+
+def test_query_summary_rounding_against_torch_mean():
+    """The summary is the bf16 rounding of the exact mean; torch's bf16 mean
+    (fp32 accumulation, the reference's q.mean, m12_runtime.py:53-67) agrees
+    on all but rare elements whose exact mean lies next to a bf16 rounding
+    boundary, and there by one bf16 ulp (measured: 1 of 12288 on three
+    4096-query chunks)."""
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(4096, 32, 128, generator=g).to(torch.bfloat16)
+    ref = q.mean(dim=0).float().numpy()
+    ours = O.query_summaries(q.float().numpy(), 1)[0]
+    diff = ref != ours
+    assert diff.mean() <= 1e-3
+    ulp = np.abs(O.bf16_round(ours * (1 + 2.0 ** -7)) - ours)
+    assert (np.abs(ref - ours)[diff] <= ulp[diff] * 1.0001).all()

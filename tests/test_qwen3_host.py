@@ -200,3 +200,34 @@ def test_yarn_with_factor_one_is_plain_rope():
     plain = _rope_table(128, 1e6, 64, "cpu")
     yarn = _rope_table(128, 1e6, 64, "cpu", (1.0, 4096, 32.0, 1.0, 1.0, True))
     assert torch.allclose(plain[0], yarn[0], atol=1e-6) and torch.allclose(plain[1], yarn[1], atol=1e-6)
+
+
+def test_prefill_chunk_plan_never_leaves_a_one_token_chunk():
+    from nanokv_amd.qwen3 import prefill_chunk_bounds
+
+    for n in range(2, 40):
+        for chunk in range(2, 12):
+            b = prefill_chunk_bounds(n, chunk)
+            assert b[0][0] == 0 and b[-1][1] == n
+            assert all(e0 == s1 for (_, e0), (s1, _) in zip(b, b[1:])), (n, chunk, b)
+            assert all(e - s >= 2 for s, e in b), (n, chunk, b)
+            assert all(e - s <= max(chunk, 3) for s, e in b), (n, chunk, b)
+    assert prefill_chunk_bounds(4097, 4096) == [(0, 4095), (4095, 4097)]
+    assert prefill_chunk_bounds(8192, 4096) == [(0, 4096), (4096, 8192)]
+    with pytest.raises(ValueError):
+        prefill_chunk_bounds(1, 4096)
+    with pytest.raises(ValueError):
+        prefill_chunk_bounds(100, 1)
+
+
+def test_gemv_rejects_mismatched_weights_before_launching():
+    from nanokv_amd.qwen3 import _gemv_ok, gemv_dev, gemv_silu_mul_dev
+
+    x = torch.zeros(1, 64, dtype=torch.bfloat16)
+    for bad in (torch.zeros(16, 32, dtype=torch.bfloat16), torch.zeros(16, 64, dtype=torch.float32),
+                torch.zeros(64, dtype=torch.bfloat16), torch.zeros(64, 16, dtype=torch.bfloat16).t()):
+        assert not _gemv_ok(x, bad)
+        with pytest.raises(ValueError):
+            gemv_dev(x, bad)
+    with pytest.raises(ValueError):
+        gemv_silu_mul_dev(x, torch.zeros(15, 64, dtype=torch.bfloat16))

@@ -281,6 +281,37 @@ int64_t nkv_prefill_workspace_floats(int num_layers, int num_kv_heads, int num_h
                                      int splits);
 
 /*
+ * Exact attention over caller-packed keys: M12LayerRuntime._fused_attention
+ * (nanovllm/sparse/m12_runtime.py:845-896), the reference's inspectable
+ * attention over [selected | sink | recent | chunk] that its packing paths
+ * and tests call.
+ *
+ * q    : bf16 [tq][num_heads][D];  k, v : bf16 [s_len][num_kv_heads][D]
+ *        (token-major, as the reference packs them).
+ * Query t, head hq (KV head hq / G) sees key j iff j - causal_from <= t and
+ * (mask == NULL or mask[t][j] == 0): the reference's mask
+ * (cols >= t + causal_from + 1) & (cols >= causal_from), OR'd with its
+ * attn_mask (True = disallowed).  causal_from >= s_len = every key visible
+ * (the decode fast path).
+ * mask : uint8 [tq][s_len], nonzero = hidden, or NULL.
+ * out  : bf16 [tq][num_heads][D].
+ * Queries of more than 16 / G tokens run on the matrix-core kernel (P enters
+ * P.V rounded to bf16, as flash-attention's; the reference's torch backend is
+ * fp32), fewer on the few-query kernel (fp32-accurate P.V).  splits: as
+ * nkv_attend / nkv_prefill_attend; partial_ws >=
+ * nkv_attend_packed_workspace_floats(...) floats when splits > 1.
+ * Constraints: G = num_heads / num_kv_heads in {1, 2, 4, 8, 16}, D = 128,
+ *              1 <= tq <= 65536, 1 <= s_len <= 2^20.
+ */
+int nkv_attend_packed(int num_heads, int num_kv_heads, const uint16_t* q, int tq,
+                      const uint16_t* k, const uint16_t* v, int s_len, int causal_from,
+                      const uint8_t* mask, float scale, int splits, float* partial_ws,
+                      uint16_t* out, void* stream);
+
+/* Floats of partial_ws needed by nkv_attend_packed (0 when splits == 1). */
+int64_t nkv_attend_packed_workspace_floats(int num_heads, int num_kv_heads, int tq, int splits);
+
+/*
  * Append one prefill chunk to the history of `num_layers` layers.
  *
  * Replaces the history / quantisation / sink part of M12LayerRuntime._store_kv

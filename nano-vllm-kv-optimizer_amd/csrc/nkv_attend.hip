@@ -287,7 +287,9 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
           if (lp < 0) lp += p.R;
           ok = ok && static_cast<unsigned>(lp - p.rec_lo) < static_cast<unsigned>(p.rec_len);
         } else if (g.type == kSegChunk) {
-          ok = ok && (g.off + tk) <= my_t;
+          ok = ok && (g.off + tk) - p.causal_off <= my_t;
+          if (ok && p.tok_mask != nullptr)
+            ok = p.tok_mask[static_cast<int64_t>(my_t) * p.n_chunk + g.off + tk] == 0;
         }
         if (FMT == NKV_KV_INT8_TOKEN && int8_seg)
           v *= f16_bits_to_f32(p.k_tscale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap * kBlock +
@@ -544,29 +546,29 @@ void group_shape(int tq, int G, int* qpg, int* M) {
   *M = rows <= 4 ? 4 : (rows <= 8 ? 8 : 16);
 }
 
+}  // namespace
+
 // The few-query kernel over (split, KV head, layer x query group), then the
 // split merge.
-int launch_grouped(const nkv_store* st, int num_layers, int tq, AttendParams& p, hipStream_t s) {
+int launch_grouped(int hkv, int kv_format, int num_layers, int tq, AttendParams& p, hipStream_t s) {
   int qpg, M;
   group_shape(tq, p.G, &qpg, &M);
   p.qpg = qpg;
   p.nqg = (tq + qpg - 1) / qpg;
-  dim3 grid(p.splits, st->num_kv_heads, num_layers * p.nqg);
+  dim3 grid(p.splits, hkv, num_layers * p.nqg);
   int bad = 0;
-  switch (st->kv_format) {
+  switch (kv_format) {
     case NKV_KV_BF16: bad = launch_fmt<NKV_KV_BF16>(M, grid, s, p); break;
     case NKV_KV_INT8_CHANNEL: bad = launch_fmt<NKV_KV_INT8_CHANNEL>(M, grid, s, p); break;
     case NKV_KV_INT8_TOKEN: bad = launch_fmt<NKV_KV_INT8_TOKEN>(M, grid, s, p); break;
     default: bad = -1;
   }
-  NKV_CHECK_SUPPORTED(bad == 0, "nkv_attend: unsupported row count %d", M);
+  NKV_CHECK_SUPPORTED(bad == 0, "nkv_attend: unsupported row count %d / kv_format %d", M, kv_format);
   if (p.splits > 1)
-    hipLaunchKernelGGL(attend_merge_kernel, dim3(st->num_kv_heads, num_layers * p.nqg, qpg * p.G), dim3(kHeadDim),
-                       0, s, p);
+    hipLaunchKernelGGL(attend_merge_kernel, dim3(hkv, num_layers * p.nqg, qpg * p.G), dim3(kHeadDim), 0, s, p);
   return NKV_OK;
 }
 
-}  // namespace
 }  // namespace nkv
 
 using namespace nkv;
@@ -675,6 +677,8 @@ int fill_attend_params(const char* who, const nkv_store* st, int layer0, int num
   p.nseg = nseg;
   p.splits = splits;
   p.scale_log2 = scale * 1.4426950408889634f;
+  p.causal_off = 0;
+  p.tok_mask = nullptr;
   return NKV_OK;
 }
 
@@ -694,7 +698,7 @@ extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const
                                     rec_len, scale, splits, partial_ws, out, &p);
   if (rc != NKV_OK) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int lrc = launch_grouped(st, num_layers, tq, p, s);
+  const int lrc = launch_grouped(st->num_kv_heads, st->kv_format, num_layers, tq, p, s);
   return lrc != NKV_OK ? lrc : launch_status("nkv_attend");
 }
 
@@ -727,10 +731,71 @@ extern "C" int nkv_decode_step_ring(const nkv_store* st, int layer0, int num_lay
   if (rc != NKV_OK) return rc;
   p.ring_start = ring_start;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  rc = launch_grouped(st, num_layers, 1, p, s);   // with splits > 1 the merge advances the ring
+  rc = launch_grouped(st->num_kv_heads, st->kv_format, num_layers, 1, p, s);   // with splits > 1 the merge advances the ring
   if (rc != NKV_OK) return rc;
   if (splits == 1)
     hipLaunchKernelGGL(ring_advance_kernel, dim3((num_layers + kWave - 1) / kWave), dim3(kWave), 0, s, ring_start,
                        num_layers, R);
   return launch_status("nkv_decode_step_ring");
+}
+
+// Caller-packed keys: every key is a chunk key (token-major [s_len][Hkv][D]),
+// visible to query t iff key - causal_from <= t and mask[t][key] == 0.
+// Queries whose rows exceed one 16-row MFMA tile per KV head go to the
+// matrix-core kernel, the others to the few-query kernel.
+namespace {
+bool packed_uses_prefill(int tq, int G) { return tq * G > kMaxRows; }
+}  // namespace
+
+extern "C" int64_t nkv_attend_packed_workspace_floats(int num_heads, int num_kv_heads, int tq, int splits) {
+  if (num_kv_heads < 1 || num_heads < num_kv_heads || num_heads % num_kv_heads != 0 || tq < 1 || splits < 1)
+    return 0;
+  if (packed_uses_prefill(tq, num_heads / num_kv_heads))
+    return nkv_prefill_workspace_floats(1, num_kv_heads, num_heads, tq, splits);
+  return splits == 1 ? 0 : nkv_attend_workspace_floats(1, num_kv_heads, num_heads, tq, splits);
+}
+
+extern "C" int nkv_attend_packed(int num_heads, int num_kv_heads, const uint16_t* q, int tq, const uint16_t* k,
+                                 const uint16_t* v, int s_len, int causal_from, const uint8_t* mask, float scale,
+                                 int splits, float* partial_ws, uint16_t* out, void* stream) {
+  NKV_CHECK_ARG(num_kv_heads >= 1 && num_heads >= num_kv_heads && num_heads % num_kv_heads == 0,
+                "nkv_attend_packed: num_heads (%d) must be a positive multiple of num_kv_heads (%d)", num_heads,
+                num_kv_heads);
+  const int G = num_heads / num_kv_heads;
+  NKV_CHECK_SUPPORTED(G == 1 || G == 2 || G == 4 || G == 8 || G == 16,
+                      "nkv_attend_packed: query heads per KV head must be 1, 2, 4, 8 or 16 (got %d)", G);
+  NKV_CHECK_ARG(q != nullptr && k != nullptr && v != nullptr && out != nullptr,
+                "nkv_attend_packed: q, k, v and out must be non-NULL");
+  NKV_CHECK_ARG(tq >= 1 && tq <= 65536, "nkv_attend_packed: tq must be in [1, 65536] (got %d)", tq);
+  NKV_CHECK_ARG(s_len >= 1 && s_len <= (1 << 20), "nkv_attend_packed: s_len must be in [1, 2^20] (got %d)", s_len);
+  NKV_CHECK_ARG(causal_from >= 0, "nkv_attend_packed: causal_from must be >= 0 (got %d)", causal_from);
+  NKV_CHECK_ARG(splits >= 1 && splits <= 64, "nkv_attend_packed: splits must be in [1, 64] (got %d)", splits);
+  NKV_CHECK_ARG(splits == 1 || partial_ws != nullptr, "nkv_attend_packed: splits > 1 needs partial_ws");
+  AttendParams p = {};
+  p.q = q;
+  p.k_new = k;
+  p.v_new = v;
+  p.partial = partial_ws;
+  p.out = out;
+  p.hkv = num_kv_heads;
+  p.G = G;
+  p.cap = 1;
+  p.S = 0;
+  p.R = 1;
+  p.tq = tq;
+  p.qpg = 1;
+  p.nqg = tq;
+  p.n_chunk = s_len;
+  p.write_slot = -1;
+  p.ring_start = nullptr;
+  p.nseg = (s_len + kBlock - 1) / kBlock;
+  p.splits = splits;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  // keys past causal_from + tq - 1 are hidden from every query
+  p.causal_off = causal_from < s_len ? causal_from : s_len;
+  p.tok_mask = mask;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int rc = packed_uses_prefill(tq, G) ? launch_prefill(num_kv_heads, NKV_KV_BF16, 1, tq, p, s)
+                                            : launch_grouped(num_kv_heads, NKV_KV_BF16, 1, tq, p, s);
+  return rc != NKV_OK ? rc : launch_status("nkv_attend_packed");
 }

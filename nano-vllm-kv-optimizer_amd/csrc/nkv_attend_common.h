@@ -58,6 +58,12 @@ struct AttendParams {
   int n_sink_seg, n_rec_seg, nseg;
   int splits;
   float scale_log2;
+  // chunk visibility: query t sees chunk token c iff c - causal_off <= t
+  // (0 for prefill / verify / decode chunks; caller-packed keys put their
+  // causal start here) and, with tok_mask != NULL, tok_mask[t][c] == 0
+  // (uint8 [tq][n_chunk], nonzero = hidden)
+  int causal_off;
+  const uint8_t* tok_mask;
 };
 
 __device__ __forceinline__ void wave_lds_sync() {
@@ -163,6 +169,13 @@ __device__ __forceinline__ Seg make_seg(const AttendParams& p, int layer, int h,
 }
 
 }  // namespace attend_detail
+
+// Launch the few-query kernel (+ split merge) / the matrix-core kernel (+
+// split merge) over filled parameters; hkv / kv_format describe the keys.
+int launch_grouped(int hkv, int kv_format, int num_layers, int tq, attend_detail::AttendParams& p,
+                   hipStream_t s);
+int launch_prefill(int hkv, int kv_format, int num_layers, int tq, attend_detail::AttendParams& p,
+                   hipStream_t s);
 
 // Validates the arguments shared by nkv_attend and nkv_prefill_attend and
 // fills the launch parameters (everything except the query grouping, which

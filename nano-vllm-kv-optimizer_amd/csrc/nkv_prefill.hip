@@ -164,7 +164,7 @@ __device__ __forceinline__ bool needs_mask(const AttendParams& p, const Seg& g, 
     case kSegHist: return g.vlen < kBlock || p.allowed != nullptr;
     case kSegSink: return g.len < kBlock;
     case kSegRecent: return !(p.rec_len == p.R && g.len == kBlock);
-    default: return g.len < kBlock || g.off + kBlock - 1 > t0;
+    default: return g.len < kBlock || g.off + kBlock - 1 - p.causal_off > t0 || p.tok_mask != nullptr;
   }
 }
 
@@ -195,7 +195,7 @@ __device__ __forceinline__ void apply_mask(const AttendParams& p, const Seg& g, 
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
     int thr = g.vlen - 1;
-    if (g.type == kSegChunk) thr = min(thr, tcol[ct] - g.off);
+    if (g.type == kSegChunk) thr = min(thr, tcol[ct] + p.causal_off - g.off);
     else if (allow[ct] == 0) thr = -1;
     base[ct] = 4 * lg - thr;
   }
@@ -205,6 +205,21 @@ __device__ __forceinline__ void apply_mask(const AttendParams& p, const Seg& g, 
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
       for (int e = 0; e < 4; ++e) S[kt][ct][e] = fminf(S[kt][ct][e], vis_bound(base[ct] + 16 * kt + e));
+  if (g.type == kSegChunk && p.tok_mask != nullptr) {
+    // caller-packed keys with a per-(query, key) mask: keys past vlen are
+    // already hidden and never read; padding columns read row tq - 1
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const uint8_t* mrow = p.tok_mask + static_cast<int64_t>(min(tcol[ct], p.tq - 1)) * p.n_chunk + g.off;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int key = 16 * kt + 4 * lg + e;
+          if (key < g.vlen && mrow[key] != 0) S[kt][ct][e] = -INFINITY;
+        }
+    }
+  }
 }
 
 template <int FMT>
@@ -271,7 +286,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
   float m_run[2] = {-INFINITY, -INFINITY};
   float l_run[2] = {0.0f, 0.0f};
 
-  const int n_chunk_seg = p.n_chunk > 0 ? t_last / kBlock + 1 : 0;
+  // chunk segments up to the last key visible to the tile's last token
+  const int n_chunk_seg =
+      p.n_chunk > 0 ? min((p.n_chunk + kBlock - 1) / kBlock, (t_last + p.causal_off) / kBlock + 1) : 0;
   const int nseg_all = p.n_hist + p.n_sink_seg + p.n_rec_seg + n_chunk_seg;
   // split-K: this workgroup attends segments [seg_lo, nseg) of the list
   const int split = blockIdx.z;
@@ -487,6 +504,31 @@ __global__ __launch_bounds__(kHeadDim) void prefill_merge_kernel(const AttendPar
 }
 
 }  // namespace
+
+// The matrix-core kernel over (query tile x KV head, layer, split), then the
+// split merge.
+int launch_prefill(int hkv, int kv_format, int num_layers, int tq, AttendParams& p, hipStream_t s) {
+  NKV_CHECK_SUPPORTED(p.G >= 1 && kPfCols % p.G == 0,
+                      "nkv_prefill_attend: query heads per KV head (%d) must divide %d", p.G, kPfCols);
+  const int tpw = kPfCols / p.G;
+  const int nqt = (tq + tpw - 1) / tpw;
+  const dim3 grid(nqt * hkv, num_layers, p.splits);
+  switch (kv_format) {
+    case NKV_KV_BF16: hipLaunchKernelGGL(prefill_kernel<NKV_KV_BF16>, grid, dim3(kPfThreads), 0, s, p, nqt); break;
+    case NKV_KV_INT8_CHANNEL:
+      hipLaunchKernelGGL(prefill_kernel<NKV_KV_INT8_CHANNEL>, grid, dim3(kPfThreads), 0, s, p, nqt);
+      break;
+    case NKV_KV_INT8_TOKEN:
+      hipLaunchKernelGGL(prefill_kernel<NKV_KV_INT8_TOKEN>, grid, dim3(kPfThreads), 0, s, p, nqt);
+      break;
+    default: NKV_CHECK_SUPPORTED(false, "nkv_prefill_attend: unknown kv_format %d", kv_format);
+  }
+  if (p.splits > 1)
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3(nqt * hkv, num_layers, min(kPfCols, tq * p.G)), dim3(kHeadDim), 0,
+                       s, p, nqt);
+  return NKV_OK;
+}
+
 }  // namespace nkv
 
 using namespace nkv;
@@ -515,24 +557,7 @@ extern "C" int nkv_prefill_attend(const nkv_store* st, int layer0, int num_layer
                                     allowed, allowed_layer_stride, sink_len, ring_base, rec_lo, rec_len,
                                     scale, splits, partial_ws, out, &p);
   if (rc != NKV_OK) return rc;
-  NKV_CHECK_SUPPORTED(p.G >= 1 && kPfCols % p.G == 0,
-                      "nkv_prefill_attend: query heads per KV head (%d) must divide %d", p.G, kPfCols);
-  const int tpw = kPfCols / p.G;
-  const int nqt = (tq + tpw - 1) / tpw;
-  const dim3 grid(nqt * st->num_kv_heads, num_layers, splits);
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  switch (st->kv_format) {
-    case NKV_KV_BF16: hipLaunchKernelGGL(prefill_kernel<NKV_KV_BF16>, grid, dim3(kPfThreads), 0, s, p, nqt); break;
-    case NKV_KV_INT8_CHANNEL:
-      hipLaunchKernelGGL(prefill_kernel<NKV_KV_INT8_CHANNEL>, grid, dim3(kPfThreads), 0, s, p, nqt);
-      break;
-    case NKV_KV_INT8_TOKEN:
-      hipLaunchKernelGGL(prefill_kernel<NKV_KV_INT8_TOKEN>, grid, dim3(kPfThreads), 0, s, p, nqt);
-      break;
-    default: NKV_CHECK_SUPPORTED(false, "nkv_prefill_attend: unknown kv_format %d", st->kv_format);
-  }
-  if (splits > 1)
-    hipLaunchKernelGGL(prefill_merge_kernel, dim3(nqt * st->num_kv_heads, num_layers, min(kPfCols, tq * p.G)),
-                       dim3(kHeadDim), 0, s, p, nqt);
-  return launch_status("nkv_prefill_attend");
+  const int lrc = launch_prefill(st->num_kv_heads, st->kv_format, num_layers, tq, p,
+                                 reinterpret_cast<hipStream_t>(stream));
+  return lrc != NKV_OK ? lrc : launch_status("nkv_prefill_attend");
 }

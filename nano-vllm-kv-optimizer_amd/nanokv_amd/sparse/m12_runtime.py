@@ -5,7 +5,8 @@ Drop-in for ``nanovllm/sparse/m12_runtime.py`` of the reference: the same
 the same call surface (``decode``, ``prefill_first``, ``prefill_chunk``,
 ``verify_tokens``, ``commit_verified``, ``rollback_verified``, ``reset``,
 ``reserve_blocks``, ``_gpu_select``, ``_gpu_select_per_query``,
-``_build_reps_gpu``) and state attributes (``nblocks_filled``,
+``_fused_attention``, ``_prefill_attention``, ``_build_reps_gpu``) and state
+attributes (``nblocks_filled``,
 ``valid_len``, ``prefill_len``, ``reps_gpu``, ``protected_blocks``,
 ``last_block_ids``, ``timings`` ...), so ``Attention.forward``
 (nanovllm/layers/attention.py:64-99) and the engine wiring
@@ -22,13 +23,14 @@ a model in one launch per stage.
 from __future__ import annotations
 
 import math
+from contextlib import nullcontext
 from dataclasses import dataclass
 from time import perf_counter
 
 import torch
 
 from .. import _lib
-from ..store import SparseKVStore, query_summaries
+from ..store import SparseKVStore, packed_attention, query_summaries
 
 # ---------------------------------------------------------------------------
 # Host-side helpers (same contracts as the reference's module functions)
@@ -643,6 +645,81 @@ class M12LayerRuntime:
         if nblocks > self.max_blocks:
             raise ValueError(f"{nblocks} blocks exceed max_model_len ({self.max_blocks} blocks)")
 
+    # -- stage profiling (m12_runtime.py:1130-1136, :1155-1162) ---------------------
+    def _profile_range(self, name: str):
+        """A named profiler range when enabled: torch profiler (profile_torch_stages)
+        or an NVTX / roctx range (profile_nsys_stages)."""
+        if self.profile_torch_stages:
+            return torch.profiler.record_function(f"m12.{name}")
+        if self.profile_nsys_stages:
+            return torch.cuda.nvtx.range(f"m12.{name}.layer{self.layer_id}")
+        return nullcontext()
+
+    def _event_pair(self, name: str):
+        """With profile_cuda_stages: a timing-event pair stored under `name` in
+        cuda_stage_events, its start recorded now on the current stream."""
+        if not self.profile_cuda_stages:
+            return None
+        pair = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        self.cuda_stage_events[name] = pair
+        pair[0].record()
+        return pair
+
+    @staticmethod
+    def _event_end(pair) -> None:
+        if pair is not None:
+            pair[1].record()
+
+    # -- caller overrides of the selector -----------------------------------------
+    def _select_override(self):
+        """An instance-level ``_gpu_select`` (the reference's tests force block ids
+        by assigning one, tests/test_m14_prefill_layout.py:76), else None."""
+        return self.__dict__.get("_gpu_select")
+
+    @staticmethod
+    def _ids_from_override(result) -> torch.Tensor:
+        ids = result[0] if isinstance(result, tuple) else result
+        return torch.as_tensor(ids).to("cpu", torch.int64).flatten()
+
+    # -- exact attention over caller-packed K/V (m12_runtime.py:845-896) -------------
+    def _fused_attention(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, hist_len: int,
+                         sink_len: int, causal_from: int, attn_mask: torch.Tensor | None = None) -> torch.Tensor:
+        """q [Tq, Hq, D], k / v [S, Hkv, D] bf16 on the device -> [Tq, Hq, D] bf16.
+
+        Query t sees key j iff j < causal_from + t + 1 (keys before causal_from
+        are fully visible; causal_from >= S is the unmasked decode fast path),
+        and, with attn_mask [Tq, S] (True = disallowed), only where the mask is
+        False.  hist_len / sink_len describe the packing and do not change the
+        result (as in the reference).  Runs on nkv_attend_packed: the few-query
+        kernel (fp32 P.V) when Tq * G <= 16, else the matrix-core kernel (P
+        rounded to bf16 for P.V, as flash-attention does)."""
+        cfg = self.cfg
+        if q.ndim != 3 or tuple(q.shape[1:]) != (cfg.num_heads, cfg.head_dim):
+            raise ValueError(f"q must be [Tq, {cfg.num_heads}, {cfg.head_dim}] (got {tuple(q.shape)})")
+        if k.ndim != 3 or tuple(k.shape[1:]) != (cfg.num_kv_heads, cfg.head_dim) or k.shape != v.shape:
+            raise ValueError(f"k and v must be [S, {cfg.num_kv_heads}, {cfg.head_dim}] "
+                             f"(got {tuple(k.shape)}, {tuple(v.shape)})")
+        if min(hist_len, sink_len, causal_from) < 0:
+            raise ValueError("hist_len, sink_len and causal_from must be >= 0")
+        q = self._as_bf16(q, "q")
+        k = self._as_bf16(k, "k")
+        v = self._as_bf16(v, "v")
+        return packed_attention(q, k, v, causal_from, cfg.scale, attn_mask)
+
+    def _prefill_attention(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                           causal_from: int) -> torch.Tensor:
+        """Packed later-chunk attention with the configured backend
+        (m12_runtime.py:809-839).  "torch" is _fused_attention's masked path;
+        "flash" is flash-attention's bottom-right causal alignment over the
+        same keys, the same mask, so both run the same kernel here."""
+        self._check_prefill_backend()
+        return self._fused_attention(q, k, v, hist_len=causal_from, sink_len=0, causal_from=causal_from)
+
+    def _check_prefill_backend(self) -> None:
+        backend = self.cfg.prefill_attention_backend
+        if backend not in ("torch", "flash"):
+            raise ValueError(f"unknown prefill attention backend: {backend!r}")
+
     # -- input checks ------------------------------------------------------------
     def _as_bf16(self, t: torch.Tensor, name: str) -> torch.Tensor:
         if t.dtype != torch.bfloat16:
@@ -662,7 +739,8 @@ class M12LayerRuntime:
     def prefill_first(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> dict:
         """Store the first chunk; its dense attention is the caller's (m12_runtime.py:518-523)."""
         assert self.prefill_len == 0, "prefill_first called after history exists"
-        self._store_kv(k, v)
+        with self._profile_range("prefill_first_store_kv"):
+            self._store_kv(k, v)
         return {"nblocks": self.nblocks_filled, "valid_len": self.valid_len}
 
     def dense_prefill(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -813,25 +891,46 @@ class M12LayerRuntime:
         else:
             q_route = q
         requested = cfg.top_k_blocks if cfg.decode_top_k_blocks is None else cfg.decode_top_k_blocks
-        host_rule = cfg.decode_relative_a is not None or (cfg.dynamic_top_k)
-        if self.device_ring and self.device_ring_ready():
+        override = self._select_override()
+        host_rule = cfg.decode_relative_a is not None or cfg.dynamic_top_k or override is not None
+        if (self.device_ring and self.device_ring_ready() and override is None
+                and not self.profile_cuda_stages):
             return self._decode_ring(q, k, v, requested, t0)
-        if host_rule:
-            ids_cpu, info = self._gpu_select(q_route, dynamic=cfg.dynamic_top_k, budget=requested,
-                                             use_relative=cfg.decode_relative_a is not None)
-            if cfg.gather_sort and ids_cpu.numel() > 1:
-                ids_cpu = ids_cpu.sort().values
-            n_hist = ids_cpu.numel()
-            ids_dev = ids_cpu.to(torch.int32).to(self.store.device).view(1, 1, n_hist)
-            stride = n_hist
-        else:
-            order = _lib.NKV_ORDER_ID_ASC if cfg.gather_sort else _lib.NKV_ORDER_SCORE_DESC
-            ids_dev, _, n_hist = self._select_dev(q_route, requested, order)
-            stride = ids_dev.shape[-1]
+        # the recent append runs inside the attention launch (the new token is
+        # written to the ring slot it frees), so its event pair spans nothing
+        ev = self._event_pair("recent")
+        self._event_end(ev)
+        ev = self._event_pair("selector")
+        with self._profile_range("selector"):
+            if override is not None:
+                ids_cpu = self._ids_from_override(override(
+                    q_route[0], dynamic=cfg.dynamic_top_k, budget=cfg.decode_top_k_blocks,
+                    use_graph=cfg.selector_cuda_graph, use_static_mask=cfg.selector_static_mask,
+                    use_relative=cfg.decode_relative_a is not None))
+            elif host_rule:
+                ids_cpu, info = self._gpu_select(q_route, dynamic=cfg.dynamic_top_k, budget=requested,
+                                                 use_relative=cfg.decode_relative_a is not None)
+            if host_rule:
+                if cfg.gather_sort and ids_cpu.numel() > 1:
+                    ids_cpu = ids_cpu.sort().values
+                n_hist = ids_cpu.numel()
+                ids_dev = ids_cpu.to(torch.int32).to(self.store.device).view(1, 1, n_hist)
+                stride = n_hist
+            else:
+                order = _lib.NKV_ORDER_ID_ASC if cfg.gather_sort else _lib.NKV_ORDER_SCORE_DESC
+                ids_dev, _, n_hist = self._select_dev(q_route, requested, order)
+                stride = ids_dev.shape[-1]
+        self._event_end(ev)
         selector_ms = (perf_counter() - t0) * 1000.0
+        # the selected blocks are read in place: no gather, no pack
+        ev = self._event_pair("h2d_pack")
+        self._event_end(ev)
         t_a = perf_counter()
-        out, sink_len, rec_len = self._core.decode_attend(
-            q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), ids_dev, stride, n_hist)
+        ev = self._event_pair("packed_attention")
+        with self._profile_range("packed_attention"):
+            out, sink_len, rec_len = self._core.decode_attend(
+                q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), ids_dev, stride, n_hist)
+        self._event_end(ev)
         attn_ms = (perf_counter() - t_a) * 1000.0
         self._set_last_ids(ids_dev[0, 0, :n_hist])
         if self.record_ids:
@@ -903,22 +1002,73 @@ class M12LayerRuntime:
         """Later prefill chunk: attention over [selected | sink | prev recent | chunk]."""
         cfg = self.cfg
         assert self.prefill_len > 0, "prefill_chunk requires prior history"
+        assert not (self.quant_history and cfg.prefill_adapter is not None), \
+            "quant_history is incompatible with the segmented prefill adapter"
+        self._check_prefill_backend()
         q = self._as_bf16(q, "q")
         k = self._as_bf16(k, "k")
         v = self._as_bf16(v, "v")
-        q_summary = prefill_query_summaries(q, cfg.prefill_query_segments)
-        self.last_prefill_query_summaries = q_summary.shape[0]
-        requested = cfg.top_k_blocks if cfg.prefill_top_k_blocks is None else cfg.prefill_top_k_blocks
-        order = _lib.NKV_ORDER_ID_ASC if cfg.gather_sort else _lib.NKV_ORDER_SCORE_DESC
-        ids_dev, _, n_hist = self._select_dev(q_summary, requested, order)
-        out, _, _ = self._core.chunk_attend(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0),
-                                            ids_dev, ids_dev.shape[-1], n_hist)
-        ids_cpu = ids_dev[0, 0, :n_hist].to("cpu", torch.int64)
-        self._store_kv(k, v)
+        with self._profile_range("prefill_selector"):
+            q_summary = prefill_query_summaries(q, cfg.prefill_query_segments)
+            self.last_prefill_query_summaries = q_summary.shape[0]
+            requested = cfg.top_k_blocks if cfg.prefill_top_k_blocks is None else cfg.prefill_top_k_blocks
+            override = self._select_override()
+            if override is not None:
+                res = override(q_summary) if cfg.prefill_top_k_blocks is None else \
+                    override(q_summary, budget=cfg.prefill_top_k_blocks)
+                ids_cpu = self._ids_from_override(res)
+                if cfg.gather_sort and ids_cpu.numel() > 1:
+                    ids_cpu = ids_cpu.sort().values
+                n_hist = ids_cpu.numel()
+                ids_dev = ids_cpu.to(torch.int32).to(self.store.device).view(1, 1, n_hist)
+            else:
+                order = _lib.NKV_ORDER_ID_ASC if cfg.gather_sort else _lib.NKV_ORDER_SCORE_DESC
+                ids_dev, _, n_hist = self._select_dev(q_summary, requested, order)
+                ids_cpu = None
+        if cfg.prefill_adapter is not None:
+            out = self._adapter_attention(cfg.prefill_adapter, q, k, v, ids_dev[0, 0, :n_hist])
+        else:
+            with self._profile_range("prefill_attention"):
+                out = self._core.chunk_attend(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0),
+                                              ids_dev, ids_dev.shape[-1], n_hist)[0][0]
+        if ids_cpu is None:
+            ids_cpu = ids_dev[0, 0, :n_hist].to("cpu", torch.int64)
+        with self._profile_range("prefill_store_kv"):
+            self._store_kv(k, v)
         self._last_prefill_ids = ids_cpu.clone()
         self._last_ids_dev = None
         self._last_ids_cpu = ids_cpu
-        return out[0]
+        return out
+
+    def _adapter_attention(self, adapter, q, k, v, ids_dev) -> torch.Tensor:
+        """The segmented-prefill adapter contract (segmented_prefill_adapter.py:95-147,
+        m12_runtime.py:596-611, :633-636): adapter.prepare(q, selected_k,
+        selected_v, (sink_k, sink_v), (recent_k, recent_v), (k, v)) then
+        adapter.attend(invocation) -> o.  Every segment is token-major
+        [tokens, Hkv, D]: the selected blocks gathered from the history (device
+        tensors; pinned host tensors with history_tier="host"), the sink, the
+        previous recent window in logical order, the chunk."""
+        cfg = self.cfg
+        st, L = self.store, self.store_layer
+        R, D, hkv = cfg.recent_tokens, cfg.head_dim, cfg.num_kv_heads
+        with self._profile_range("prefill_h2d_pack"):
+            ids = ids_dev.to(torch.int64)
+            if st.history_tier == "host":
+                ids = ids.cpu()
+            sel_k = st.hist_k[L][:, ids].permute(1, 2, 0, 3).reshape(-1, hkv, D)
+            sel_v = st.hist_v[L][:, ids].permute(1, 2, 0, 3).reshape(-1, hkv, D)
+            if st.history_tier == "host":
+                sel_k, sel_v = sel_k.pin_memory(), sel_v.pin_memory()
+            sink_len = min(cfg.sink_tokens, self.valid_len)
+            _, off, ln = prefill_recent_slice(self.valid_len, cfg.sink_tokens, R)
+            slots = (torch.arange(off, off + ln, device=st.device) + self._core.ring_start) % R
+            sink = (st.sink_k[L][:, :sink_len].permute(1, 0, 2).contiguous(),
+                    st.sink_v[L][:, :sink_len].permute(1, 0, 2).contiguous())
+            recent = (st.recent_k[L][:, slots].permute(1, 0, 2).contiguous(),
+                      st.recent_v[L][:, slots].permute(1, 0, 2).contiguous())
+            invocation = adapter.prepare(q, sel_k.contiguous(), sel_v.contiguous(), sink, recent, (k, v))
+        with self._profile_range("prefill_attention"):
+            return adapter.attend(invocation)
 
     # -- speculative verify (m12_runtime.py:656-807) -------------------------------------
     def verify_tokens(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, device=None) -> torch.Tensor:
@@ -927,23 +1077,35 @@ class M12LayerRuntime:
         tq = k.shape[0]
         assert tq >= 1, "verify needs at least one token"
         assert self.prefill_len > 0, "verify requires a complete prefill"
+        assert not (self.quant_history and cfg.prefill_adapter is not None), \
+            "quant_history is incompatible with the segmented prefill adapter"
         q = self._as_bf16(q, "q")
         k = self._as_bf16(k, "k")
         v = self._as_bf16(v, "v")
+        if not self.verify_lossless:   # the shared selection's attention is _prefill_attention's
+            self._check_prefill_backend()
         t0 = perf_counter()
         allowed_dev = None
-        if self.verify_lossless:
-            union, allowed = self._gpu_select_per_query(q, cfg.top_k_blocks)
-            ids_dev = union.to(torch.int32).to(self.store.device).view(1, 1, -1)
-            n_hist = union.numel()
-            allowed_dev = allowed.to(torch.uint8).contiguous()
-            ids_cpu = union
-        else:
-            ids_dev, _, n_hist = self._select_dev(q, cfg.top_k_blocks, _lib.NKV_ORDER_SCORE_DESC)
-            ids_cpu = None
+        override = self._select_override()
+        with self._profile_range("verify_selector"):
+            if self.verify_lossless:
+                union, allowed = self._gpu_select_per_query(q, cfg.top_k_blocks)
+                union = torch.as_tensor(union).to("cpu", torch.int64).flatten()
+                ids_dev = union.to(torch.int32).to(self.store.device).view(1, 1, -1)
+                n_hist = union.numel()
+                allowed_dev = torch.as_tensor(allowed).to(self.store.device, torch.uint8).contiguous()
+                ids_cpu = union
+            elif override is not None:
+                ids_cpu = self._ids_from_override(override(q))
+                n_hist = ids_cpu.numel()
+                ids_dev = ids_cpu.to(torch.int32).to(self.store.device).view(1, 1, n_hist)
+            else:
+                ids_dev, _, n_hist = self._select_dev(q, cfg.top_k_blocks, _lib.NKV_ORDER_SCORE_DESC)
+                ids_cpu = None
         t_sel = perf_counter()
-        out, _, _ = self._core.chunk_attend(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0),
-                                            ids_dev, ids_dev.shape[-1], n_hist, allowed_dev)
+        with self._profile_range("verify_attention"):
+            out, _, _ = self._core.chunk_attend(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0),
+                                                ids_dev, ids_dev.shape[-1], n_hist, allowed_dev)
         t_attn = perf_counter()
         if ids_cpu is None:
             ids_cpu = ids_dev[0, 0, :n_hist].to("cpu", torch.int64)

@@ -263,3 +263,45 @@ def query_summaries(q, nsegments: int):
     _lib.check(lib.nkv_query_summaries(_ptr(q), q.stride(0), nl, T, hq, d, nsegments, _ptr(out),
                                        out.stride(0), _stream()), "query_summaries")
     return out
+
+
+def packed_attention(q, k, v, causal_from: int, scale: float, mask=None, splits: int | None = None):
+    """Exact attention over caller-packed keys on the device (nkv_attend_packed).
+
+    q [Tq, Hq, 128], k / v [S, Hkv, 128] bf16 (token-major); query t sees key
+    j iff j - causal_from <= t and mask[t, j] is False (mask: bool / uint8
+    [Tq, S], True = hidden, or None) -> [Tq, Hq, 128] bf16.
+    """
+    lib = _lib.load()
+    q = SparseKVStore._bf16(q.contiguous(), "q")
+    k = SparseKVStore._bf16(k.contiguous(), "k")
+    v = SparseKVStore._bf16(v.contiguous(), "v")
+    if q.dim() != 3 or k.dim() != 3 or k.shape != v.shape or q.shape[-1] != HEAD_DIM or k.shape[-1] != HEAD_DIM:
+        raise ValueError(f"packed attention needs q [Tq, Hq, {HEAD_DIM}] and k = v [S, Hkv, {HEAD_DIM}] "
+                         f"(got q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)})")
+    if not (q.device == k.device == v.device) or q.device.type != "cuda":
+        raise ValueError("packed attention: q, k and v must be on one GPU")
+    tq, hq, _ = q.shape
+    s_len, hkv, _ = k.shape
+    if hq % hkv:
+        raise ValueError(f"num_heads {hq} is not a multiple of num_kv_heads {hkv}")
+    g = hq // hkv
+    m8 = None
+    if mask is not None:
+        if tuple(mask.shape) != (tq, s_len):
+            raise ValueError(f"attn_mask must be [{tq}, {s_len}] (got {tuple(mask.shape)})")
+        m8 = mask.to(device=q.device, dtype=torch.uint8).contiguous()
+    nseg = -(-s_len // BLOCK_SIZE)
+    if splits is None:
+        if tq * g > 16:   # matrix-core kernel: ~1536 workgroups, >= 4 segments per split
+            tiles = -(-tq // (128 // g)) * hkv
+            splits = max(1, min(round(1536 / tiles), nseg // 4, 64))
+        else:             # few-query kernel: ~1440 workgroups, >= 4 segments per split
+            groups = -(-tq // max(1, min(tq, 16 // g))) * hkv
+            splits = max(1, min(round(1440 / groups), -(-nseg // 4), 64))
+    ws = int(lib.nkv_attend_packed_workspace_floats(hq, hkv, tq, splits))
+    part = torch.empty(max(ws, 1), dtype=torch.float32, device=q.device) if ws else None
+    out = torch.empty_like(q)
+    _lib.check(lib.nkv_attend_packed(hq, hkv, _ptr(q), tq, _ptr(k), _ptr(v), s_len, int(causal_from), _ptr(m8),
+                                     float(scale), splits, _ptr(part), _ptr(out), _stream()), "attend_packed")
+    return out

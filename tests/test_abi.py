@@ -164,3 +164,21 @@ def test_model_ops_reject_bad_sizes_without_device_work():
                                 None) == _lib.NKV_ERR_ARG
     assert lib.nkv_qk_norm_rope(None, 1, 32, 8, fake, fake, fake, fake, 10, fake, 1e-6, fake, fake, fake,
                                 None) == _lib.NKV_ERR_ARG
+
+
+def test_packed_attention_rejects_bad_arguments_without_device_work():
+    lib = _lib.load()
+    d = ctypes.c_void_p(256)    # never dereferenced: the checks come first
+    assert lib.nkv_attend_packed(24, 8, d, 4, d, d, 64, 0, None, 1.0, 1, None, d, None) == _lib.NKV_ERR_UNSUPPORTED
+    assert lib.nkv_attend_packed(32, 7, d, 4, d, d, 64, 0, None, 1.0, 1, None, d, None) == _lib.NKV_ERR_ARG
+    assert lib.nkv_attend_packed(32, 8, None, 4, d, d, 64, 0, None, 1.0, 1, None, d, None) == _lib.NKV_ERR_ARG
+    assert lib.nkv_attend_packed(32, 8, d, 0, d, d, 64, 0, None, 1.0, 1, None, d, None) == _lib.NKV_ERR_ARG
+    assert lib.nkv_attend_packed(32, 8, d, 4, d, d, 0, 0, None, 1.0, 1, None, d, None) == _lib.NKV_ERR_ARG
+    assert lib.nkv_attend_packed(32, 8, d, 4, d, d, 64, -1, None, 1.0, 1, None, d, None) == _lib.NKV_ERR_ARG
+    assert b"causal_from" in lib.nkv_last_error()
+    assert lib.nkv_attend_packed(32, 8, d, 4, d, d, 64, 0, None, 1.0, 3, None, d, None) == _lib.NKV_ERR_ARG
+    assert b"partial_ws" in lib.nkv_last_error()
+    # the workspace follows the kernel choice: few-query rows (tq * G <= 16) vs query tiles
+    assert lib.nkv_attend_packed_workspace_floats(32, 8, 4, 1) == 0
+    assert lib.nkv_attend_packed_workspace_floats(32, 8, 4, 3) == lib.nkv_attend_workspace_floats(1, 8, 32, 4, 3)
+    assert lib.nkv_attend_packed_workspace_floats(32, 8, 256, 3) == lib.nkv_prefill_workspace_floats(1, 8, 32, 256, 3)

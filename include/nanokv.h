@@ -200,6 +200,31 @@ int64_t nkv_decode_step_workspace_floats(int num_layers, int num_kv_heads, int n
                                          int splits, int nstreams);
 
 /*
+ * nkv_decode_step without caller workspaces and without any allocation.
+ * No counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).
+ *
+ * Same arguments and results as nkv_decode_step with one range on `stream`,
+ * except that score_keys and partial_ws live in a 16 MiB array in the
+ * library's device code object, one per GPU, held until the process ends:
+ * 1 MiB of score keys (num_layers x nblocks <= 262144) and 15 MiB of split
+ * partials (nkv_attend_workspace_floats(num_layers, Hkv, Hq, 1, splits) <=
+ * 3932160 floats: 16 x 130 per layer, KV head and split, e.g. 36 layers x 8
+ * KV heads x up to 6 splits).  Larger sizes
+ * are rejected with NKV_ERR_ARG before any device work.  The first call on a
+ * device looks the array up (hipGetSymbolAddress) and clears its key region
+ * with a fill kernel on `stream`; every call leaves the keys it used at zero.
+ * All calls on one GPU share the array: calls that overlap (other streams,
+ * other host threads) race and must be serialised by the caller.
+ */
+int nkv_decode_step_noalloc(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
+                            const uint16_t* k_new, const uint16_t* v_new, int nblocks,
+                            const int32_t* protected_ids, int n_protected, int k, int n_hist,
+                            int sink_len, int write_slot, int ring_base, int rec_lo, int rec_len,
+                            float scale, int splits, int32_t* out_ids, uint16_t* out, void* stream);
+
+/*
  * The steady-state decode layer-step (recent window full) with the ring
  * position in device memory, so that every argument is the same from one
  * step to the next and the call can be captured in a HIP graph and replayed.

@@ -16,6 +16,7 @@
 // range's bandwidth-bound scoring and attention.  The per-call joins cost
 // GPU time too (on the 36-layer 32K step two ranges measured 135 us against
 // 128 us for one), so one range is the default of the Python runtime.
+#include <mutex>
 #include <vector>
 
 #include "nkv_common.h"
@@ -24,6 +25,59 @@ namespace nkv {
 namespace {
 
 constexpr int kMaxStepStreams = 8;
+
+// ---- scratch of the allocation-free decode step ---------------------------
+// One array per GPU, in the library's code object: the score keys (uint32
+// [L][nblocks], zero between calls) then the split partials of the attention.
+constexpr int64_t kScratchBytes = int64_t(16) << 20;
+constexpr int64_t kScratchKeyBytes = int64_t(1) << 20;
+constexpr int64_t kScratchKeys = kScratchKeyBytes / 4;                      // 262144 keys
+constexpr int64_t kScratchPartialFloats = (kScratchBytes - kScratchKeyBytes) / 4;
+constexpr int kMaxScratchDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// The device address of this GPU's `scratch` (the host-side name is only a
+// stand-in for the symbol), looked up once per device with the device
+// current; the first lookup also clears the key region on `s` with a fill
+// kernel (every later call leaves the keys it used at zero).
+__global__ void zero_words_kernel(uint32_t* p, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = 0u;
+}
+
+struct ScratchSlot {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[kMaxScratchDevices];
+
+int scratch_address(hipStream_t s, char** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("nkv_decode_step_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return NKV_ERR_HIP;
+  }
+  NKV_CHECK_SUPPORTED(dev >= 0 && dev < kMaxScratchDevices, "nkv_decode_step_noalloc: device %d beyond %d", dev,
+                      kMaxScratchDevices);
+  ScratchSlot& slot = g_scratch[dev];
+  std::call_once(slot.once, [&] {
+    void* p = nullptr;
+    slot.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (slot.err != hipSuccess) return;
+    hipLaunchKernelGGL(zero_words_kernel, dim3(256), dim3(256), 0, s, static_cast<uint32_t*>(p), kScratchKeys);
+    slot.err = hipGetLastError();
+    if (slot.err == hipSuccess) slot.ptr = p;
+  });
+  if (slot.ptr == nullptr) {
+    set_error("nkv_decode_step_noalloc: scratch set-up failed: %s", hipGetErrorString(slot.err));
+    return NKV_ERR_HIP;
+  }
+  *out = static_cast<char*>(slot.ptr);
+  return NKV_OK;
+}
 
 // Events of this host thread for the current device, created on first use
 // (disable-timing events; they live as long as the thread).
@@ -131,4 +185,35 @@ extern "C" int nkv_decode_step(const nkv_store* st, int layer0, int num_layers, 
     if (e != hipSuccess) return hip_fail(e, "nkv_decode_step: hipStreamWaitEvent");
   }
   return NKV_OK;
+}
+
+extern "C" int nkv_decode_step_noalloc(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
+                                       const uint16_t* k_new, const uint16_t* v_new, int nblocks,
+                                       const int32_t* protected_ids, int n_protected, int k, int n_hist,
+                                       int sink_len, int write_slot, int ring_base, int rec_lo, int rec_len,
+                                       float scale, int splits, int32_t* out_ids, uint16_t* out, void* stream) {
+  int rc = check_store(st, layer0, num_layers);
+  if (rc != NKV_OK) return rc;
+  NKV_CHECK_ARG(nblocks >= 1, "nkv_decode_step_noalloc: nblocks must be >= 1 (got %d)", nblocks);
+  NKV_CHECK_ARG(splits >= 1 && splits <= 64, "nkv_decode_step_noalloc: splits must be in [1, 64] (got %d)", splits);
+  NKV_CHECK_ARG(static_cast<int64_t>(num_layers) * nblocks <= kScratchKeys,
+                "nkv_decode_step_noalloc: num_layers x nblocks = %lld exceeds the scratch's %lld score keys",
+                static_cast<long long>(num_layers) * nblocks, static_cast<long long>(kScratchKeys));
+  const int64_t part = nkv_attend_workspace_floats(num_layers, st->num_kv_heads, st->num_heads, 1, splits);
+  NKV_CHECK_ARG(part <= kScratchPartialFloats,
+                "nkv_decode_step_noalloc: the split partials need %lld floats, the scratch holds %lld "
+                "(fewer layers or splits)",
+                static_cast<long long>(part), static_cast<long long>(kScratchPartialFloats));
+  NKV_CHECK_ARG(q != nullptr && k_new != nullptr && v_new != nullptr && out_ids != nullptr && out != nullptr,
+                "nkv_decode_step_noalloc: q, k_new, v_new, out_ids and out must be non-NULL");
+  NKV_CHECK_ARG(n_hist >= 1 && n_hist <= k, "nkv_decode_step_noalloc: n_hist must be in [1, k] (got %d, k=%d)",
+                n_hist, k);
+  char* base = nullptr;
+  rc = scratch_address(reinterpret_cast<hipStream_t>(stream), &base);
+  if (rc != NKV_OK) return rc;
+  void* streams[1] = {stream};
+  return nkv_decode_step(st, layer0, num_layers, q, k_new, v_new, nblocks, protected_ids, n_protected, k, n_hist,
+                         sink_len, write_slot, ring_base, rec_lo, rec_len, scale, splits,
+                         reinterpret_cast<uint32_t*>(base), out_ids, reinterpret_cast<float*>(base + kScratchKeyBytes),
+                         out, 1, streams);
 }

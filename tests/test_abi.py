@@ -182,3 +182,26 @@ def test_packed_attention_rejects_bad_arguments_without_device_work():
     assert lib.nkv_attend_packed_workspace_floats(32, 8, 4, 1) == 0
     assert lib.nkv_attend_packed_workspace_floats(32, 8, 4, 3) == lib.nkv_attend_workspace_floats(1, 8, 32, 4, 3)
     assert lib.nkv_attend_packed_workspace_floats(32, 8, 256, 3) == lib.nkv_prefill_workspace_floats(1, 8, 32, 256, 3)
+
+
+def test_noalloc_decode_step_rejects_sizes_beyond_its_scratch_without_device_work():
+    lib = _lib.load()
+    st = _lib.NkvStore()
+    st.num_layers, st.num_heads, st.num_kv_heads = 64, 32, 8
+    st.head_dim, st.block_size, st.r, st.cap_blocks = 128, 64, 4, 8192
+    st.sink_tokens, st.recent_tokens, st.kv_format = 64, 512, 0
+    d = ctypes.c_void_p(256)    # never dereferenced: the size checks come first
+    st.hist_k = st.hist_v = st.reps = d
+    st.sink_k = st.sink_v = st.recent_k = st.recent_v = d
+
+    def call(nl, nblocks, splits):
+        return lib.nkv_decode_step_noalloc(ctypes.byref(st), 0, nl, d, d, d, nblocks, d, 1, 32, 32, 64, 0, 1, 0,
+                                           511, 1.0, splits, d, d, None)
+
+    # 64 layers x 4097 blocks = 262208 score keys > 262144
+    assert call(64, 4097, 1) == _lib.NKV_ERR_ARG and b"score keys" in lib.nkv_last_error()
+    # 36 layers x 8 heads x 7 splits of 16 x 130 floats = 4193280 > 3932160
+    assert call(36, 512, 7) == _lib.NKV_ERR_ARG and b"split partials" in lib.nkv_last_error()
+    assert call(36, 512, 0) == _lib.NKV_ERR_ARG
+    with pytest.raises(ValueError, match="score keys"):
+        _lib.check(call(64, 4097, 1), "decode_step_noalloc")

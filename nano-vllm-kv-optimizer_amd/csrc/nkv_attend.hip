@@ -120,6 +120,13 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
     ring_base = write_slot + 1 == p.R ? 0 : write_slot + 1;
   }
 
+  // the decode step's score keys: read by its top-k launch, cleared here for
+  // the next step's scoring (stream order makes both safe)
+  if (p.zero_keys != nullptr && split == 0 && h == 0 && qg == 0) {
+    uint32_t* zk = p.zero_keys + static_cast<int64_t>(layer) * p.zero_n;
+    for (int i = threadIdx.x; i < p.zero_n; i += kAttendThreads) zk[i] = 0u;
+  }
+
   // decode's shift+append: the new token (chunk token 0) also goes into the
   // freed ring slot, which no workgroup of this launch reads.
   if (write_slot >= 0 && split == 0 && qg == 0 && wave == 0 && lane < 32) {
@@ -679,9 +686,31 @@ int fill_attend_params(const char* who, const nkv_store* st, int layer0, int num
   p.scale_log2 = scale * 1.4426950408889634f;
   p.causal_off = 0;
   p.tok_mask = nullptr;
+  p.zero_keys = nullptr;
+  p.zero_n = 0;
   return NKV_OK;
 }
 
+}  // namespace nkv
+
+namespace nkv {
+int attend_impl(const nkv_store* st, int layer0, int num_layers, const uint16_t* q, int64_t q_layer_stride, int tq,
+                const uint16_t* k_new, const uint16_t* v_new, int64_t kv_layer_stride, int n_chunk, int write_slot,
+                const int32_t* ids, int64_t ids_layer_stride, int n_hist, const uint8_t* allowed,
+                int64_t allowed_layer_stride, int sink_len, int ring_base, int rec_lo, int rec_len, float scale,
+                int splits, float* partial_ws, uint16_t* out, uint32_t* zero_keys, int zero_n, void* stream) {
+  AttendParams p;
+  const int rc = fill_attend_params("nkv_attend", st, layer0, num_layers, q, q_layer_stride, tq, k_new,
+                                    v_new, kv_layer_stride, n_chunk, write_slot, ids, ids_layer_stride,
+                                    n_hist, allowed, allowed_layer_stride, sink_len, ring_base, rec_lo,
+                                    rec_len, scale, splits, partial_ws, out, &p);
+  if (rc != NKV_OK) return rc;
+  p.zero_keys = zero_keys;
+  p.zero_n = zero_n;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int lrc = launch_grouped(st->num_kv_heads, st->kv_format, num_layers, tq, p, s);
+  return lrc != NKV_OK ? lrc : launch_status("nkv_attend");
+}
 }  // namespace nkv
 
 extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
@@ -691,15 +720,9 @@ extern "C" int nkv_attend(const nkv_store* st, int layer0, int num_layers, const
                           int n_hist, const uint8_t* allowed, int64_t allowed_layer_stride,
                           int sink_len, int ring_base, int rec_lo, int rec_len, float scale, int splits,
                           float* partial_ws, uint16_t* out, void* stream) {
-  AttendParams p;
-  const int rc = fill_attend_params("nkv_attend", st, layer0, num_layers, q, q_layer_stride, tq, k_new,
-                                    v_new, kv_layer_stride, n_chunk, write_slot, ids, ids_layer_stride,
-                                    n_hist, allowed, allowed_layer_stride, sink_len, ring_base, rec_lo,
-                                    rec_len, scale, splits, partial_ws, out, &p);
-  if (rc != NKV_OK) return rc;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int lrc = launch_grouped(st->num_kv_heads, st->kv_format, num_layers, tq, p, s);
-  return lrc != NKV_OK ? lrc : launch_status("nkv_attend");
+  return attend_impl(st, layer0, num_layers, q, q_layer_stride, tq, k_new, v_new, kv_layer_stride, n_chunk,
+                     write_slot, ids, ids_layer_stride, n_hist, allowed, allowed_layer_stride, sink_len, ring_base,
+                     rec_lo, rec_len, scale, splits, partial_ws, out, nullptr, 0, stream);
 }
 
 extern "C" int nkv_decode_step_ring(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
@@ -719,17 +742,24 @@ extern "C" int nkv_decode_step_ring(const nkv_store* st, int layer0, int num_lay
   NKV_CHECK_ARG(R >= 2, "nkv_decode_step_ring: needs a recent window of at least 2 tokens");
   const int64_t q_ls = static_cast<int64_t>(st->num_heads) * kHeadDim;
   const int64_t kv_ls = static_cast<int64_t>(st->num_kv_heads) * kHeadDim;
-  rc = nkv_select(st, layer0, num_layers, q, q_ls, 1, 0, nblocks, protected_ids, n_protected, k,
-                  NKV_ORDER_SCORE_DESC, score_keys, nullptr, out_ids, nullptr, stream);
-  if (rc != NKV_OK) return rc;
   // The full window: the R - 1 recent tokens before the write slot, then the
   // new token.  Write slot 0 / base 1 stand in for the host checks; the
-  // kernel reads each layer's ring start from device memory.
+  // kernel reads each layer's ring start from device memory.  Checked before
+  // the selection is enqueued (its step form leaves the keys for the
+  // attention launch to clear).
   AttendParams p;
   rc = fill_attend_params("nkv_decode_step_ring", st, layer0, num_layers, q, q_ls, 1, k_new, v_new, kv_ls, 1, 0,
                           out_ids, k, n_hist, nullptr, 0, sink_len, 1, 0, R - 1, scale, splits, partial_ws, out, &p);
   if (rc != NKV_OK) return rc;
+  rc = select_impl(st, layer0, num_layers, q, q_ls, 1, 0, nblocks, protected_ids, n_protected, k,
+                   NKV_ORDER_SCORE_DESC, score_keys, nullptr, out_ids, nullptr, true, stream);
+  if (rc != NKV_OK) return rc;
+  const bool step_keys = select_step_form(1, n_protected, nblocks);
   p.ring_start = ring_start;
+  if (step_keys) {
+    p.zero_keys = score_keys;
+    p.zero_n = nblocks;
+  }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   rc = launch_grouped(st->num_kv_heads, st->kv_format, num_layers, 1, p, s);   // with splits > 1 the merge advances the ring
   if (rc != NKV_OK) return rc;

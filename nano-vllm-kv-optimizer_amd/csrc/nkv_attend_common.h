@@ -64,6 +64,10 @@ struct AttendParams {
   // (uint8 [tq][n_chunk], nonzero = hidden)
   int causal_off;
   const uint8_t* tok_mask;
+  // non-null: the layer's first workgroup clears zero_keys[layer][0 .. zero_n)
+  // (the decode step's score keys, consumed by the top-k launch before it)
+  uint32_t* zero_keys;
+  int zero_n;
 };
 
 __device__ __forceinline__ void wave_lds_sync() {

@@ -45,6 +45,27 @@ int check_store(const nkv_store* st, int layer0, int num_layers);
 // Compute units of the current device (cached per thread); 0 on error.
 int device_cus();
 
+// nkv_select with the decode step's option: with step set (and one query, no
+// raw scores or values, at most 64 protected ids, at most 2048 blocks) the
+// scorer leaves the protected blocks' keys at zero and the top-k neither
+// reads the protected list nor clears the keys -- the caller's attention
+// launch must clear them (AttendParams.zero_keys).  Same ids either way.
+int select_impl(const nkv_store* st, int layer0, int num_layers, const uint16_t* q, int64_t q_layer_stride, int nq,
+                int per_query, int nblocks, const int32_t* protected_ids, int n_protected, int k, int order,
+                uint32_t* score_keys, float* out_scores, int32_t* out_ids, float* out_vals, bool step,
+                void* stream);
+// Whether select_impl takes the step form for these sizes (out_scores and
+// out_vals NULL, per_query 0).
+bool select_step_form(int nq, int n_protected, int nblocks);
+
+// nkv_attend; with zero_keys non-NULL the launch also clears
+// zero_keys[l][0 .. zero_n) of every layer l it attends.
+int attend_impl(const nkv_store* st, int layer0, int num_layers, const uint16_t* q, int64_t q_layer_stride, int tq,
+                const uint16_t* k_new, const uint16_t* v_new, int64_t kv_layer_stride, int n_chunk, int write_slot,
+                const int32_t* ids, int64_t ids_layer_stride, int n_hist, const uint8_t* allowed,
+                int64_t allowed_layer_stride, int sink_len, int ring_base, int rec_lo, int rec_len, float scale,
+                int splits, float* partial_ws, uint16_t* out, uint32_t* zero_keys, int zero_n, void* stream);
+
 // ------------------------------------------------------------ bf16 / fp16 --
 __device__ __forceinline__ float bf16_lo(uint32_t packed) {
   return __uint_as_float(packed << 16);

@@ -30,8 +30,6 @@
 // m12_runtime.py:1004-1014 (protected mask) and :1033 (torch.topk).
 #include "nkv_common.h"
 
-#include <stdlib.h>
-
 namespace nkv {
 namespace {
 
@@ -106,7 +104,13 @@ __device__ __forceinline__ unsigned long long sel_entry(uint32_t key, int id) {
 // count being J ballots.  Collection is the same ascending-id ballot pass as
 // topk_kernel; up to 64 selected entries are then placed by their rank among
 // the selection, larger k sorted by a bitonic network over LDS.
-template <int J>
+//
+// STEP (the decode step's selection): the scorer left the protected blocks'
+// keys at 0 (every scored key is >= score_key(-inf) > 0), and the step's
+// attention launch zeroes the keys afterwards, so the row needs neither the
+// protected list nor the zeroing stores; key 0 is read as score_key(-inf),
+// exactly the protected mask of the general form.
+template <int J, bool STEP>
 __device__ __forceinline__ void select_row_wave(
     uint32_t* __restrict__ sk, int nblocks, const int32_t* __restrict__ prot, int nprot,
     int k_req, int order, int32_t* __restrict__ ids, float* __restrict__ vals,
@@ -124,43 +128,120 @@ __device__ __forceinline__ void select_row_wave(
     key[j] = sk[i < nblocks ? i : nblocks - 1];
   }
 
-  for (int w = lane; w < nwords; w += kWave) pmask[w] = 0u;
-  wave_lds_sync();
-  for (int i = lane; i < nprot; i += kWave) {
-    const int p = prot[i];
-    if (p >= 0 && p < nblocks) atomicOr(&pmask[p >> 5], 1u << (p & 31));
-  }
-  wave_lds_sync();
-
-  // blocks in range and not protected, counted with ballots
   int avail = 0;
+  if constexpr (STEP) {
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int i = kWave * j + lane;
-    const bool valid = i < nblocks;
-    const bool prot_i = valid && ((pmask[i >> 5] >> (i & 31)) & 1u);
-    if (valid) {
-      sk[i] = 0u;  // leave the key buffer zeroed for the next scoring pass
-      if (scores) scores[i] = key_score(key[j]);
-      if (prot_i) key[j] = kNegInfKey;
-    } else {
-      key[j] = 0u;
+    for (int j = 0; j < J; ++j) {
+      const int i = kWave * j + lane;
+      const bool valid = i < nblocks;
+      avail += __popcll(__ballot(valid && key[j] != 0u));
+      key[j] = !valid ? 0u : (key[j] == 0u ? kNegInfKey : key[j]);
     }
-    avail += __popcll(__ballot(valid && !prot_i));
+  } else {
+    for (int w = lane; w < nwords; w += kWave) pmask[w] = 0u;
+    wave_lds_sync();
+    for (int i = lane; i < nprot; i += kWave) {
+      const int p = prot[i];
+      if (p >= 0 && p < nblocks) atomicOr(&pmask[p >> 5], 1u << (p & 31));
+    }
+    wave_lds_sync();
+
+    // blocks in range and not protected, counted with ballots
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int i = kWave * j + lane;
+      const bool valid = i < nblocks;
+      const bool prot_i = valid && ((pmask[i >> 5] >> (i & 31)) & 1u);
+      if (valid) {
+        sk[i] = 0u;  // leave the key buffer zeroed for the next scoring pass
+        if (scores) scores[i] = key_score(key[j]);
+        if (prot_i) key[j] = kNegInfKey;
+      } else {
+        key[j] = 0u;
+      }
+      avail += __popcll(__ballot(valid && !prot_i));
+    }
   }
   const int k = min(k_req, max(1, avail));
+
+  // ---- fast path: rank a short candidate list -----------------------------
+  // L0 = the k-th largest of the 64 lane maxima (one ballot per search step)
+  // bounds the k-th largest key from below: k lanes hold a key >= L0.  Every
+  // valid key >= L0 is a candidate; when there are at most 64 of them they
+  // go to LDS in ascending block order and each lane ranks one against all
+  // (the entries are distinct: the id is part of each), which places the
+  // selection directly.  Otherwise (ties, adversarial spreads) the bitwise
+  // search below runs over all keys.  Same selection either way.
+  if (k <= kWave) {
+    uint32_t lmax = key[0];
+#pragma unroll
+    for (int j = 1; j < J; ++j) lmax = max(lmax, key[j]);   // keys past nblocks are 0
+    uint32_t L0 = 0u;
+    for (uint32_t m = 0x80000000u; m != 0u; m >>= 1) {
+      const uint32_t cand = L0 | m;
+      const int cnt = __popcll(__ballot(lmax >= cand));
+      if (cnt >= k) L0 = cand;
+      if (cnt == k) break;
+    }
+    unsigned long long bc[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) bc[j] = __ballot(kWave * j + lane < nblocks && key[j] >= L0);
+    int C = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) C += __popcll(bc[j]);
+    if (C <= kWave) {
+      const unsigned long long lt = (1ull << lane) - 1ull;
+      int base = 0;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        if ((bc[j] >> lane) & 1ull) sel[base + __popcll(bc[j] & lt)] = sel_entry(key[j], kWave * j + lane);
+        base += __popcll(bc[j]);
+      }
+      wave_lds_sync();
+      // sel holds >= 64 entries, so the pair read at j = C - 1 stays inside it
+      const unsigned long long e = sel[lane < C ? lane : 0];
+      int rank = 0;
+      const int cp = (C + 1) & ~1;
+#pragma unroll 8
+      for (int j = 0; j < cp; j += 2) {
+        const unsigned long long a = sel[j], b = sel[j + 1];
+        rank += (a > e) + ((j + 1 < C) & (b > e));
+      }
+      const bool chosen = lane < C && rank < k;
+      int pos = rank;
+      if (order != NKV_ORDER_SCORE_DESC) pos = __popcll(__ballot(chosen) & lt);   // ascending id
+      if (chosen) {
+        ids[pos] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(e & 0xffffffffull));
+        if (vals) vals[pos] = key_score(static_cast<uint32_t>(e >> 32));
+      }
+      return;
+    }
+  }
 
   // ---- k-th largest key: largest T with count(key >= T) >= k ------------
   // Once count(key >= T) == k the k keys >= T are the selection itself (every
   // key equal to the k-th largest is among them), so the search stops there:
   // the collection below then takes exactly those keys, as it would with the
   // fully resolved T.
+  // T and the candidate stay scalar (one vector-to-scalar hand-off per
+  // ballot, none back), and the J ballot counts are summed as a tree.
   uint32_t T = 0u;
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = T | (1u << bit);
-    int cnt = 0;
+  for (uint32_t m = 0x80000000u; m != 0u; m >>= 1) {
+    const uint32_t cand = T | m;
+    // all J compares issue before the first count reads one, so only the
+    // first count waits for a compare result
+    unsigned long long b[J];
 #pragma unroll
-    for (int j = 0; j < J; ++j) cnt += __popcll(__ballot(key[j] >= cand));
+    for (int j = 0; j < J; ++j) b[j] = __ballot(key[j] >= cand);
+    __builtin_amdgcn_sched_barrier(0);
+    int c[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) c[j] = __popcll(b[j]);
+#pragma unroll
+    for (int w = 1; w < J; w <<= 1)
+#pragma unroll
+      for (int j = 0; j + w < J; j += 2 * w) c[j] += c[j + w];
+    const int cnt = c[0];
     if (cnt >= k) T = cand;
     if (cnt == k) break;
   }
@@ -278,7 +359,8 @@ __device__ __forceinline__ void score_load(
 template <int R, int G>
 __device__ __forceinline__ void score_dots(
     const uint16_t* __restrict__ q, int64_t q_ls, int nq, int per_query, int hkv, int nblocks,
-    uint32_t* __restrict__ keys, int layer, int unit, int lane, ScoreTile<G>& t, uint4* my) {
+    uint32_t* __restrict__ keys, int layer, int unit, int lane, ScoreTile<G>& t, uint4* my,
+    const int32_t* __restrict__ skip_ids, int n_skip) {
   constexpr int TB = kWave / R;
   const int nqo = per_query ? nq : 1;
   const int h = unit % hkv;
@@ -318,8 +400,14 @@ __device__ __forceinline__ void score_dots(
       best = fmaxf(best, m);
     }
   }
-  if (!per_query && (lane % R) == 0 && b < nblocks)
-    atomicMax(&keys[static_cast<int64_t>(layer) * nblocks + b], score_key(best));
+  if (!per_query) {
+    // blocks on the skip list (the protected set, in the decode step) keep
+    // key 0, which the step's top-k reads as "protected"
+    bool skip = false;
+    for (int i = 0; i < n_skip; ++i) skip |= skip_ids[i] == b;
+    if ((lane % R) == 0 && b < nblocks && !skip)
+      atomicMax(&keys[static_cast<int64_t>(layer) * nblocks + b], score_key(best));
+  }
 }
 
 // One (tile, head) unit per wavefront (any nq).
@@ -327,7 +415,7 @@ template <int R, int G>
 __global__ __launch_bounds__(kScoreThreads) void score_kernel(
     const uint16_t* __restrict__ q, int64_t q_ls, int nq, int per_query,
     const uint16_t* __restrict__ reps, int64_t reps_ls, int hkv, int cap,
-    int nblocks, int units, uint32_t* __restrict__ keys) {
+    int nblocks, int units, uint32_t* __restrict__ keys, const int32_t* __restrict__ skip_ids, int n_skip) {
   __shared__ uint4 stage[kScoreWaves][64 * 8];  // per wave: 64 rows x 8 chunks (one half), swizzled
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // the 4 waves of a workgroup take 4 consecutive tiles of one KV head
@@ -338,7 +426,8 @@ __global__ __launch_bounds__(kScoreThreads) void score_kernel(
   const int lane = threadIdx.x & 63;
   ScoreTile<G> t;
   score_load<R, G>(q, q_ls, reps, reps_ls, hkv, cap, nblocks, blockIdx.y, unit, lane, t);
-  score_dots<R, G>(q, q_ls, nq, per_query, hkv, nblocks, keys, blockIdx.y, unit, lane, t, stage[wave]);
+  score_dots<R, G>(q, q_ls, nq, per_query, hkv, nblocks, keys, blockIdx.y, unit, lane, t, stage[wave], skip_ids,
+                   n_skip);
 }
 
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
@@ -489,7 +578,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
 }
 
 // One wavefront per (layer[, query]) row.
-template <int J>
+template <int J, bool STEP>
 __global__ __launch_bounds__(kWave) void topk_wave_kernel(
     uint32_t* __restrict__ score_keys, int nblocks, const int32_t* __restrict__ prot,
     int nprot, int k_req, int order, int32_t* __restrict__ out_ids,
@@ -497,7 +586,7 @@ __global__ __launch_bounds__(kWave) void topk_wave_kernel(
   __shared__ uint32_t pmask[J * 2];  // protected bitmap, one bit per block
   __shared__ unsigned long long sel[kMaxTopk];
   const int64_t row = blockIdx.x;
-  select_row_wave<J>(score_keys + row * nblocks, nblocks, prot, nprot, k_req, order,
+  select_row_wave<J, STEP>(score_keys + row * nblocks, nblocks, prot, nprot, k_req, order,
                      out_ids + row * k_stride, out_vals ? out_vals + row * k_stride : nullptr,
                      out_scores ? out_scores + row * nblocks : nullptr, pmask, sel, threadIdx.x);
 }
@@ -579,48 +668,66 @@ __global__ __launch_bounds__(kUnionThreads) void union_kernel(
   }
 }
 
-// NANOKV_TOPK_WAVE=0 keeps every row on the workgroup top-k kernel (A/B and
-// cross-checks of the two selection kernels).
-bool topk_wave_enabled() {
-  static const bool on = [] {
-    const char* e = getenv("NANOKV_TOPK_WAVE");
-    return !(e && e[0] == '0');
-  }();
-  return on;
-}
+struct ScoreLaunch {
+  const uint16_t* q;
+  int64_t q_ls;
+  int nq, per_query;
+  const uint16_t* reps;
+  int64_t reps_ls;
+  int hkv, cap, nblocks, units;
+  uint32_t* keys;
+  const int32_t* skip_ids;
+  int n_skip;
+};
 
 template <int R, int G>
-void launch_score(dim3 grid, hipStream_t s, const uint16_t* q, int64_t q_ls, int nq,
-                  int per_query, const uint16_t* reps, int64_t reps_ls, int hkv, int cap,
-                  int nblocks, int units, uint32_t* keys) {
-  hipLaunchKernelGGL((score_kernel<R, G>), grid, dim3(kScoreThreads), 0, s, q, q_ls, nq,
-                     per_query, reps, reps_ls, hkv, cap, nblocks, units, keys);
+void launch_score(dim3 grid, hipStream_t s, const ScoreLaunch& a) {
+  hipLaunchKernelGGL((score_kernel<R, G>), grid, dim3(kScoreThreads), 0, s, a.q, a.q_ls, a.nq, a.per_query, a.reps,
+                     a.reps_ls, a.hkv, a.cap, a.nblocks, a.units, a.keys, a.skip_ids, a.n_skip);
 }
 
 template <int R>
-int dispatch_g(int g, dim3 grid, hipStream_t s, const uint16_t* q, int64_t q_ls, int nq,
-               int per_query, const uint16_t* reps, int64_t reps_ls, int hkv, int cap,
-               int nblocks, int units, uint32_t* keys) {
+int dispatch_g(int g, dim3 grid, hipStream_t s, const ScoreLaunch& a) {
   switch (g) {
-    case 1: launch_score<R, 1>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
-    case 2: launch_score<R, 2>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
-    case 4: launch_score<R, 4>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
-    case 8: launch_score<R, 8>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
-    case 16: launch_score<R, 16>(grid, s, q, q_ls, nq, per_query, reps, reps_ls, hkv, cap, nblocks, units, keys); return 0;
+    case 1: launch_score<R, 1>(grid, s, a); return 0;
+    case 2: launch_score<R, 2>(grid, s, a); return 0;
+    case 4: launch_score<R, 4>(grid, s, a); return 0;
+    case 8: launch_score<R, 8>(grid, s, a); return 0;
+    case 16: launch_score<R, 16>(grid, s, a); return 0;
     default: return -1;
   }
 }
+
+template <bool STEP>
+void launch_topk_wave(int nblocks, dim3 rows, hipStream_t s, uint32_t* keys, const int32_t* prot, int nprot, int k,
+                      int order, int32_t* out_ids, float* out_vals, float* out_scores) {
+  if (nblocks <= 8 * kWave)
+    hipLaunchKernelGGL((topk_wave_kernel<8, STEP>), rows, dim3(kWave), 0, s, keys, nblocks, prot, nprot, k, order,
+                       out_ids, out_vals, k, out_scores);
+  else if (nblocks <= 16 * kWave)
+    hipLaunchKernelGGL((topk_wave_kernel<16, STEP>), rows, dim3(kWave), 0, s, keys, nblocks, prot, nprot, k, order,
+                       out_ids, out_vals, k, out_scores);
+  else
+    hipLaunchKernelGGL((topk_wave_kernel<32, STEP>), rows, dim3(kWave), 0, s, keys, nblocks, prot, nprot, k, order,
+                       out_ids, out_vals, k, out_scores);
+}
+
+// Protected lists up to this length are handled inside the decode step's
+// scorer (one uniform comparison per entry and block); longer ones take the
+// general selection.
+constexpr int kMaxStepSkip = 64;
 
 }  // namespace
 }  // namespace nkv
 
 using namespace nkv;
 
-extern "C" int nkv_select(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
-                          int64_t q_layer_stride, int nq, int per_query, int nblocks,
-                          const int32_t* protected_ids, int n_protected, int k, int order,
-                          uint32_t* score_keys, float* out_scores, int32_t* out_ids,
-                          float* out_vals, void* stream) {
+namespace nkv {
+
+int select_impl(const nkv_store* st, int layer0, int num_layers, const uint16_t* q, int64_t q_layer_stride, int nq,
+                int per_query, int nblocks, const int32_t* protected_ids, int n_protected, int k, int order,
+                uint32_t* score_keys, float* out_scores, int32_t* out_ids, float* out_vals, bool step,
+                void* stream) {
   int rc = check_store(st, layer0, num_layers);
   if (rc != NKV_OK) return rc;
   NKV_CHECK_ARG(q != nullptr && score_keys != nullptr && out_ids != nullptr,
@@ -635,22 +742,37 @@ extern "C" int nkv_select(const nkv_store* st, int layer0, int num_layers, const
   NKV_CHECK_ARG(order == NKV_ORDER_SCORE_DESC || order == NKV_ORDER_ID_ASC, "nkv_select: unknown order %d", order);
   NKV_CHECK_ARG(q_layer_stride >= static_cast<int64_t>(nq) * st->num_heads * kHeadDim || num_layers == 1,
                 "nkv_select: q_layer_stride too small");
+  // the decode step's form: one query, no raw scores / values, a short
+  // protected list, rows the wave top-k covers
+  step = step && nq == 1 && !per_query && out_scores == nullptr && out_vals == nullptr &&
+         n_protected <= kMaxStepSkip && nblocks <= 32 * kWave;
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int g = st->num_heads / st->num_kv_heads;
   const int R = st->r;
   const int TB = kWave / R;
   const int nqo = per_query ? nq : 1;
-  const int64_t reps_ls = static_cast<int64_t>(st->num_kv_heads) * st->cap_blocks * R * kHeadDim;
-  const uint16_t* reps = static_cast<const uint16_t*>(st->reps) + layer0 * reps_ls;
-  const int units = ((nblocks + TB - 1) / TB) * st->num_kv_heads;
-  dim3 grid(((units / st->num_kv_heads + kScoreWaves - 1) / kScoreWaves) * st->num_kv_heads, num_layers);
+  ScoreLaunch a;
+  a.q = q;
+  a.q_ls = q_layer_stride;
+  a.nq = nq;
+  a.per_query = per_query;
+  a.reps_ls = static_cast<int64_t>(st->num_kv_heads) * st->cap_blocks * R * kHeadDim;
+  a.reps = static_cast<const uint16_t*>(st->reps) + layer0 * a.reps_ls;
+  a.hkv = st->num_kv_heads;
+  a.cap = st->cap_blocks;
+  a.nblocks = nblocks;
+  a.units = ((nblocks + TB - 1) / TB) * st->num_kv_heads;
+  a.keys = score_keys;
+  a.skip_ids = step ? protected_ids : nullptr;
+  a.n_skip = step ? n_protected : 0;
+  dim3 grid(((a.units / st->num_kv_heads + kScoreWaves - 1) / kScoreWaves) * st->num_kv_heads, num_layers);
   int bad = 0;
   switch (R) {
-    case 1: bad = dispatch_g<1>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
-    case 2: bad = dispatch_g<2>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
-    case 4: bad = dispatch_g<4>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
-    case 8: bad = dispatch_g<8>(g, grid, s, q, q_layer_stride, nq, per_query, reps, reps_ls, st->num_kv_heads, st->cap_blocks, nblocks, units, score_keys); break;
+    case 1: bad = dispatch_g<1>(g, grid, s, a); break;
+    case 2: bad = dispatch_g<2>(g, grid, s, a); break;
+    case 4: bad = dispatch_g<4>(g, grid, s, a); break;
+    case 8: bad = dispatch_g<8>(g, grid, s, a); break;
     default: bad = -1;
   }
   NKV_CHECK_SUPPORTED(bad == 0, "nkv_select: unsupported (r=%d, G=%d)", R, g);
@@ -658,16 +780,13 @@ extern "C" int nkv_select(const nkv_store* st, int layer0, int num_layers, const
   if (rc != NKV_OK) return rc;
 
   const dim3 rows(num_layers * nqo);
-  if (topk_wave_enabled() && nblocks <= 32 * kWave) {
-    if (nblocks <= 8 * kWave)
-      hipLaunchKernelGGL(topk_wave_kernel<8>, rows, dim3(kWave), 0, s, score_keys, nblocks,
-                         protected_ids, n_protected, k, order, out_ids, out_vals, k, out_scores);
-    else if (nblocks <= 16 * kWave)
-      hipLaunchKernelGGL(topk_wave_kernel<16>, rows, dim3(kWave), 0, s, score_keys, nblocks,
-                         protected_ids, n_protected, k, order, out_ids, out_vals, k, out_scores);
-    else
-      hipLaunchKernelGGL(topk_wave_kernel<32>, rows, dim3(kWave), 0, s, score_keys, nblocks,
-                         protected_ids, n_protected, k, order, out_ids, out_vals, k, out_scores);
+  if (step) {
+    launch_topk_wave<true>(nblocks, rows, s, score_keys, nullptr, 0, k, order, out_ids, nullptr, nullptr);
+    return launch_status("nkv_select/topk");
+  }
+  if (nblocks <= 32 * kWave) {
+    launch_topk_wave<false>(nblocks, rows, s, score_keys, protected_ids, n_protected, k, order, out_ids, out_vals,
+                            out_scores);
     return launch_status("nkv_select/topk");
   }
   const int nwords = (nblocks + 31) >> 5;
@@ -675,6 +794,21 @@ extern "C" int nkv_select(const nkv_store* st, int layer0, int num_layers, const
   hipLaunchKernelGGL(topk_kernel, rows, dim3(kTopkThreads), tsmem, s, score_keys,
                      nblocks, protected_ids, n_protected, k, order, out_ids, out_vals, k, out_scores);
   return launch_status("nkv_select/topk");
+}
+
+bool select_step_form(int nq, int n_protected, int nblocks) {
+  return nq == 1 && n_protected <= kMaxStepSkip && nblocks <= 32 * kWave;
+}
+
+}  // namespace nkv
+
+extern "C" int nkv_select(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
+                          int64_t q_layer_stride, int nq, int per_query, int nblocks,
+                          const int32_t* protected_ids, int n_protected, int k, int order,
+                          uint32_t* score_keys, float* out_scores, int32_t* out_ids,
+                          float* out_vals, void* stream) {
+  return select_impl(st, layer0, num_layers, q, q_layer_stride, nq, per_query, nblocks, protected_ids, n_protected,
+                     k, order, score_keys, out_scores, out_ids, out_vals, false, stream);
 }
 
 extern "C" int nkv_select_union(const int32_t* ids, int num_layers, int tq, int k, int k_eff, int umax,

@@ -19,7 +19,7 @@
 #include <mutex>
 #include <vector>
 
-#include "nkv_common.h"
+#include "nkv_attend_common.h"
 
 namespace nkv {
 namespace {
@@ -150,6 +150,19 @@ extern "C" int nkv_decode_step(const nkv_store* st, int layer0, int num_layers, 
   const int per = (num_layers + nranges - 1) / nranges;
   const int64_t ws_range = nkv_attend_workspace_floats(per, st->num_kv_heads, st->num_heads, 1, splits);
 
+  // the attention arguments are checked before anything is enqueued (the
+  // selection's step form leaves the keys for the attention launch to clear)
+  for (int r = 0; r < nranges; ++r) {
+    const int l0 = static_cast<int>(static_cast<int64_t>(r) * num_layers / nranges);
+    const int l1 = static_cast<int>(static_cast<int64_t>(r + 1) * num_layers / nranges);
+    attend_detail::AttendParams p;
+    rc = fill_attend_params("nkv_decode_step", st, layer0 + l0, l1 - l0, q + l0 * q_ls, q_ls, 1, k_new + l0 * kv_ls,
+                            v_new + l0 * kv_ls, kv_ls, 1, write_slot, out_ids + static_cast<int64_t>(l0) * k, k,
+                            n_hist, nullptr, 0, sink_len, ring_base, rec_lo, rec_len, scale, splits,
+                            partial_ws ? partial_ws + r * ws_range : nullptr, out + l0 * q_ls, &p);
+    if (rc != NKV_OK) return rc;
+  }
+
   hipStream_t s0 = reinterpret_cast<hipStream_t>(streams[0]);
   hipEvent_t ev[kMaxStepStreams];
   if (nranges > 1) {
@@ -166,14 +179,16 @@ extern "C" int nkv_decode_step(const nkv_store* st, int layer0, int num_layers, 
       const hipError_t e = hipStreamWaitEvent(reinterpret_cast<hipStream_t>(sr), ev[0], 0);
       if (e != hipSuccess) return hip_fail(e, "nkv_decode_step: hipStreamWaitEvent");
     }
-    rc = nkv_select(st, layer0 + l0, nl, q + l0 * q_ls, q_ls, 1, 0, nblocks, protected_ids, n_protected, k,
-                    NKV_ORDER_SCORE_DESC, score_keys + static_cast<int64_t>(l0) * nblocks, nullptr,
-                    out_ids + static_cast<int64_t>(l0) * k, nullptr, sr);
+    // the selection's step form leaves the keys for the attention launch to clear
+    uint32_t* keys = score_keys + static_cast<int64_t>(l0) * nblocks;
+    rc = select_impl(st, layer0 + l0, nl, q + l0 * q_ls, q_ls, 1, 0, nblocks, protected_ids, n_protected, k,
+                     NKV_ORDER_SCORE_DESC, keys, nullptr, out_ids + static_cast<int64_t>(l0) * k, nullptr, true, sr);
     if (rc != NKV_OK) return rc;
-    rc = nkv_attend(st, layer0 + l0, nl, q + l0 * q_ls, q_ls, 1, k_new + l0 * kv_ls, v_new + l0 * kv_ls, kv_ls,
-                    1, write_slot, out_ids + static_cast<int64_t>(l0) * k, k, n_hist, nullptr, 0, sink_len,
-                    ring_base, rec_lo, rec_len, scale, splits, partial_ws ? partial_ws + r * ws_range : nullptr,
-                    out + l0 * q_ls, sr);
+    const bool step_keys = select_step_form(1, n_protected, nblocks);
+    rc = attend_impl(st, layer0 + l0, nl, q + l0 * q_ls, q_ls, 1, k_new + l0 * kv_ls, v_new + l0 * kv_ls, kv_ls,
+                     1, write_slot, out_ids + static_cast<int64_t>(l0) * k, k, n_hist, nullptr, 0, sink_len,
+                     ring_base, rec_lo, rec_len, scale, splits, partial_ws ? partial_ws + r * ws_range : nullptr,
+                     out + l0 * q_ls, step_keys ? keys : nullptr, nblocks, sr);
     if (rc != NKV_OK) return rc;
     if (r > 0) {
       const hipError_t e = hipEventRecord(ev[r], reinterpret_cast<hipStream_t>(sr));

@@ -232,3 +232,31 @@ def test_layer_streams_identical_to_one_stream(streams):
         assert torch.equal(one.last_ids_dev[:, :, :n], many.last_ids_dev[:, :, :n])
         assert torch.equal(o1, o2)
         assert many.valid_len == one.valid_len
+
+
+@pytest.mark.parametrize("quant", [False, True])
+def test_decode_step_selection_with_tied_scores(quant):
+    """nkv_decode_step's selection (protected blocks left unscored by the
+    scorer, keys cleared by the attention launch) on layers whose scores tie
+    heavily: random, half the blocks all-zero, all zero.  Ids equal the
+    oracle's top-k of the oracle's scores over the same representatives, step
+    after step (the keys start from zero every step)."""
+    from nanokv_amd import workload
+    from nanokv_amd.sparse import M12Config, M12ModelRuntime
+    L, T = 3, 8192
+    model = M12ModelRuntime(L, M12Config(max_model_len=T + 64, quant_history=quant))
+    hist = [workload.history(T, 400 + i) for i in range(L)]
+    model.prefill(torch.stack([h[0] for h in hist]).cuda(), torch.stack([h[1] for h in hist]).cuda())
+    nb = model.nblocks_filled
+    reps = model.store.reps[:, :, :nb]
+    reps[1, :, ::2] = 0
+    reps[2].zero_()
+    prot = model.core.protected_blocks
+    qs, ks, vs = workload.decode_inputs(3, 41, layers=L)
+    for s in range(3):
+        model.decode(qs[s].cuda(), ks[s].cuda(), vs[s].cuda())
+        ids = model.last_ids_dev[:, 0, :model.last_n_selected].cpu()
+        for i in range(L):
+            s_or = O.block_scores(to_np(qs[s, i]), to_np(reps[i]), nb, 8)
+            ids_or, _ = O.topk_blocks(s_or, prot, 32)
+            assert ids[i].tolist() == ids_or.tolist(), f"step {s} layer {i}"

@@ -210,3 +210,36 @@ def test_select_union_matches_unique_and_searchsorted(L, tq, k, k_eff, hi, seed)
         for t in range(tq):
             want[t, np.searchsorted(u, ids[l, t, :k_eff])] = 1
         assert np.array_equal(allowed[l], want)
+
+
+def _pattern_reps(pattern, nb, r, seed):
+    """Representatives whose scores tie a lot: 'zero_half' (every other block
+    all-zero: score 0), 'levels' (reps = +-1/16 patterns shared by groups of
+    blocks: a handful of distinct scores), 'equal' (all zero)."""
+    g = torch.Generator().manual_seed(seed)
+    reps = torch.randn(HKV, nb, r, D, generator=g) / D ** 0.5
+    if pattern == "zero_half":
+        reps[:, ::2] = 0.0
+    elif pattern == "levels":
+        base = torch.sign(torch.randn(HKV, 5, r, D, generator=g)) / 16
+        reps = base[:, torch.randint(0, 5, (nb,), generator=g)]
+    elif pattern == "equal":
+        reps.zero_()
+    return reps.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("pattern", ["random", "zero_half", "levels", "equal"])
+@pytest.mark.parametrize("nb,budget", [(40, 32), (512, 32), (512, 64), (2048, 1), (700, 48)])
+def test_topk_short_candidate_path_and_full_search_give_the_same_ids(pattern, nb, budget):
+    """The wave top-k ranks a short candidate list when at most 64 keys reach
+    the k-th largest lane maximum and searches all keys otherwise (ties,
+    equal scores); either way the ids equal the oracle's (score desc, id asc)."""
+    rt = _runtime(nb, top_k=max(budget, 32))
+    reps = _pattern_reps(pattern, nb, 4, nb + budget)
+    rt.reps_gpu[:, :nb].copy_(reps.cuda())
+    rt.protected_blocks = O.protected_blocks_after_store(nb, 512, 64)
+    q = _rand_q(1, nb)
+    ids, _ = rt._gpu_select(q.cuda(), budget=budget)
+    s_or = O.block_scores(to_np(q), to_np(reps), nb, HKV)
+    ids_or, _ = O.topk_blocks(s_or, rt.protected_blocks, budget)
+    assert ids.tolist() == ids_or.tolist()

@@ -22,6 +22,7 @@ a model in one launch per stage.
 
 from __future__ import annotations
 
+import ctypes
 import math
 from contextlib import nullcontext
 from dataclasses import dataclass
@@ -1273,28 +1274,57 @@ class M12ModelRuntime:
     def decode(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         """One decode step for every layer: q [L, 1, Hq, D], k/v [L, 1, Hkv, D] -> o [L, 1, Hq, D]."""
         cfg, core = self.cfg, self.core
-        if core.nblocks_filled <= 0:
+        nb = core.nblocks_filled
+        if nb <= 0:
             raise ValueError("selection needs at least one history block")
-        req = cfg.top_k_blocks if cfg.decode_top_k_blocks is None else cfg.decode_top_k_blocks
-        L, nb = self.num_layers, core.nblocks_filled
-        dev = self.store.device
+        L = self.num_layers
+        if (q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16
+                or tuple(q.shape) != (L, 1, cfg.num_heads, cfg.head_dim)
+                or tuple(k.shape) != (L, 1, cfg.num_kv_heads, cfg.head_dim) or k.shape != v.shape
+                or not (q.is_cuda and k.is_cuda and v.is_cuda)):
+            raise ValueError(f"decode expects bf16 device tensors q [{L}, 1, {cfg.num_heads}, {cfg.head_dim}] "
+                             f"and k, v [{L}, 1, {cfg.num_kv_heads}, {cfg.head_dim}]")
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        w = core.decode_window()
+        plan = self._step_plan(nb, w)
+        out = torch.empty_like(q)
+        ids = torch.empty(L, 1, plan["req"], dtype=torch.int32, device=q.device)
+        _lib.check(self.store.lib.nkv_decode_step(
+            self.store._desc_ref, 0, L, q.data_ptr(), k.data_ptr(), v.data_ptr(), nb, plan["prot_ptr"],
+            plan["n_prot"], plan["req"], plan["n"], w["sink_len"], w["write_slot"], w["ring_base"], w["rec_lo"],
+            w["rec_len"], plan["scale"], plan["splits"], plan["keys_ptr"], ids.data_ptr(), plan["part_ptr"],
+            out.data_ptr(), plan["nstreams"], plan["streams"]), "decode_step")
+        core.advance_decode()
+        self.last_ids_dev = ids
+        self.last_n_selected = plan["n"]
+        return out
+
+    def _step_plan(self, nb: int, w: dict) -> dict:
+        """The decode step's launch arguments that only change with the history
+        length, the protected set, the window shape and the current stream
+        (workspaces, split count, effective budget, the stream list)."""
+        cfg, core = self.cfg, self.core
+        prot, n_prot = core.protected_dev()
+        dev = self.store.device
+        cur = torch.cuda.current_stream(dev).cuda_stream
+        key = (nb, core._prot_key, w["sink_len"], w["rec_len"] > 0, cur, cfg.top_k_blocks, cfg.decode_top_k_blocks,
+               cfg.attend_splits, cfg.scale)
+        plan = getattr(self, "_plan", None)
+        if plan is not None and plan["key"] == key:
+            return plan
+        req = cfg.top_k_blocks if cfg.decode_top_k_blocks is None else cfg.decode_top_k_blocks
+        L = self.num_layers
         if len(self._side_streams) < self.layer_streams - 1:
             self._side_streams = [torch.cuda.Stream(dev) for _ in range(self.layer_streams - 1)]
-        streams = [torch.cuda.current_stream(dev).cuda_stream] + [s.cuda_stream for s in self._side_streams]
-        prot, n_prot = core.protected_dev()
+        streams = [cur] + [s.cuda_stream for s in self._side_streams[:self.layer_streams - 1]]
         n = core.effective_k(req)
         splits = core.decode_splits(n)
-        w = core.decode_window()
-        out = torch.empty_like(q)
-        ids = torch.empty(L, 1, req, dtype=torch.int32, device=dev)
         keys = core._zeroed_keys(L * nb, "/step")
         part = core._buf("partial/step", self.store.decode_step_workspace_floats(L, splits, len(streams)),
                          torch.float32)
-        self.store.decode_step(0, q, k, v, nb, prot, n_prot, req, n, w["sink_len"], w["write_slot"],
-                               w["ring_base"], w["rec_lo"], w["rec_len"], cfg.scale, splits, keys, ids,
-                               part, out, streams)
-        core.advance_decode()
-        self.last_ids_dev = ids
-        self.last_n_selected = n
-        return out
+        plan = {"key": key, "req": req, "n": n, "splits": splits, "n_prot": n_prot, "scale": float(cfg.scale),
+                "prot_ptr": prot.data_ptr(), "keys_ptr": keys.data_ptr(), "part_ptr": part.data_ptr(),
+                "nstreams": len(streams), "streams": (ctypes.c_void_p * len(streams))(*streams),
+                "_keep": (prot, keys, part)}
+        self._plan = plan
+        return plan

@@ -185,7 +185,8 @@ def bench_prefill(args, dev):
     L, T0, T = args.layers, args.context, args.chunk
     quant = args.kv_format != "bf16"
     cfg = M12Config(max_model_len=T0 + T, top_k_blocks=args.top_k, quant_history=quant,
-                    quant_scale_layout="token" if args.kv_format == "int8_token" else "channel_block")
+                    quant_scale_layout="token" if args.kv_format == "int8_token" else "channel_block",
+                    prefill_selection=args.prefill_selection)
     model = M12ModelRuntime(L, cfg, device=dev)
     kh = torch.empty(L, T0, 8, 128, dtype=torch.bfloat16, device=dev)
     vh = torch.empty_like(kh)
@@ -198,12 +199,20 @@ def bench_prefill(args, dev):
     q, k, v = workload.prefill_chunk_inputs(T, args.seed, device=dev, layers=L)
     core = model.core
 
+    tile = cfg.prefill_selection_tile
+
     def step(ev=None):
-        qs = query_summaries(q, cfg.prefill_query_segments)
-        ids, _, n = core.select(qs, args.top_k)
+        if cfg.prefill_selection == "tile":
+            ids, n = core.select_tiles(q, args.top_k, tile)
+        else:
+            qs = query_summaries(q, cfg.prefill_query_segments)
+            ids, _, n = core.select(qs, args.top_k)
         if ev is not None:
             ev[0].record()
-        out, _, _ = core.chunk_attend(q, k, v, ids, ids.shape[-1], n)
+        if cfg.prefill_selection == "tile":
+            out, _, _ = core.chunk_attend_tiled(q, k, v, ids, tile, n)
+        else:
+            out, _, _ = core.chunk_attend(q, k, v, ids, ids.shape[-1], n)
         if ev is not None:
             ev[1].record()
         return out
@@ -243,8 +252,10 @@ def bench_prefill(args, dev):
             "workload": (f"chunked prefill, {T}-token chunk vs {T0}-token history x {L} layers, "
                          f"Qwen3-4B attention shape (Hq=32, Hkv=8, D=128), top-{args.top_k} + sink "
                          f"{cfg.sink_tokens} + recent {cfg.recent_tokens} + causal chunk, "
-                         f"{args.kv_format} history"),
+                         f"{args.kv_format} history, selection per "
+                         + ("chunk" if cfg.prefill_selection == "chunk" else f"{tile}-query tile")),
             "layers": L, "context": T0, "chunk": T, "top_k": args.top_k, "kv_format": args.kv_format,
+            "prefill_selection": cfg.prefill_selection,
         },
         "tokens_per_s": round(T * 1e3 / ms_step, 1),
         "flops_per_step": flops,
@@ -474,6 +485,8 @@ def main():
                          "lossless speculative verify (use --context 16384), or whole-model "
                          "Qwen3-4B decode (tokens/s = 1 / TPOT)")
     ap.add_argument("--chunk", type=int, default=4096, help="prefill chunk length")
+    ap.add_argument("--prefill-selection", choices=["chunk", "tile"], default="chunk",
+                    help="prefill: one selection per chunk (the reference's routing) or per 64-query tile")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (counter calibration)")
     args = ap.parse_args()

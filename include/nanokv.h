@@ -306,6 +306,28 @@ int64_t nkv_prefill_workspace_floats(int num_layers, int num_kv_heads, int num_h
                                      int splits);
 
 /*
+ * nkv_prefill_attend with one history selection per tile of `sel_tile`
+ * queries instead of one per chunk: query t attends the n_hist blocks
+ * ids[l][(t / sel_tile) * ids_tile_stride + i], then the sink, the previous
+ * recent window and the chunk (causal), as nkv_prefill_attend.  No reference
+ * counterpart: the reference selects once per chunk from its query summaries
+ * (m12_runtime.py:550-556); this is that selection applied to each tile of a
+ * chunk (the per-tile summaries come from nkv_query_summaries, the per-tile
+ * ids from nkv_select with per_query = 1).  No per-query mask.
+ * Constraints: sel_tile a positive multiple of 128 / G tokens (the
+ * workgroup's query tile); ids_tile_stride >= n_hist; ids_layer_stride >=
+ * ceil(tq / sel_tile) * ids_tile_stride; otherwise as nkv_prefill_attend
+ * (partial_ws: nkv_prefill_workspace_floats floats when splits > 1).
+ */
+int nkv_prefill_attend_tiled(const nkv_store* st, int layer0, int num_layers,
+                             const uint16_t* q, int64_t q_layer_stride, int tq,
+                             const uint16_t* k_new, const uint16_t* v_new, int64_t kv_layer_stride,
+                             const int32_t* ids, int64_t ids_layer_stride, int64_t ids_tile_stride,
+                             int sel_tile, int n_hist, int sink_len, int ring_base, int rec_lo,
+                             int rec_len, float scale, int splits, float* partial_ws, uint16_t* out,
+                             void* stream);
+
+/*
  * Exact attention over caller-packed keys: M12LayerRuntime._fused_attention
  * (nanovllm/sparse/m12_runtime.py:845-896), the reference's inspectable
  * attention over [selected | sink | recent | chunk] that its packing paths

@@ -94,7 +94,10 @@ constexpr int kVTileBytes = kBlock * kHeadDim * 2;   // one bf16 V tile in LDS
 static_assert(2 * kAttendWaves * kMaxRows + kAttendWaves * 4 * kHeadDim <= kAttendWaves * kVTileBytes / 4,
               "the cross-wave merge fits in the V tiles");
 
-template <int FMT, int M>
+// PACKED: caller-packed keys (nkv_attend_packed): the chunk's causal start is
+// causal_off and an optional per-token mask applies; its own instantiation,
+// so the decode and verify paths carry none of that code.
+template <int FMT, int M, bool PACKED>
 __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 1) void attend_kernel(const AttendParams p) {
   constexpr bool kMfmaPV = attend_mfma_pv<FMT, M>();
   __shared__ __attribute__((aligned(16))) float s_lds[kMfmaPV ? kAttendWaves * kVTileBytes / 4 : attend_lds_floats<M>()];
@@ -294,9 +297,13 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
           if (lp < 0) lp += p.R;
           ok = ok && static_cast<unsigned>(lp - p.rec_lo) < static_cast<unsigned>(p.rec_len);
         } else if (g.type == kSegChunk) {
-          ok = ok && (g.off + tk) - p.causal_off <= my_t;
-          if (ok && p.tok_mask != nullptr)
-            ok = p.tok_mask[static_cast<int64_t>(my_t) * p.n_chunk + g.off + tk] == 0;
+          if constexpr (PACKED) {
+            ok = ok && (g.off + tk) - p.causal_off <= my_t;
+            if (ok && p.tok_mask != nullptr)
+              ok = p.tok_mask[static_cast<int64_t>(my_t) * p.n_chunk + g.off + tk] == 0;
+          } else {
+            ok = ok && (g.off + tk) <= my_t;
+          }
         }
         if (FMT == NKV_KV_INT8_TOKEN && int8_seg)
           v *= f16_bits_to_f32(p.k_tscale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap * kBlock +
@@ -534,12 +541,12 @@ __global__ __launch_bounds__(kWave) void ring_advance_kernel(int32_t* ring_start
   }
 }
 
-template <int FMT>
+template <int FMT, bool PACKED = false>
 int launch_fmt(int M, dim3 grid, hipStream_t s, const AttendParams& p) {
   switch (M) {
-    case 4: hipLaunchKernelGGL((attend_kernel<FMT, 4>), grid, dim3(kAttendThreads), 0, s, p); return 0;
-    case 8: hipLaunchKernelGGL((attend_kernel<FMT, 8>), grid, dim3(kAttendThreads), 0, s, p); return 0;
-    case 16: hipLaunchKernelGGL((attend_kernel<FMT, 16>), grid, dim3(kAttendThreads), 0, s, p); return 0;
+    case 4: hipLaunchKernelGGL((attend_kernel<FMT, 4, PACKED>), grid, dim3(kAttendThreads), 0, s, p); return 0;
+    case 8: hipLaunchKernelGGL((attend_kernel<FMT, 8, PACKED>), grid, dim3(kAttendThreads), 0, s, p); return 0;
+    case 16: hipLaunchKernelGGL((attend_kernel<FMT, 16, PACKED>), grid, dim3(kAttendThreads), 0, s, p); return 0;
     default: return -1;
   }
 }
@@ -564,8 +571,12 @@ int launch_grouped(int hkv, int kv_format, int num_layers, int tq, AttendParams&
   p.nqg = (tq + qpg - 1) / qpg;
   dim3 grid(p.splits, hkv, num_layers * p.nqg);
   int bad = 0;
+  const bool packed = p.tok_mask != nullptr || p.causal_off != 0;
+  NKV_CHECK_SUPPORTED(!packed || kv_format == NKV_KV_BF16, "nkv_attend: caller-packed keys must be bf16");
   switch (kv_format) {
-    case NKV_KV_BF16: bad = launch_fmt<NKV_KV_BF16>(M, grid, s, p); break;
+    case NKV_KV_BF16:
+      bad = packed ? launch_fmt<NKV_KV_BF16, true>(M, grid, s, p) : launch_fmt<NKV_KV_BF16>(M, grid, s, p);
+      break;
     case NKV_KV_INT8_CHANNEL: bad = launch_fmt<NKV_KV_INT8_CHANNEL>(M, grid, s, p); break;
     case NKV_KV_INT8_TOKEN: bad = launch_fmt<NKV_KV_INT8_TOKEN>(M, grid, s, p); break;
     default: bad = -1;
@@ -688,6 +699,8 @@ int fill_attend_params(const char* who, const nkv_store* st, int layer0, int num
   p.tok_mask = nullptr;
   p.zero_keys = nullptr;
   p.zero_n = 0;
+  p.ids_tile_ls = 0;
+  p.sel_tile = 0;
   return NKV_OK;
 }
 

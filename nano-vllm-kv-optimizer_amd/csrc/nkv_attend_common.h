@@ -68,6 +68,11 @@ struct AttendParams {
   // (the decode step's score keys, consumed by the top-k launch before it)
   uint32_t* zero_keys;
   int zero_n;
+  // per-query-tile selection (matrix-core kernel): with sel_tile > 0 the
+  // queries t of tile t / sel_tile attend the history blocks
+  // ids[layer][tile * ids_tile_ls + i]
+  int64_t ids_tile_ls;
+  int sel_tile;
 };
 
 __device__ __forceinline__ void wave_lds_sync() {

@@ -159,12 +159,14 @@ __device__ __forceinline__ void dequant_i8(const AttendParams& p, const Seg& g, 
 
 // Whether any (key, column) of segment g may be invisible to the workgroup's
 // tokens t0.. (otherwise the mask pass is skipped).
+template <bool PACKED>
 __device__ __forceinline__ bool needs_mask(const AttendParams& p, const Seg& g, int t0) {
   switch (g.type) {
     case kSegHist: return g.vlen < kBlock || p.allowed != nullptr;
     case kSegSink: return g.len < kBlock;
     case kSegRecent: return !(p.rec_len == p.R && g.len == kBlock);
-    default: return g.len < kBlock || g.off + kBlock - 1 - p.causal_off > t0 || p.tok_mask != nullptr;
+    default: return PACKED ? (p.tok_mask != nullptr || g.len < kBlock || g.off + kBlock - 1 - p.causal_off > t0)
+                           : (g.len < kBlock || g.off + kBlock - 1 > t0);
   }
 }
 
@@ -172,6 +174,7 @@ __device__ __forceinline__ bool needs_mask(const AttendParams& p, const Seg& g, 
 // holds key 16 kt + 4 lg + e of column ct.  Key k of the segment is visible
 // to column ct iff k <= thr[ct] (history / sink / chunk), or, for a ring
 // piece, iff k < vlen and the slot's logical position lies in the window.
+template <bool PACKED>
 __device__ __forceinline__ void apply_mask(const AttendParams& p, const Seg& g, int lg, const int (&tcol)[2],
                                            const int (&allow)[2], f32x4 (&S)[4][2]) {
   if (g.type == kSegRecent) {
@@ -195,7 +198,7 @@ __device__ __forceinline__ void apply_mask(const AttendParams& p, const Seg& g, 
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
     int thr = g.vlen - 1;
-    if (g.type == kSegChunk) thr = min(thr, tcol[ct] + p.causal_off - g.off);
+    if (g.type == kSegChunk) thr = min(thr, tcol[ct] + (PACKED ? p.causal_off : 0) - g.off);
     else if (allow[ct] == 0) thr = -1;
     base[ct] = 4 * lg - thr;
   }
@@ -205,7 +208,7 @@ __device__ __forceinline__ void apply_mask(const AttendParams& p, const Seg& g, 
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
       for (int e = 0; e < 4; ++e) S[kt][ct][e] = fminf(S[kt][ct][e], vis_bound(base[ct] + 16 * kt + e));
-  if (g.type == kSegChunk && p.tok_mask != nullptr) {
+  if (PACKED && g.type == kSegChunk && p.tok_mask != nullptr) {
     // caller-packed keys with a per-(query, key) mask: keys past vlen are
     // already hidden and never read; padding columns read row tq - 1
 #pragma unroll
@@ -222,7 +225,10 @@ __device__ __forceinline__ void apply_mask(const AttendParams& p, const Seg& g, 
   }
 }
 
-template <int FMT>
+// PACKED: caller-packed keys (nkv_attend_packed): the chunk's causal start is
+// causal_off and an optional per-token mask applies; its own instantiation,
+// so the history paths carry none of that code.
+template <int FMT, bool PACKED>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendParams p, int nqt) {
   // two stage buffers as separate objects, so that the compiler can tell the
   // buffer being read from the one the asynchronous copies write
@@ -288,7 +294,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
 
   // chunk segments up to the last key visible to the tile's last token
   const int n_chunk_seg =
-      p.n_chunk > 0 ? min((p.n_chunk + kBlock - 1) / kBlock, (t_last + p.causal_off) / kBlock + 1) : 0;
+      p.n_chunk <= 0 ? 0
+                     : (PACKED ? min((p.n_chunk + kBlock - 1) / kBlock, (t_last + p.causal_off) / kBlock + 1)
+                               : t_last / kBlock + 1);
   const int nseg_all = p.n_hist + p.n_sink_seg + p.n_rec_seg + n_chunk_seg;
   // split-K: this workgroup attends segments [seg_lo, nseg) of the list
   const int split = blockIdx.z;
@@ -318,13 +326,17 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
     }
   };
 
+  // this tile's selected history blocks (per-query-tile selection: the ids
+  // of the selection tile holding the workgroup's tokens)
+  const int32_t* ids_row = p.ids + static_cast<int64_t>(layer) * p.ids_ls +
+                           (p.sel_tile > 0 ? static_cast<int64_t>(t0 / p.sel_tile) * p.ids_tile_ls : 0);
   // the next segment at or after s that attends anything (its block id in
   // *blk): history ids outside [0, cap) (a union padded with -1) are passed
   // over, never staged
   auto next_seg = [&](int s, int* blk) {
     *blk = 0;
     for (; s < p.n_hist; ++s) {
-      *blk = p.ids[static_cast<int64_t>(layer) * p.ids_ls + s];
+      *blk = ids_row[s];
       if (*blk >= 0 && *blk < p.cap) break;
     }
     return s;
@@ -370,7 +382,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
         S[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bq[1][ks], S[kt][1], 0, 0, 0);
       }
     }
-    if (needs_mask(p, cur, t0)) apply_mask(p, cur, lg, tcol, allow_cur, S);
+    if (needs_mask<PACKED>(p, cur, t0)) apply_mask<PACKED>(p, cur, lg, tcol, allow_cur, S);
 
     // ---- online softmax (fp32) ----------------------------------------------
     float alpha[2];
@@ -513,13 +525,20 @@ int launch_prefill(int hkv, int kv_format, int num_layers, int tq, AttendParams&
   const int tpw = kPfCols / p.G;
   const int nqt = (tq + tpw - 1) / tpw;
   const dim3 grid(nqt * hkv, num_layers, p.splits);
+  const bool packed = p.tok_mask != nullptr || p.causal_off != 0;
+  NKV_CHECK_SUPPORTED(!packed || kv_format == NKV_KV_BF16, "nkv_prefill_attend: caller-packed keys must be bf16");
   switch (kv_format) {
-    case NKV_KV_BF16: hipLaunchKernelGGL(prefill_kernel<NKV_KV_BF16>, grid, dim3(kPfThreads), 0, s, p, nqt); break;
+    case NKV_KV_BF16:
+      if (packed)
+        hipLaunchKernelGGL((prefill_kernel<NKV_KV_BF16, true>), grid, dim3(kPfThreads), 0, s, p, nqt);
+      else
+        hipLaunchKernelGGL((prefill_kernel<NKV_KV_BF16, false>), grid, dim3(kPfThreads), 0, s, p, nqt);
+      break;
     case NKV_KV_INT8_CHANNEL:
-      hipLaunchKernelGGL(prefill_kernel<NKV_KV_INT8_CHANNEL>, grid, dim3(kPfThreads), 0, s, p, nqt);
+      hipLaunchKernelGGL((prefill_kernel<NKV_KV_INT8_CHANNEL, false>), grid, dim3(kPfThreads), 0, s, p, nqt);
       break;
     case NKV_KV_INT8_TOKEN:
-      hipLaunchKernelGGL(prefill_kernel<NKV_KV_INT8_TOKEN>, grid, dim3(kPfThreads), 0, s, p, nqt);
+      hipLaunchKernelGGL((prefill_kernel<NKV_KV_INT8_TOKEN, false>), grid, dim3(kPfThreads), 0, s, p, nqt);
       break;
     default: NKV_CHECK_SUPPORTED(false, "nkv_prefill_attend: unknown kv_format %d", kv_format);
   }
@@ -560,4 +579,32 @@ extern "C" int nkv_prefill_attend(const nkv_store* st, int layer0, int num_layer
   const int lrc = launch_prefill(st->num_kv_heads, st->kv_format, num_layers, tq, p,
                                  reinterpret_cast<hipStream_t>(stream));
   return lrc != NKV_OK ? lrc : launch_status("nkv_prefill_attend");
+}
+
+extern "C" int nkv_prefill_attend_tiled(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
+                                        int64_t q_layer_stride, int tq, const uint16_t* k_new, const uint16_t* v_new,
+                                        int64_t kv_layer_stride, const int32_t* ids, int64_t ids_layer_stride,
+                                        int64_t ids_tile_stride, int sel_tile, int n_hist, int sink_len, int ring_base,
+                                        int rec_lo, int rec_len, float scale, int splits, float* partial_ws,
+                                        uint16_t* out, void* stream) {
+  AttendParams p;
+  const int rc = fill_attend_params("nkv_prefill_attend_tiled", st, layer0, num_layers, q, q_layer_stride, tq, k_new,
+                                    v_new, kv_layer_stride, tq, -1, ids, ids_layer_stride, n_hist, nullptr, 0,
+                                    sink_len, ring_base, rec_lo, rec_len, scale, splits, partial_ws, out, &p);
+  if (rc != NKV_OK) return rc;
+  NKV_CHECK_SUPPORTED(p.G >= 1 && kPfCols % p.G == 0,
+                      "nkv_prefill_attend_tiled: query heads per KV head (%d) must divide %d", p.G, kPfCols);
+  const int tpw = kPfCols / p.G;
+  NKV_CHECK_ARG(sel_tile >= tpw && sel_tile % tpw == 0,
+                "nkv_prefill_attend_tiled: sel_tile %d must be a positive multiple of the %d-token query tile",
+                sel_tile, tpw);
+  const int ntiles = (tq + sel_tile - 1) / sel_tile;
+  NKV_CHECK_ARG(ids_tile_stride >= n_hist && ids_layer_stride >= static_cast<int64_t>(ntiles) * ids_tile_stride,
+                "nkv_prefill_attend_tiled: id strides too small (tile %lld, layer %lld for %d tiles of %d ids)",
+                static_cast<long long>(ids_tile_stride), static_cast<long long>(ids_layer_stride), ntiles, n_hist);
+  p.ids_tile_ls = ids_tile_stride;
+  p.sel_tile = sel_tile;
+  const int lrc = launch_prefill(st->num_kv_heads, st->kv_format, num_layers, tq, p,
+                                 reinterpret_cast<hipStream_t>(stream));
+  return lrc != NKV_OK ? lrc : launch_status("nkv_prefill_attend_tiled");
 }

@@ -92,6 +92,8 @@ SIGNATURES = {
     "nkv_host_device_pointer": (_I, [_P, ctypes.POINTER(ctypes.c_void_p)]),
     "nkv_attend_packed": (_I, [_I, _I, _P, _I, _P, _P, _I, _I, _P, _F, _I, _P, _P, _P]),
     "nkv_attend_packed_workspace_floats": (_I64, [_I, _I, _I, _I]),
+    "nkv_prefill_attend_tiled": (_I, [_SP, _I, _I, _P, _I64, _I, _P, _P, _I64, _P, _I64, _I64, _I, _I, _I, _I,
+                                      _I, _I, _F, _I, _P, _P, _P]),
     "nkv_decode_step_noalloc": (_I, [_SP, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F,
                                      _I, _P, _P, _P]),
 }

@@ -31,7 +31,7 @@ from time import perf_counter
 import torch
 
 from .. import _lib
-from ..store import SparseKVStore, packed_attention, query_summaries
+from ..store import SparseKVStore, packed_attention, query_summaries, tile_summaries
 
 # ---------------------------------------------------------------------------
 # Host-side helpers (same contracts as the reference's module functions)
@@ -106,6 +106,10 @@ reference's offload mode without its gather and H2D copy).  ``use_index_select``
     ``decode_kv_pipeline`` and ``gather_sort``'s gather-locality purpose
     belong to the host-offload design and do not change the HBM path
     (``gather_sort`` still orders ``last_block_ids`` ascending).
+    ``prefill_selection`` ("chunk": one selection per prefill chunk, the
+    reference's routing; "tile": one per tile of ``prefill_selection_tile``
+    queries, from each tile's bf16 query mean -- no reference counterpart;
+    the tile must be a multiple of 128 / (num_heads / num_kv_heads) tokens).
     """
     block_size: int = 64
     r: int = 4
@@ -143,6 +147,8 @@ reference's offload mode without its gather and H2D copy).  ``use_index_select``
     attend_splits: int | None = None
     mfma_chunk_min_tokens: int | None = None
     history_tier: str = "hbm"
+    prefill_selection: str = "chunk"
+    prefill_selection_tile: int = 64
 
     def __post_init__(self):
         if self.decode_kv_pipeline and not self.use_index_select:
@@ -170,6 +176,10 @@ reference's offload mode without its gather and H2D copy).  ``use_index_select``
             raise ValueError("mfma_chunk_min_tokens must be >= 1 or None")
         if self.history_tier not in ("hbm", "host"):
             raise ValueError("history_tier must be 'hbm' or 'host'")
+        if self.prefill_selection not in ("chunk", "tile"):
+            raise ValueError("prefill_selection must be 'chunk' or 'tile'")
+        if self.prefill_selection_tile < 1:
+            raise ValueError("prefill_selection_tile must be >= 1")
 
     @property
     def kv_format(self) -> str:
@@ -187,6 +197,9 @@ def _check_hip_shapes(cfg: M12Config) -> None:
         raise ValueError("num_heads / num_kv_heads must be 1, 2, 4, 8 or 16")
     if cfg.r not in (1, 2, 4, 8):
         raise ValueError("r must be 1, 2, 4 or 8")
+    tpw = 128 // (cfg.num_heads // cfg.num_kv_heads)
+    if cfg.prefill_selection == "tile" and cfg.prefill_selection_tile % tpw:
+        raise ValueError(f"prefill_selection_tile must be a multiple of {tpw} tokens for this head shape")
 
 
 # ---------------------------------------------------------------------------
@@ -477,6 +490,45 @@ class _SparseCore:
         """Host bookkeeping of one device-ring decode step (the device array moved itself)."""
         self.advance_decode()
         self._ring_dev_pos = self.ring_start
+
+    def select_tiles(self, q, requested: int, tile: int, order: int = _lib.NKV_ORDER_SCORE_DESC):
+        """Per-query-tile selection of a prefill chunk: q [nl, T, Hq, D] ->
+        (ids [nl, ntiles, requested] int32, k_eff).  Tile i's routing query is
+        the bf16 mean of queries [i * tile, min(T, (i + 1) * tile)) (the
+        reference's query summary, m12_runtime.py:53-67, per tile), selected
+        with the chunk's protected set and budget."""
+        nl, T = q.shape[0], q.shape[1]
+        ntiles = -(-T // tile)
+        if ntiles > 64:
+            raise ValueError(f"per-tile prefill selection supports at most 64 tiles per chunk "
+                             f"(got {ntiles} tiles of {tile} tokens)")
+        summ = tile_summaries(q, tile)
+        ids, _, k_eff = self.select(summ, requested, per_query=True, order=order, ws="/tiles")
+        return ids, k_eff
+
+    def chunk_attend_tiled(self, q, k, v, ids, tile: int, n_hist: int, scale=None):
+        """chunk_attend with one history selection per tile of `tile` queries:
+        ids [nl, ntiles, K] (nkv_prefill_attend_tiled; chunks too short for the
+        matrix-core kernel are one tile and take chunk_attend)."""
+        cfg = self.cfg
+        scale = cfg.scale if scale is None else float(scale)
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        tq, g = q.shape[1], cfg.num_heads // cfg.num_kv_heads
+        ids = ids.contiguous()
+        if tq <= tile and not (tq * g > 16 if cfg.mfma_chunk_min_tokens is None else tq >= cfg.mfma_chunk_min_tokens):
+            return self.chunk_attend(q, k, v, ids, ids.shape[1] * ids.shape[2], n_hist, scale=scale)
+        sink_len = min(cfg.sink_tokens, self.valid_len)
+        _, off, ln = prefill_recent_slice(self.valid_len, cfg.sink_tokens, cfg.recent_tokens)
+        out = torch.empty_like(q)
+        B = cfg.block_size
+        nseg = n_hist + -(-sink_len // B) + (-(-cfg.recent_tokens // B) if ln else 0) + -(-tq // B)
+        splits = self._prefill_splits(tq, nseg)
+        part = None
+        if splits > 1:
+            part = self._buf("pf_partial", self.store.prefill_workspace_floats(self.nl, tq, splits), torch.float32)
+        self.store.prefill_attend_tiled(self.layer0, q, k, v, ids, ids.shape[1] * ids.shape[2], ids.shape[2],
+                                        tile, n_hist, sink_len, self.ring_start, off, ln, scale, out, splits, part)
+        return out, sink_len, ln
 
     def chunk_attend(self, q, k, v, ids, ids_stride, n_hist, allowed=None, allowed_stride=0,
                      scale=None):
@@ -1014,6 +1066,8 @@ class M12LayerRuntime:
             self.last_prefill_query_summaries = q_summary.shape[0]
             requested = cfg.top_k_blocks if cfg.prefill_top_k_blocks is None else cfg.prefill_top_k_blocks
             override = self._select_override()
+            if cfg.prefill_selection == "tile" and override is None and cfg.prefill_adapter is None:
+                return self._prefill_chunk_tiled(q, k, v, requested)
             if override is not None:
                 res = override(q_summary) if cfg.prefill_top_k_blocks is None else \
                     override(q_summary, budget=cfg.prefill_top_k_blocks)
@@ -1034,6 +1088,27 @@ class M12LayerRuntime:
                                               ids_dev, ids_dev.shape[-1], n_hist)[0][0]
         if ids_cpu is None:
             ids_cpu = ids_dev[0, 0, :n_hist].to("cpu", torch.int64)
+        with self._profile_range("prefill_store_kv"):
+            self._store_kv(k, v)
+        self._last_prefill_ids = ids_cpu.clone()
+        self._last_ids_dev = None
+        self._last_ids_cpu = ids_cpu
+        return out
+
+    def _prefill_chunk_tiled(self, q, k, v, requested: int) -> torch.Tensor:
+        """prefill_chunk with prefill_selection="tile": one Top-K per tile of
+        prefill_selection_tile queries (from the tile's query mean); each
+        tile's queries attend [its blocks | sink | previous recent | chunk
+        (causal)].  last_prefill_block_ids is then [ntiles, K]."""
+        cfg = self.cfg
+        tile = cfg.prefill_selection_tile
+        order = _lib.NKV_ORDER_ID_ASC if cfg.gather_sort else _lib.NKV_ORDER_SCORE_DESC
+        ids, n_hist = self._core.select_tiles(q.unsqueeze(0), requested, tile, order)
+        self.last_prefill_query_summaries = ids.shape[1]
+        with self._profile_range("prefill_attention"):
+            out = self._core.chunk_attend_tiled(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), ids, tile,
+                                                n_hist)[0][0]
+        ids_cpu = ids[0, :, :n_hist].to("cpu", torch.int64)
         with self._profile_range("prefill_store_kv"):
             self._store_kv(k, v)
         self._last_prefill_ids = ids_cpu.clone()
@@ -1211,11 +1286,15 @@ class M12ModelRuntime:
         cfg = self.cfg
         if self.core.prefill_len <= 0:
             raise ValueError("prefill_chunk requires prior history")
-        qs = query_summaries(q.contiguous(), cfg.prefill_query_segments)
         req = cfg.top_k_blocks if cfg.prefill_top_k_blocks is None else cfg.prefill_top_k_blocks
         order = _lib.NKV_ORDER_ID_ASC if cfg.gather_sort else _lib.NKV_ORDER_SCORE_DESC
-        ids, _, n = self.core.select(qs, req, order=order)
-        out, _, _ = self.core.chunk_attend(q, k, v, ids, ids.shape[-1], n)
+        if cfg.prefill_selection == "tile":
+            ids, n = self.core.select_tiles(q.contiguous(), req, cfg.prefill_selection_tile, order)
+            out, _, _ = self.core.chunk_attend_tiled(q, k, v, ids, cfg.prefill_selection_tile, n)
+        else:
+            qs = query_summaries(q.contiguous(), cfg.prefill_query_segments)
+            ids, _, n = self.core.select(qs, req, order=order)
+            out, _, _ = self.core.chunk_attend(q, k, v, ids, ids.shape[-1], n)
         self.core.store_kv(k, v)
         self.last_ids_dev = ids
         self.last_n_selected = n

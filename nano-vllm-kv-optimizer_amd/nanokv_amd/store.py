@@ -182,6 +182,20 @@ class SparseKVStore:
             allowed_layer_stride, sink_len, ring_base, rec_lo, rec_len, float(scale), splits,
             _ptr(partial_ws), _ptr(out), _stream()), "prefill_attend")
 
+    def prefill_attend_tiled(self, layer0: int, q, k_new, v_new, ids, ids_layer_stride: int,
+                             ids_tile_stride: int, sel_tile: int, n_hist: int, sink_len: int, ring_base: int,
+                             rec_lo: int, rec_len: int, scale: float, out, splits: int = 1, partial=None) -> None:
+        """nkv_prefill_attend_tiled: one history selection per tile of sel_tile queries."""
+        self._bf16(q, "q")
+        self._bf16(out, "out")
+        if ids.dtype != torch.int32 or not ids.is_contiguous():
+            raise ValueError("prefill_attend_tiled: ids must be contiguous int32")
+        nl, tq = q.shape[0], q.shape[1]
+        _lib.check(self.lib.nkv_prefill_attend_tiled(
+            self._desc_ref, layer0, nl, _ptr(q), q.stride(0), tq, _ptr(k_new), _ptr(v_new), k_new.stride(0),
+            _ptr(ids), ids_layer_stride, ids_tile_stride, sel_tile, n_hist, sink_len, ring_base, rec_lo, rec_len,
+            float(scale), splits, _ptr(partial), _ptr(out), _stream()), "prefill_attend_tiled")
+
     def prefill_workspace_floats(self, nl: int, tq: int, splits: int) -> int:
         return int(self.lib.nkv_prefill_workspace_floats(nl, self.num_kv_heads, self.num_heads,
                                                          tq, splits))
@@ -262,6 +276,26 @@ def query_summaries(q, nsegments: int):
     out = torch.empty(nl, nseg, hq, d, dtype=torch.bfloat16, device=q.device)
     _lib.check(lib.nkv_query_summaries(_ptr(q), q.stride(0), nl, T, hq, d, nsegments, _ptr(out),
                                        out.stride(0), _stream()), "query_summaries")
+    return out
+
+
+def tile_summaries(q, tile: int):
+    """Per-tile query means of a chunk: q [nl, T, Hq, D] -> [nl, ceil(T / tile), Hq, D]
+    bf16; tile i is queries [i * tile, min(T, (i + 1) * tile)) (the last tile
+    may be shorter), each mean rounded as prefill_query_summaries rounds."""
+    lib = _lib.load()
+    SparseKVStore._bf16(q, "q")
+    nl, T, hq, d = q.shape
+    nfull, rem = divmod(T, tile)
+    out = torch.empty(nl, nfull + (1 if rem else 0), hq, d, dtype=torch.bfloat16, device=q.device)
+    if nfull:
+        _lib.check(lib.nkv_query_summaries(_ptr(q), q.stride(0), nl, nfull * tile, hq, d, nfull, _ptr(out),
+                                           out.stride(0), _stream()), "query_summaries")
+    if rem:
+        tail = ctypes.c_void_p(q.data_ptr() + nfull * tile * q.stride(1) * q.element_size())
+        dst = ctypes.c_void_p(out.data_ptr() + nfull * out.stride(1) * out.element_size())
+        _lib.check(lib.nkv_query_summaries(tail, q.stride(0), nl, rem, hq, d, 1, dst, out.stride(0), _stream()),
+                   "query_summaries")
     return out
 
 

@@ -644,6 +644,37 @@ class M12Oracle:
         self.last_block_ids = ids
         return ids, o
 
+    def prefill_chunk_tiled(self, q, k, v, tile: int):
+        """prefill_chunk with one selection per tile of `tile` queries.
+
+        No reference counterpart: the reference selects once per chunk from
+        its query summary (m12_runtime.py:550-556); here that routing is
+        applied to each tile -- tile i's summary is the bf16 mean of queries
+        [i*tile, min(T, (i+1)*tile)) (query_summaries with one segment), its
+        Top-K uses the chunk's protected set and budget, and its queries
+        attend [its blocks | sink | previous recent | chunk (causal)] as
+        prefill_chunk's do.  Returns (ids [ntiles, K], o [T, Hq, D])."""
+        c = self.cfg
+        assert self.prefill_len > 0
+        q = np.asarray(q, F32)
+        kc, vc = np.asarray(k, F32), np.asarray(v, F32)
+        T = q.shape[0]
+        all_ids, outs = [], []
+        for t0 in range(0, T, tile):
+            t1 = min(T, t0 + tile)
+            ids, _ = self.select(query_summaries(q[t0:t1], 1), c.prefill_top_k_blocks)
+            pk, pv, _ = self._pack_prior(ids)
+            off = pk.shape[0]
+            pk = np.concatenate([pk, kc])
+            pv = np.concatenate([pv, vc])
+            mask = causal_mask(T, pk.shape[0], off)[t0:t1]
+            outs.append(attention_fp64(q[t0:t1], pk, pv, c.scale, mask))
+            all_ids.append(ids)
+        self.store_kv(k, v)
+        ids = np.stack(all_ids)
+        self.last_block_ids = ids
+        return ids, np.concatenate(outs)
+
     # -- decode (m12_runtime.py:1141-1346) ---------------------------------
     def decode(self, q, k, v, budget=None):
         c = self.cfg

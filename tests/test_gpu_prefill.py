@@ -203,3 +203,41 @@ def test_prefill_4096_chunk_on_32k_history_full_size():
     for t in rows:
         o_ref = O.attention_fp64(qn[t:t + 1], pkn[:off + t + 1], pvn[:off + t + 1], cfg.scale)
         assert_close_bf16(to_np(out[t:t + 1]), o_ref, **PREFILL_TOL)
+
+
+@pytest.mark.parametrize("T0,T,tile,top_k,model", [
+    (4096, 300, 64, 8, False),     # 5 tiles, the last one short
+    (8192, 512, 64, 32, False),    # 8 full tiles
+    (8192, 512, 128, 32, True),    # all layers at once, 4 tiles of 128
+])
+def test_prefill_per_tile_selection_matches_oracle(T0, T, tile, top_k, model):
+    """prefill_selection="tile": one Top-K per tile of queries from the tile's
+    query mean; each tile attends its own blocks (oracle prefill_chunk_tiled)."""
+    from nanokv_amd import workload
+    from nanokv_amd.sparse import M12Config, M12LayerRuntime, M12ModelRuntime
+    cfg = M12Config(max_model_len=T0 + T + 64, top_k_blocks=top_k, prefill_selection="tile",
+                    prefill_selection_tile=tile)
+    L = 3 if model else 1
+    hist = [workload.history(T0, 700 + i) for i in range(L)]
+    q, k, v = workload.prefill_chunk_inputs(T, 71, layers=L)
+    if model:
+        rt = M12ModelRuntime(L, cfg)
+        rt.prefill(torch.stack([h[0] for h in hist]).cuda(), torch.stack([h[1] for h in hist]).cuda())
+        reps = [rt.store.reps[i] for i in range(L)]
+        out = rt.prefill_chunk(q.cuda(), k.cuda(), v.cuda())
+        ids_all = rt.last_ids_dev[:, :, :rt.last_n_selected].cpu()
+    else:
+        rt = M12LayerRuntime(0, cfg)
+        rt.prefill_first(None, hist[0][0].cuda(), hist[0][1].cuda())
+        reps = [rt.reps_gpu]
+        out = rt.prefill_chunk(q[0].cuda(), k[0].cuda(), v[0].cuda(), torch.device("cuda")).unsqueeze(0)
+        ids_all = rt.last_prefill_block_ids.unsqueeze(0)
+    assert ids_all.shape[1] == -(-T // tile)
+    for i in range(L):
+        ob = O.M12Oracle(O.OracleConfig(top_k_blocks=top_k))
+        ob.store_kv(to_np(hist[i][0]), to_np(hist[i][1]), with_reps=False)
+        nb = ob.nblocks_filled
+        ob.reps[:, :nb] = to_np(reps[i][:, :nb])
+        ids_or, o_ref = ob.prefill_chunk_tiled(to_np(q[i]), to_np(k[i]), to_np(v[i]), tile)
+        assert ids_all[i].tolist() == ids_or.tolist(), f"layer {i}: tile ids differ"
+        assert_close_bf16(to_np(out[i]), o_ref, **PREFILL_TOL)

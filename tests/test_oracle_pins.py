@@ -553,3 +553,63 @@ def test_query_summary_rounding_against_torch_mean():
     assert diff.mean() <= 1e-3
     ulp = np.abs(O.bf16_round(ours * (1 + 2.0 ** -7)) - ours)
     assert (np.abs(ref - ours)[diff] <= ulp[diff] * 1.0001).all()
+
+
+# ---- per-query-tile prefill selection (no reference counterpart) -----------------
+
+def _tile_oracle(T0, seed, **kw):
+    cfg = O.OracleConfig(block_size=4, r=1, recent_tokens=8, sink_tokens=4, num_heads=4, num_kv_heads=2,
+                         head_dim=8, scale=0.35, **kw)
+    ob = O.M12Oracle(cfg)
+    rng = np.random.default_rng(seed)
+    k = _rand_bf16(rng, (T0, 2, 8), 0.5)
+    v = _rand_bf16(rng, (T0, 2, 8), 0.5)
+    ob.store_kv(k, v)
+    return ob, k, v, rng
+
+
+def test_tiled_prefill_with_one_tile_is_the_chunk_routing():
+    """A chunk no longer than the tile is one tile: same ids, same output as
+    prefill_chunk (one query summary, m12_runtime.py:550-556)."""
+    for seed in range(5):
+        a, _, _, rng = _tile_oracle(64, seed, top_k_blocks=3)
+        b, _, _, _ = _tile_oracle(64, seed, top_k_blocks=3)
+        q = _rand_bf16(rng, (12, 4, 8))
+        kn, vn = _rand_bf16(rng, (12, 2, 8), 0.5), _rand_bf16(rng, (12, 2, 8), 0.5)
+        ids_t, o_t = a.prefill_chunk_tiled(q, kn, vn, tile=16)
+        ids_c, o_c = b.prefill_chunk(q, kn, vn)
+        assert ids_t.shape[0] == 1 and ids_t[0].tolist() == ids_c.tolist()
+        assert np.array_equal(o_t, o_c)
+        assert a.valid_len == b.valid_len and np.array_equal(a.recent_k, b.recent_k)
+
+
+def test_tiled_prefill_selecting_everything_is_full_causal_attention():
+    """With a budget above every selectable block each tile attends the whole
+    history exactly once, so every query's output equals plain causal
+    attention over [history | chunk] (the coverage identity of
+    test_m14_prefill_layout.py:12-44)."""
+    ob, k0, v0, rng = _tile_oracle(64, 3, top_k_blocks=64)
+    q = _rand_bf16(rng, (40, 4, 8))
+    kn, vn = _rand_bf16(rng, (40, 2, 8), 0.5), _rand_bf16(rng, (40, 2, 8), 0.5)
+    ids, o = ob.prefill_chunk_tiled(q, kn, vn, tile=8)
+    assert ids.shape == (5, 13)        # 16 blocks, protected {0} and the recent blocks {14, 15}
+    kk, vv = np.concatenate([k0, kn]), np.concatenate([v0, vn])
+    ref = O.attention_fp64(q, kk, vv, 0.35, O.causal_mask(40, 104, 64))
+    assert np.allclose(o, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_tiled_prefill_routes_each_tile_to_its_own_blocks():
+    """Two tiles whose queries point at different planted blocks select
+    different blocks (budget 1): tile 0 -> block 5, tile 1 -> block 9; a
+    shared selection would pick one block for both."""
+    ob, _, _, rng = _tile_oracle(64, 4, top_k_blocks=1)
+    da = np.zeros((4, 8), np.float32); da[:, 0] = 1.0
+    db = np.zeros((4, 8), np.float32); db[:, 1] = 1.0
+    reps = np.zeros_like(ob.reps)
+    reps[:, 5, 0, 0] = 1.0
+    reps[:, 9, 0, 1] = 1.0
+    ob.reps = reps
+    q = np.concatenate([np.repeat(da[None], 8, 0), np.repeat(db[None], 8, 0)]).astype(np.float32)
+    kn, vn = _rand_bf16(rng, (16, 2, 8), 0.5), _rand_bf16(rng, (16, 2, 8), 0.5)
+    ids, _ = ob.prefill_chunk_tiled(q, kn, vn, tile=8)
+    assert ids.tolist() == [[5], [9]]

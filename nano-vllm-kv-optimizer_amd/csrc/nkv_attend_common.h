@@ -83,6 +83,24 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// Max / sum of x over the four 16-lane rows of the wavefront (lanes l, l ^ 16,
+// l ^ 32, l ^ 48), the result in every lane.  gfx950's row swaps
+// (v_permlane16_swap / v_permlane32_swap: with both operands x, the pair holds
+// x of lane l & ~16 and of lane l | 16, resp. & ~32 and | 32) stay in the VALU,
+// where a shuffle through ds_bpermute waits on the LDS pipeline.
+__device__ __forceinline__ float max_over_rows(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_over_rows(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // 8 signed bytes -> 8 bf16 (exact: |x| <= 127 has <= 7 significant bits).
 __device__ __forceinline__ uint4 i8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
   uint32_t o[4];

@@ -8,34 +8,33 @@
 // (query t sees chunk token c iff c <= t).  The chunk segments a workgroup
 // visits stop at its last query token.
 //
-// Work split: one workgroup (4 wavefronts) per (layer, KV head, query tile).
-// A query tile is 128 columns = 128/G tokens x the G query heads of the KV
-// head, so every K/V tile staged in LDS serves all G heads.  Wavefront w owns
-// columns 32w..32w+31 (two 16-column MFMA tiles).  Workgroups are ordered so
-// that the linear id cycles over the KV heads (one head per XCD when
-// Hkv = 8, keeping that head's keys in one L2) and the longest causal tiles
-// start first.
+// Work split: one workgroup (4 wavefronts, two per CU) per (layer, KV head,
+// query tile).  A query tile is 64 NCT columns = 64 NCT / G tokens x the G
+// query heads of the KV head, so every K/V tile staged in LDS serves all G
+// heads; wavefront w owns NCT 16-column MFMA tiles.  NCT = 3 (192 columns)
+// for long chunks: each staged tile then feeds 1.5x the products of NCT = 2
+// (128 columns, kept for short chunks, verify's per-query history flags and
+// selection tiles 192 columns do not divide).  Workgroups are ordered so that
+// the linear id cycles over the KV heads (one head per XCD when Hkv = 8,
+// keeping that head's keys in one L2) and the longest causal tiles start
+// first.
 //
 // Per 64-key segment (double-buffered LDS, one barrier per segment):
-//   * staging: rows go global -> LDS directly (buffer_load ... lds, no
-//     registers; bounds-checked descriptors read rows past the segment as
-//     zero, so no index is clamped).  int8 history rows land raw with their
-//     scales and are dequantised to bf16 in LDS after the copy.  The next
-//     segment is in flight while the current one is computed;
-//   * S^T = K . Q^T: v_mfma_f32_16x16x32_bf16, A = 16 keys x 32 dims read from
-//     the K tile, B = 32 dims x 16 columns held in registers all along;
-//   * online softmax in fp32 per column (exp2, scale folded in); each lane's
-//     column is fixed, so the running max and the rescale stay in the lane;
-//   * O^T += V^T . P^T: A = 16 dims x 32 keys assembled from the key-major V
-//     tile with two transposing LDS reads (ds_read_b64_tr_b16), B = the
-//     lane's own probabilities rounded to bf16 (the 32-key contraction index
-//     is ordered as the S^T accumulator holds the keys, so P never leaves the
-//     registers).
+//   * staging: rows go global -> LDS directly (buffer_load ... lds issued as
+//     inline assembly, no registers; bounds-checked descriptors read rows
+//     past the segment as zero, so no index is clamped).  int8 history rows
+//     land raw with their scales and are dequantised to bf16 in LDS after the
+//     copy.  The next segment is in flight while the current one is computed;
+//   * attend_segment: S^T = K . Q^T and O^T += V^T . P^T on the matrix cores
+//     with an online softmax in between (its comment has the operand layout),
+//     in one pass over the 64 keys (NCT = 2) or two of 32 (NCT = 3, half the
+//     logits live).
 //
 // The reference runs this as flash-attention over the packed
 // [selected | sink | recent | chunk] keys with bottom-right causal masking
 // (nanovllm/sparse/m12_runtime.py:592-651, :809-839); the fp32 masked path
 // (:875-896) is the same function.
+#include <algorithm>
 #include <type_traits>
 
 #include "nkv_stage.h"
@@ -52,6 +51,15 @@ constexpr int kPfCols = 128;                     // (token, head) columns per wo
 // pad words, acc[128] (16-byte aligned for vector stores)
 constexpr int kPfPart = 4 + kHeadDim;
 
+// Workgroup barrier that drains this wavefront's LDS operations only: the
+// asynchronous global -> LDS copies stay in flight (__syncthreads' fence would
+// wait for every outstanding vector-memory operation, copies included).  The
+// memory clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt, expcnt untouched
+  asm volatile("s_barrier" ::: "memory");
+}
+
 // 8 int8 codes (lo, hi) -> 8 x bf16(code * scale[e]), rounded to nearest even.
 __device__ __forceinline__ u32x4 dequant8(uint32_t lo, uint32_t hi, const float (&sc)[8]) {
   float f[8];
@@ -61,6 +69,78 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t lo, uint32_t hi, const float 
     f[e] = static_cast<float>(static_cast<int8_t>((w >> ((e & 3) * 8)) & 0xffu)) * sc[e];
   }
   return u32x4{pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]), pack_bf16(f[6], f[7])};
+}
+
+// Raw buffer descriptor words of bytes [base, base + bytes): reads at or past
+// `bytes` return zero.
+// The words are read from the first active lane: they are uniform by
+// construction, and the copy's descriptor operand must sit in SGPRs.
+typedef uint32_t rsrc_words __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ rsrc_words rsrc_of(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  auto uni = [](uint32_t x) { return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x))); };
+  return rsrc_words{uni(static_cast<uint32_t>(a)), uni(static_cast<uint32_t>(a >> 32) & 0xffffu), uni(bytes),
+                    static_cast<uint32_t>(kRsrcWord3)};
+}
+
+// One global -> LDS copy, 16 bytes a lane (buffer_load_dwordx4 ... lds): lane
+// u's bytes at `voffset` of the buffer land at LDS address lds + 16 u.  Issued
+// as inline assembly, so that the compiler (which counts such copies against
+// all of LDS) adds no waits of its own: the kernels order them with explicit
+// vmcnt waits.  The memory clobber keeps every LDS access on its side of the
+// copy.  M0 (the LDS base, read when the copy issues) is restored after it;
+// the s_nops cover the descriptor-write and M0-write hazards.
+__device__ __forceinline__ void lds_copy16(rsrc_words rsrc, const char* lds, int voffset) {
+  const uint32_t m0 = static_cast<uint32_t>(
+      __builtin_amdgcn_readfirstlane(static_cast<int>(reinterpret_cast<uintptr_t>((lds_void*)lds))));
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_nop 4\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(m0), "v"(voffset), "s"(rsrc)
+      : "memory");
+}
+// The same, 4 bytes a lane (buffer_load_dword ... lds): lane u lands at lds + 4 u.
+__device__ __forceinline__ void lds_copy4(rsrc_words rsrc, const char* lds, int voffset) {
+  const uint32_t m0 = static_cast<uint32_t>(
+      __builtin_amdgcn_readfirstlane(static_cast<int>(reinterpret_cast<uintptr_t>((lds_void*)lds))));
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_nop 4\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dword %2, %3, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(m0), "v"(voffset), "s"(rsrc)
+      : "memory");
+}
+
+// bf16 segment -> stage buffer with WAVES wavefronts: wavefront w copies K and
+// V rows (64 / WAVES) w .. + 64 / WAVES, four rows (1 KiB) per instruction;
+// lane u lands at 16 u of its 1 KiB, so it fetches the global chunk that the
+// swizzle puts there.  Whole offsets go in the bounds-checked lane offset.
+template <int WAVES>
+__device__ __forceinline__ void dma_rows(const Seg& g, char* buf, int wave, int lane, bool live) {
+  constexpr int RPW = kBlock / WAVES;
+  const uint32_t bytes = live ? static_cast<uint32_t>(g.len * g.rowb) : 0u;
+  const rsrc_words rk = rsrc_of(g.kbase, bytes);
+  const rsrc_words rv = rsrc_of(g.vbase, bytes);
+  const int ln = lane & 15;
+  const int lg = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < RPW / 4; ++i) {
+    const int row = RPW * wave + 4 * i + lg;
+    const char* dst = buf + (RPW * wave + 4 * i) * 256;
+    lds_copy16(rk, dst, row * g.rowb + ((ln ^ (row & 15)) << 4));
+    lds_copy16(rv, dst + kTileBytes, row * g.rowb + ((ln ^ (2 * lg)) << 4));
+  }
 }
 
 // int8 history block: the raw codes (and the scales) are copied into the
@@ -75,56 +155,56 @@ constexpr int kI8VScales = 512;
 constexpr int kI8RawK = kTileBytes;
 constexpr int kI8RawV = kTileBytes + kBlock * kHeadDim;
 
-template <int FMT>
+template <int FMT, int WAVES = 4>
 __device__ __forceinline__ void dma_i8_segment(const AttendParams& p, const Seg& g, int lh, char* buf, int wave,
-                                               int lane) {
-  const __amdgpu_buffer_rsrc_t rk = seg_rsrc(g.kbase, g);
-  const __amdgpu_buffer_rsrc_t rv = seg_rsrc(g.vbase, g);
+                                               int lane, bool live = true) {
+  const uint32_t bytes = live ? static_cast<uint32_t>(g.len * g.rowb) : 0u;
+  const rsrc_words rk = rsrc_of(g.kbase, bytes);
+  const rsrc_words rv = rsrc_of(g.vbase, bytes);
+  constexpr int kPer = 8 / WAVES;   // 1 KiB copies per tensor and wavefront
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int o = (2 * wave + i) * 1024;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(buf + kI8RawK + o), 16, lane * 16, o, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(buf + kI8RawV + o), 16, lane * 16, o, 0, 0);
+  for (int i = 0; i < kPer; ++i) {
+    const int o = (kPer * wave + i) * 1024;
+    lds_copy16(rk, buf + kI8RawK + o, o + lane * 16);
+    lds_copy16(rv, buf + kI8RawV + o, o + lane * 16);
   }
   if (wave == 0) {
     if (FMT == NKV_KV_INT8_TOKEN) {
       // 64 fp16 scales = 128 B per tensor; lanes 32.. read past it (zeros)
       const int64_t tb = (static_cast<int64_t>(lh) * p.cap + g.blk) * kBlock;
-      const __amdgpu_buffer_rsrc_t sk = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint16_t*>(p.k_tscale + tb), 0, kBlock * 2, kRsrcWord3);
-      const __amdgpu_buffer_rsrc_t sv = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint16_t*>(p.v_tscale + tb), 0, kBlock * 2, kRsrcWord3);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(sk, (lds_void*)(buf + kI8Scales), 4, lane * 4, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(sv, (lds_void*)(buf + kI8VScales), 4, lane * 4, 0, 0, 0);
+      lds_copy4(rsrc_of(p.k_tscale + tb, kBlock * 2), buf + kI8Scales, lane * 4);
+      lds_copy4(rsrc_of(p.v_tscale + tb, kBlock * 2), buf + kI8VScales, lane * 4);
     } else {
       // 128 fp32 per-(head, dim) K scales
-      const __amdgpu_buffer_rsrc_t sk = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<float*>(p.k_scale + static_cast<int64_t>(lh) * kHeadDim), 0, kHeadDim * 4, kRsrcWord3);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(sk, (lds_void*)(buf + kI8Scales), 4, lane * 4, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(sk, (lds_void*)(buf + kI8Scales + 256), 4, lane * 4, 256, 0, 0);
+      const rsrc_words sk = rsrc_of(p.k_scale + static_cast<int64_t>(lh) * kHeadDim, kHeadDim * 4);
+      lds_copy4(sk, buf + kI8Scales, lane * 4);
+      lds_copy4(sk, buf + kI8Scales + 256, 256 + lane * 4);
     }
   }
 }
 
 // In-place dequantisation of a staged int8 block (the copies have landed and
-// are visible): thread tid converts rows (tid >> 4) + 16 j, dims 8 c .. 8 c + 7
-// (c = tid & 15) of K and V to bf16(code * scale) in the K / V tiles.
-template <int FMT>
+// are visible): with NT threads, thread tid converts rows (tid >> 4) + (NT / 16) j,
+// dims 8 c .. 8 c + 7 (c = tid & 15) of K and V to bf16(code * scale) in the
+// K / V tiles.
+template <int FMT, int NT = kPfThreads>
 __device__ __forceinline__ void dequant_i8(const AttendParams& p, const Seg& g, int lh, char* buf, int tid) {
+  constexpr int RS = NT / 16;        // row step
+  constexpr int NJ = kBlock / RS;    // rows per thread
   const int r0 = tid >> 4;
   const int c = tid & 15;
-  u32x2 kq[4], vq[4];
-  float ksc[4][8], vsc[4];
+  u32x2 kq[NJ], vq[NJ];
+  float ksc[NJ][8], vsc[NJ];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = r0 + 16 * j;
+  for (int j = 0; j < NJ; ++j) {
+    const int r = r0 + RS * j;
     kq[j] = *reinterpret_cast<const u32x2*>(buf + kI8RawK + r * kHeadDim + c * 8);
     vq[j] = *reinterpret_cast<const u32x2*>(buf + kI8RawV + r * kHeadDim + c * 8);
   }
   if (FMT == NKV_KV_INT8_TOKEN) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int r = r0 + 16 * j;
+    for (int j = 0; j < NJ; ++j) {
+      const int r = r0 + RS * j;
       const float ks = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(buf + kI8Scales + 2 * r));
 #pragma unroll
       for (int e = 0; e < 8; ++e) ksc[j][e] = ks;
@@ -135,7 +215,7 @@ __device__ __forceinline__ void dequant_i8(const AttendParams& p, const Seg& g, 
     const u32x4 s1 = *reinterpret_cast<const u32x4*>(buf + kI8Scales + c * 32 + 16);
     const float vs = p.v_scale[static_cast<int64_t>(lh) * p.cap + g.blk];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         ksc[j][e] = __uint_as_float(s0[e]);
@@ -144,14 +224,14 @@ __device__ __forceinline__ void dequant_i8(const AttendParams& p, const Seg& g, 
       vsc[j] = vs;
     }
   }
-  __syncthreads();   // every raw code and scale has been read
+  lds_barrier();   // every raw code and scale has been read
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = r0 + 16 * j;
+  for (int j = 0; j < NJ; ++j) {
+    const int r = r0 + RS * j;
     float vv[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) vv[e] = vsc[j];
-    *reinterpret_cast<u32x4*>(buf + r * 256 + ((c ^ r0) << 4)) = dequant8(kq[j][0], kq[j][1], ksc[j]);
+    *reinterpret_cast<u32x4*>(buf + r * 256 + ((c ^ (r0 & 15)) << 4)) = dequant8(kq[j][0], kq[j][1], ksc[j]);
     *reinterpret_cast<u32x4*>(buf + kTileBytes + r * 256 + ((c ^ (2 * (r0 & 3))) << 4)) =
         dequant8(vq[j][0], vq[j][1], vv);
   }
@@ -174,53 +254,235 @@ __device__ __forceinline__ bool needs_mask(const AttendParams& p, const Seg& g, 
 // holds key 16 kt + 4 lg + e of column ct.  Key k of the segment is visible
 // to column ct iff k <= thr[ct] (history / sink / chunk), or, for a ring
 // piece, iff k < vlen and the slot's logical position lies in the window.
-template <bool PACKED>
-__device__ __forceinline__ void apply_mask(const AttendParams& p, const Seg& g, int lg, const int (&tcol)[2],
-                                           const int (&allow)[2], f32x4 (&S)[4][2]) {
+template <bool PACKED, int NCT, int KT>
+__device__ __forceinline__ void apply_mask(const AttendParams& p, const Seg& g, int lg, const int (&tcol)[NCT],
+                                           const int (&allow)[NCT], f32x4 (&S)[KT][NCT], int kt0) {
   if (g.type == kSegRecent) {
     // x = (slot - ring_base - rec_lo) mod R for slot off + key
     int a = (g.off - p.ring_base - p.rec_lo) % p.R;
     a = a < 0 ? a + p.R : a;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+    for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int key = 16 * kt + 4 * lg + e;
+        const int key = 16 * (kt0 + kt) + 4 * lg + e;
         int x = a + key;
         x -= p.R & ((p.R - 1 - x) >> 31);
         const float bound = vis_bound(max(key - (g.vlen - 1), x - (p.rec_len - 1)));
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) S[kt][ct][e] = fminf(S[kt][ct][e], bound);
+        for (int ct = 0; ct < NCT; ++ct) S[kt][ct][e] = fminf(S[kt][ct][e], bound);
       }
     return;
   }
-  int base[2];   // 4 lg - thr[ct]
+  int base[NCT];   // 4 lg - thr[ct]
 #pragma unroll
-  for (int ct = 0; ct < 2; ++ct) {
+  for (int ct = 0; ct < NCT; ++ct) {
     int thr = g.vlen - 1;
     if (g.type == kSegChunk) thr = min(thr, tcol[ct] + (PACKED ? p.causal_off : 0) - g.off);
     else if (allow[ct] == 0) thr = -1;
     base[ct] = 4 * lg - thr;
   }
 #pragma unroll
-  for (int ct = 0; ct < 2; ++ct)
+  for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+    for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) S[kt][ct][e] = fminf(S[kt][ct][e], vis_bound(base[ct] + 16 * kt + e));
+      for (int e = 0; e < 4; ++e) S[kt][ct][e] = fminf(S[kt][ct][e], vis_bound(base[ct] + 16 * (kt0 + kt) + e));
   if (PACKED && g.type == kSegChunk && p.tok_mask != nullptr) {
     // caller-packed keys with a per-(query, key) mask: keys past vlen are
     // already hidden and never read; padding columns read row tq - 1
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
+    for (int ct = 0; ct < NCT; ++ct) {
       const uint8_t* mrow = p.tok_mask + static_cast<int64_t>(min(tcol[ct], p.tq - 1)) * p.n_chunk + g.off;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int key = 16 * kt + 4 * lg + e;
+          const int key = 16 * (kt0 + kt) + 4 * lg + e;
           if (key < g.vlen && mrow[key] != 0) S[kt][ct][e] = -INFINITY;
         }
+    }
+  }
+}
+
+// Loop-invariant LDS offsets (bytes) of a lane's MFMA operands in a stage
+// buffer.  K read (QK A operand): key 16 kt + ln, 16-byte chunk 4 ks + lg,
+// at koff[ks] + 4096 kt.  V transposing read (PV A operand): lane ln
+// addresses key 4 lg + (ln >> 2) (+ 32 k2 + 16 half), dims 16 dt + 4 (ln & 3)
+// .. +4; the swizzled chunk is 2 (dt ^ (ln >> 2)) + ((ln & 3) >> 1), so
+// dt & 4 -> + 128 and dt & 3 picks vtr[].
+struct OperandOffsets {
+  int koff[4];
+  int vtr[4];
+  __device__ __forceinline__ OperandOffsets(int ln, int lg) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) koff[ks] = ln * 256 + ((((4 * ks + lg) ^ ln) & 15) << 4);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      vtr[q] = kTileBytes + (4 * lg + (ln >> 2)) * 256 + ((2 * (q ^ (ln >> 2)) + ((ln & 3) >> 1)) << 4) + 8 * (ln & 1);
+  }
+};
+
+// Online-softmax state of one column: the reference max in log2 units is
+// -nm (nm = 0 and thr = -inf before any key was visible); a logit above thr
+// (raw units) would move it by more than 2^8; l is the running denominator.
+struct Col {
+  float nm;
+  float thr;
+  float l;
+};
+__device__ __forceinline__ void col_init(Col& c) {
+  c.nm = 0.0f;
+  c.thr = -INFINITY;
+  c.l = 0.0f;
+}
+__device__ __forceinline__ float col_max(const Col& c) { return c.thr == -INFINITY ? -INFINITY : -c.nm; }
+
+// One staged segment (64 keys in `buf`) against the wavefront's NCT 16-column
+// tiles, in passes of 16 KT keys (KT = 4: one pass; KT = 2: two passes with
+// half the logits live):
+//   * S^T = K . Q^T: v_mfma_f32_16x16x32_bf16, A = 16 keys x 32 dims read
+//     from the K tile, B = 32 dims x 16 columns held in registers (bq);
+//   * the visibility mask when `mask`;
+//   * online softmax in fp32 per column (exp2, scale folded in; the running
+//     max and the rescale stay in the lane, whose column is fixed);
+//   * O^T += V^T . P^T: A = 16 dims x 32 keys from two transposing LDS reads
+//     (ds_read_b64_tr_b16), B = the lane's own probabilities rounded to bf16
+//     (the 32-key contraction index is ordered as the S^T accumulator holds
+//     the keys, so P never leaves the registers); l accumulates the same
+//     bf16-rounded probabilities (one dot2 per pair), so numerator and
+//     denominator see the same P.
+template <bool PACKED, int NCT, int KT>
+__device__ __forceinline__ void attend_segment(const AttendParams& p, const Seg& cur, const char* buf, bool mask,
+                                               int lg, const OperandOffsets& off, const bf16x8 (&bq)[NCT][4],
+                                               const int (&tcol)[NCT], const int (&allow)[NCT],
+                                               f32x4 (&acc)[8][NCT], Col (&col)[NCT]) {
+  // Operand reads run two products ahead through a ring of three registers;
+  // the scheduling barriers keep that order (left to itself the scheduler may
+  // sink each read onto its product and wait out the full LDS latency).
+  constexpr int kQ = 4 * KT;   // K operands per pass: ks outer, kt inner
+  auto read_k = [&](int pass, int i) {
+    return *reinterpret_cast<const bf16x8*>(buf + (pass * KT + i % KT) * 4096 + off.koff[i / KT]);
+  };
+  auto read_v = [&](int k2, int dt) {
+    const char* vp = buf + off.vtr[dt & 3] + (dt >> 2) * 128 + k2 * 8192;
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vp));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vp + 4096));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+#pragma unroll
+  for (int pass = 0; pass < 4 / KT; ++pass) {
+    // ---- S^T = K . Q^T ---------------------------------------------------
+    f32x4 S[KT][NCT];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) S[kt][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    bf16x8 ka[3];
+    ka[0] = read_k(pass, 0);
+    ka[1] = read_k(pass, 1);
+#pragma unroll
+    for (int i = 0; i < kQ; ++i) {
+      if (i + 2 < kQ) ka[(i + 2) % 3] = read_k(pass, i + 2);
+      const int ks = i / KT;
+      const int kt = i % KT;
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        S[kt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[i % 3], bq[ct][ks], S[kt][ct], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // the first V operands load while the softmax runs
+    const int k2_0 = pass * (KT / 2);
+    bf16x8 va[3];
+    va[0] = read_v(k2_0, 0);
+    va[1] = read_v(k2_0, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (mask) {
+      // (an empty volatile asm: the compiler would otherwise compute the
+      // branch-free mask on every segment, though few need one)
+      asm volatile("");
+      apply_mask<PACKED, NCT, KT>(p, cur, lg, tcol, allow, S, pass * KT);
+    }
+
+    // ---- online softmax (fp32) --------------------------------------------
+    // The reference max only moves when a logit exceeds it by more than 2^8
+    // (p <= 256 is harmless in fp32 and bf16): each lane compares its own
+    // logits with the column's threshold, and only when some column of the
+    // wavefront crosses it (always on a column's first visible keys) are the
+    // column maxima reduced across lanes and the accumulators rescaled.
+    float mx[NCT];
+    bool move = false;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      mx[ct] = S[0][ct][0];
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mx[ct] = fmaxf(mx[ct], S[kt][ct][e]);
+      move = move || mx[ct] > col[ct].thr;
+    }
+    if (__any(move)) {
+      asm volatile("");
+      float alpha[NCT];
+      bool rescale = false;
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        const float m_old = col_max(col[ct]);
+        const float cand = max_over_rows(mx[ct]) * p.scale_log2;
+        const float m_new = cand > m_old + 8.0f ? cand : m_old;
+        const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+        alpha[ct] = __builtin_amdgcn_exp2f(m_old - m_use);
+        rescale = rescale || alpha[ct] != 1.0f;
+        col[ct].nm = -m_use;
+        col[ct].thr = m_new == -INFINITY ? -INFINITY : (m_new + 8.0f) / p.scale_log2;
+        col[ct].l *= alpha[ct];
+      }
+      if (__any(rescale)) {
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) acc[dt][ct] *= alpha[ct];
+      }
+    }
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          S[kt][ct][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kt][ct][e], p.scale_log2, col[ct].nm));
+
+    // ---- O^T += V^T . P^T -------------------------------------------------
+    constexpr int kV = 8 * (KT / 2);   // V operands per pass: 32-key group outer, dt inner
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+      const int j = i / 8;
+      const int dt = i % 8;
+      if (dt == 0) __builtin_amdgcn_sched_barrier(0);
+      bf16x8 bp[NCT];
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        const f32x4 a0 = S[2 * j][ct];
+        const f32x4 a1 = S[2 * j + 1][ct];
+        const u32x4 w = u32x4{pack_bf16(a0[0], a0[1]), pack_bf16(a0[2], a0[3]), pack_bf16(a1[0], a1[1]),
+                              pack_bf16(a1[2], a1[3])};
+        bp[ct] = __builtin_bit_cast(bf16x8, w);
+        if (dt == 0) {
+          const bf16x2 one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+          // (each word is copied out first: clang's __builtin_bit_cast of a
+          // vector element reads element 0)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t we = w[e];
+            col[ct].l = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, we), one, col[ct].l, false);
+          }
+        }
+      }
+      if (i + 2 < kV) va[(i + 2) % 3] = read_v(k2_0 + (i + 2) / 8, (i + 2) % 8);
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        acc[dt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[i % 3], bp[ct], acc[dt][ct], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
@@ -228,8 +490,12 @@ __device__ __forceinline__ void apply_mask(const AttendParams& p, const Seg& g, 
 // PACKED: caller-packed keys (nkv_attend_packed): the chunk's causal start is
 // causal_off and an optional per-token mask applies; its own instantiation,
 // so the history paths carry none of that code.
-template <int FMT, bool PACKED>
+template <int FMT, bool PACKED, int NCT>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendParams p, int nqt) {
+  constexpr int kCols = kPfWaves * 16 * NCT;   // (token, head) columns per workgroup
+  // per-query history flags (verify's union selections) take the 128-column
+  // tiling only: the wider one keeps those registers for its logits
+  constexpr bool kAllowed = NCT == 2;
   // two stage buffers as separate objects, so that the compiler can tell the
   // buffer being read from the one the asynchronous copies write
   __shared__ __attribute__((aligned(16))) char lds0[kBufBytes];
@@ -244,38 +510,24 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
   const int qt = nqt - 1 - static_cast<int>(blockIdx.x) / p.hkv;
   const int layer = blockIdx.y;
   const int lh = layer * p.hkv + h;
-  const int tpw = kPfCols / p.G;
+  const int tpw = kCols / p.G;
   const int t0 = qt * tpw;
   const int t_last = min(t0 + tpw, p.tq) - 1;
   const int hq = p.hkv * p.G;
 
-  // ---- loop-invariant LDS offsets (bytes) -----------------------------------
-  int koff[4];   // K read (QK A operand): key 16 kt + ln, chunk 4 ks + lg; kt -> + 4096 kt
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) koff[ks] = ln * 256 + ((((4 * ks + lg) ^ ln) & 15) << 4);
-  // V transposing read (PV A operand): lane ln addresses key 4 lg + (ln >> 2)
-  // (+ 32 k2 + 16 half), dims 16 dt + 4 (ln & 3) .. +4; the swizzled chunk is
-  // 2 (dt ^ (ln >> 2)) + ((ln & 3) >> 1), so dt & 4 -> + 128 and dt & 3 picks vtr[]
-  int vtr[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-    vtr[q] = kTileBytes + (4 * lg + (ln >> 2)) * 256 + ((2 * (q ^ (ln >> 2)) + ((ln & 3) >> 1)) << 4) + 8 * (ln & 1);
-  int kx[4];     // copy offsets: K row 16w + 4i + (lane >> 4), global chunk (lane & 15) ^ (row & 15)
-#pragma unroll
-  for (int i = 0; i < 4; ++i) kx[i] = ((ln ^ ((4 * i + lg) & 15))) << 4;
-  const int vx = (ln ^ (2 * lg)) << 4;   // V row & 3 == lane >> 4
+  const OperandOffsets off(ln, lg);
 
-  // ---- query operands: column c = 32 wave + 16 ct + ln --------------------
-  bf16x8 bq[2][4];
-  int tcol[2];
-  int hcol[2];
+  // ---- query operands: column c = 16 NCT wave + 16 ct + ln ----------------
+  bf16x8 bq[NCT][4];
+  int tcol[NCT];
+  // the column's query head (recomputed for the store: no register held)
+  auto head_of = [&](int ct) { return h * p.G + (wave * 16 * NCT + ct * 16 + ln) % p.G; };
 #pragma unroll
-  for (int ct = 0; ct < 2; ++ct) {
-    const int c = wave * 32 + ct * 16 + ln;
+  for (int ct = 0; ct < NCT; ++ct) {
+    const int c = wave * 16 * NCT + ct * 16 + ln;
     const int t = t0 + c / p.G;
     tcol[ct] = t;
-    hcol[ct] = h * p.G + c % p.G;
-    const uint16_t* qrow = p.q + p.q_ls * layer + (static_cast<int64_t>(t) * hq + hcol[ct]) * kHeadDim + lg * 8;
+    const uint16_t* qrow = p.q + p.q_ls * layer + (static_cast<int64_t>(t) * hq + head_of(ct)) * kHeadDim + lg * 8;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       u32x4 v = u32x4{0u, 0u, 0u, 0u};
@@ -284,13 +536,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
     }
   }
 
-  f32x4 acc[8][2];
+  f32x4 acc[8][NCT];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) acc[dt][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  float m_run[2] = {-INFINITY, -INFINITY};
-  float l_run[2] = {0.0f, 0.0f};
+    for (int ct = 0; ct < NCT; ++ct) acc[dt][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  Col cs[NCT];   // per-column softmax state
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) col_init(cs[ct]);
 
   // chunk segments up to the last key visible to the tile's last token
   const int n_chunk_seg =
@@ -305,17 +558,22 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
 
   // staging of segment s into buffer `buf`: asynchronous copies issued by
   // begin_stage, completed (and int8 blocks dequantised) by finish_stage
-  int allow_nxt[2] = {1, 1};
+  int allow_nxt[NCT];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) allow_nxt[ct] = 1;
   auto begin_stage = [&](const Seg& g, char* buf) {
+    // the column flags are loaded before the copies: vector memory counts
+    // complete in order, so waiting for the flags then leaves the copies in
+    // flight (issued after them, the flags' wait would drain the copies too)
+    if (kAllowed && g.type == kSegHist && p.allowed != nullptr) {
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        allow_nxt[ct] = p.allowed[p.allowed_ls * layer + static_cast<int64_t>(min(tcol[ct], p.tq - 1)) * p.n_hist + g.u];
+    }
     if (FMT != NKV_KV_BF16 && g.type == kSegHist)
       dma_i8_segment<FMT>(p, g, lh, buf, wave, lane);
     else
-      dma_segment(g, buf, wave, lane, kx, vx);
-    if (g.type == kSegHist && p.allowed != nullptr) {
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-        allow_nxt[ct] = p.allowed[p.allowed_ls * layer + static_cast<int64_t>(min(tcol[ct], p.tq - 1)) * p.n_hist + g.u];
-    }
+      dma_rows<kPfWaves>(g, buf, wave, lane, true);
   };
   auto finish_stage = [&](const Seg& g, char* buf) {
     __builtin_amdgcn_s_waitcnt(0);   // the asynchronous copies have landed
@@ -358,7 +616,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
     char* buf = P == 0 ? lds0 : lds1;
     char* other = P == 0 ? lds1 : lds0;
     const Seg cur = nxt;
-    const int allow_cur[2] = {allow_nxt[0], allow_nxt[1]};
+    int allow_cur[NCT];
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) allow_cur[ct] = allow_nxt[ct];
     int blk_next;
     const int s_next = next_seg(s + 1, &blk_next);
     const bool more = s_next < nseg;
@@ -367,81 +627,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
       begin_stage(nxt, other);
     }
 
-    // ---- S^T = K . Q^T -----------------------------------------------------
-    f32x4 S[4][2];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) S[kt][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(buf + kt * 4096 + koff[ks]);
-        S[kt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bq[0][ks], S[kt][0], 0, 0, 0);
-        S[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bq[1][ks], S[kt][1], 0, 0, 0);
-      }
-    }
-    if (needs_mask<PACKED>(p, cur, t0)) apply_mask<PACKED>(p, cur, lg, tcol, allow_cur, S);
-
-    // ---- online softmax (fp32) ----------------------------------------------
-    float alpha[2];
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      float mx = S[0][ct][0];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) mx = fmaxf(mx, S[kt][ct][e]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      // the reference max only moves when a logit exceeds it by more than
-      // 2^8 (p <= 256 is harmless in fp32 and bf16), so the accumulator
-      // rescale below is rare
-      const float cand = mx * p.scale_log2;
-      const float m_new = cand > m_run[ct] + 8.0f ? cand : m_run[ct];
-      const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-      alpha[ct] = __builtin_amdgcn_exp2f(m_run[ct] - m_use);
-      m_run[ct] = m_new;
-      float ls = 0.0f;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kt][ct][e], p.scale_log2, -m_use));
-          S[kt][ct][e] = pe;
-          ls += pe;
-        }
-      l_run[ct] = l_run[ct] * alpha[ct] + ls;
-    }
-    if (__any(alpha[0] != 1.0f || alpha[1] != 1.0f)) {
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) acc[dt][ct] *= alpha[ct];
-    }
-
-    // ---- O^T += V^T . P^T ---------------------------------------------------
-#pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      bf16x8 bp[2];
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const f32x4 a0 = S[2 * k2][ct];
-        const f32x4 a1 = S[2 * k2 + 1][ct];
-        bp[ct] = __builtin_bit_cast(bf16x8, u32x4{pack_bf16(a0[0], a0[1]), pack_bf16(a0[2], a0[3]),
-                                                  pack_bf16(a1[0], a1[1]), pack_bf16(a1[2], a1[3])});
-      }
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const char* vp = buf + vtr[dt & 3] + (dt >> 2) * 128 + k2 * 8192;
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vp));
-        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vp + 4096));
-        const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        acc[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[0], acc[dt][0], 0, 0, 0);
-        acc[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[1], acc[dt][1], 0, 0, 0);
-      }
-    }
+    attend_segment<PACKED, NCT, NCT == 2 ? 4 : 2>(p, cur, buf, needs_mask<PACKED>(p, cur, t0), lg, off, bq, tcol,
+                                                 allow_cur, acc, cs);
 
     if (more)
       finish_stage(nxt, other);
@@ -457,20 +644,18 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
 
   // ---- normalise and store: acc[dt][ct][i] = dim 16 dt + 4 lg + i -----------
 #pragma unroll
-  for (int ct = 0; ct < 2; ++ct) {
-    float l = l_run[ct];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+  for (int ct = 0; ct < NCT; ++ct) {
+    const float l = sum_over_rows(cs[ct].l);
     const int t = tcol[ct];
     if (p.splits > 1) {
       // this split's (m, l, acc) of the column, merged by prefill_merge_kernel
       if (t <= t_last) {
-        const int col = wave * 32 + ct * 16 + ln;
+        const int col = wave * 16 * NCT + ct * 16 + ln;
         float* rec = p.partial +
-                     ((((static_cast<int64_t>(layer) * p.hkv + h) * nqt + qt) * p.splits + split) * kPfCols + col) *
+                     ((((static_cast<int64_t>(layer) * p.hkv + h) * nqt + qt) * p.splits + split) * kCols + col) *
                          kPfPart;
         if (lg == 0) {
-          rec[0] = m_run[ct];
+          rec[0] = col_max(cs[ct]);
           rec[1] = l;
         }
 #pragma unroll
@@ -478,7 +663,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
       }
     } else if (t <= t_last) {
       const float inv = 1.0f / l;
-      uint16_t* orow = p.out + p.q_ls * layer + (static_cast<int64_t>(t) * hq + hcol[ct]) * kHeadDim + 4 * lg;
+      uint16_t* orow = p.out + p.q_ls * layer + (static_cast<int64_t>(t) * hq + head_of(ct)) * kHeadDim + 4 * lg;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         const f32x4 o = acc[dt][ct];
@@ -488,20 +673,21 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
   }
 }
 
+
 // Merge the split partials of one (layer, KV head, query tile, column): one
 // thread per dim, the usual rescale of each split's (m, l, acc) to the
 // largest reference max.
-__global__ __launch_bounds__(kHeadDim) void prefill_merge_kernel(const AttendParams p, int nqt) {
+__global__ __launch_bounds__(kHeadDim) void prefill_merge_kernel(const AttendParams p, int nqt, int cols) {
   const int h = blockIdx.x % p.hkv;
   const int qt = blockIdx.x / p.hkv;
   const int layer = blockIdx.y;
   const int col = blockIdx.z;
-  const int t = qt * (kPfCols / p.G) + col / p.G;
+  const int t = qt * (cols / p.G) + col / p.G;
   if (t >= p.tq) return;
   const int d = threadIdx.x;
-  const int64_t sstride = static_cast<int64_t>(kPfCols) * kPfPart;
+  const int64_t sstride = static_cast<int64_t>(cols) * kPfPart;
   const float* base =
-      p.partial + (((static_cast<int64_t>(layer) * p.hkv + h) * nqt + qt) * p.splits * kPfCols + col) * kPfPart;
+      p.partial + (((static_cast<int64_t>(layer) * p.hkv + h) * nqt + qt) * p.splits * cols + col) * kPfPart;
   float mt = -INFINITY;
   for (int s = 0; s < p.splits; ++s) mt = fmaxf(mt, base[s * sstride]);
   float L = 0.0f, A = 0.0f;
@@ -517,12 +703,34 @@ __global__ __launch_bounds__(kHeadDim) void prefill_merge_kernel(const AttendPar
 
 }  // namespace
 
+// Columns per workgroup a launch takes: 192 (three 16-column tiles per
+// wavefront: each staged K / V tile serves 1.5x the columns, for 1.5x fewer
+// LDS reads per product) when G divides it, the selection tile (if any) is a
+// whole number of its token tiles and the chunk fills two of them; 128
+// otherwise.  Per-query history flags keep the 128-column kernel, which holds
+// them in registers the wider one spends on its logits.
+int prefill_cols(const AttendParams& p, int tq) {
+  constexpr int kWide = 3 * 64;
+  if (kWide % p.G != 0 || p.allowed != nullptr) return kPfCols;
+  if (p.sel_tile > 0 && p.sel_tile % (kWide / p.G) != 0) return kPfCols;
+  return static_cast<int64_t>(tq) * p.G >= 2 * kWide ? kWide : kPfCols;
+}
+
+template <int FMT, bool PACKED>
+void launch_prefill_fmt(int cols, const dim3& grid, AttendParams& p, int nqt, hipStream_t s) {
+  if (cols == kPfCols)
+    hipLaunchKernelGGL((prefill_kernel<FMT, PACKED, 2>), grid, dim3(kPfThreads), 0, s, p, nqt);
+  else
+    hipLaunchKernelGGL((prefill_kernel<FMT, PACKED, 3>), grid, dim3(kPfThreads), 0, s, p, nqt);
+}
+
 // The matrix-core kernel over (query tile x KV head, layer, split), then the
 // split merge.
 int launch_prefill(int hkv, int kv_format, int num_layers, int tq, AttendParams& p, hipStream_t s) {
   NKV_CHECK_SUPPORTED(p.G >= 1 && kPfCols % p.G == 0,
                       "nkv_prefill_attend: query heads per KV head (%d) must divide %d", p.G, kPfCols);
-  const int tpw = kPfCols / p.G;
+  const int cols = prefill_cols(p, tq);
+  const int tpw = cols / p.G;
   const int nqt = (tq + tpw - 1) / tpw;
   const dim3 grid(nqt * hkv, num_layers, p.splits);
   const bool packed = p.tok_mask != nullptr || p.causal_off != 0;
@@ -530,21 +738,17 @@ int launch_prefill(int hkv, int kv_format, int num_layers, int tq, AttendParams&
   switch (kv_format) {
     case NKV_KV_BF16:
       if (packed)
-        hipLaunchKernelGGL((prefill_kernel<NKV_KV_BF16, true>), grid, dim3(kPfThreads), 0, s, p, nqt);
+        launch_prefill_fmt<NKV_KV_BF16, true>(cols, grid, p, nqt, s);
       else
-        hipLaunchKernelGGL((prefill_kernel<NKV_KV_BF16, false>), grid, dim3(kPfThreads), 0, s, p, nqt);
+        launch_prefill_fmt<NKV_KV_BF16, false>(cols, grid, p, nqt, s);
       break;
-    case NKV_KV_INT8_CHANNEL:
-      hipLaunchKernelGGL((prefill_kernel<NKV_KV_INT8_CHANNEL, false>), grid, dim3(kPfThreads), 0, s, p, nqt);
-      break;
-    case NKV_KV_INT8_TOKEN:
-      hipLaunchKernelGGL((prefill_kernel<NKV_KV_INT8_TOKEN, false>), grid, dim3(kPfThreads), 0, s, p, nqt);
-      break;
+    case NKV_KV_INT8_CHANNEL: launch_prefill_fmt<NKV_KV_INT8_CHANNEL, false>(cols, grid, p, nqt, s); break;
+    case NKV_KV_INT8_TOKEN: launch_prefill_fmt<NKV_KV_INT8_TOKEN, false>(cols, grid, p, nqt, s); break;
     default: NKV_CHECK_SUPPORTED(false, "nkv_prefill_attend: unknown kv_format %d", kv_format);
   }
   if (p.splits > 1)
-    hipLaunchKernelGGL(prefill_merge_kernel, dim3(nqt * hkv, num_layers, min(kPfCols, tq * p.G)), dim3(kHeadDim), 0,
-                       s, p, nqt);
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3(nqt * hkv, num_layers, min(cols, tq * p.G)), dim3(kHeadDim), 0, s, p,
+                       nqt, cols);
   return NKV_OK;
 }
 
@@ -558,9 +762,13 @@ extern "C" int64_t nkv_prefill_workspace_floats(int num_layers, int num_kv_heads
       tq < 1 || splits < 1)
     return 0;
   const int G = num_heads / num_kv_heads;
-  if (kPfCols % G != 0) return 0;
-  const int64_t nqt = (tq + kPfCols / G - 1) / (kPfCols / G);
-  return splits == 1 ? 0 : static_cast<int64_t>(num_layers) * num_kv_heads * nqt * splits * kPfCols * kPfPart;
+  if (kPfCols % G != 0 || splits == 1) return 0;
+  // any tiling may run: the largest need
+  int64_t cols_total = 0;
+  for (int cols : {kPfCols, 3 * 64})
+    if (cols % G == 0)
+      cols_total = std::max<int64_t>(cols_total, ((tq + cols / G - 1) / (cols / G)) * static_cast<int64_t>(cols));
+  return static_cast<int64_t>(num_layers) * num_kv_heads * splits * cols_total * kPfPart;
 }
 
 extern "C" int nkv_prefill_attend(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,

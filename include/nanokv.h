@@ -268,7 +268,8 @@ int nkv_decode_step_ring(const nkv_store* st, int layer0, int num_layers, const 
  * Feed out_union (n_hist = umax) and out_allowed (allowed_layer_stride =
  * tq * umax) to nkv_attend / nkv_prefill_attend.
  * Constraints: 1 <= tq <= 16, 1 <= k_eff <= k, tq * k_eff <= 4096,
- *              umax >= tq * k_eff.
+ *              umax >= tq * k_eff; ids in [0, 12288) (the block ids
+ *              nkv_select returns; other values are left out of both outputs).
  */
 int nkv_select_union(const int32_t* ids, int num_layers, int tq, int k, int k_eff, int umax,
                      int32_t* out_union, int32_t* out_count, uint8_t* out_allowed, void* stream);

@@ -48,29 +48,6 @@ namespace nkv {
 namespace {
 using namespace attend_detail;
 
-typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
-
-// K/V loads.  NT: non-temporal (a decode step reads each selected block once,
-// so the stream should not evict the lines that are reused: the next step's
-// representatives, queries, ids, partials).
-template <bool NT>
-__device__ __forceinline__ uint4 kv_load16(const char* p) {
-  if (NT) {
-    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-  }
-  return *reinterpret_cast<const uint4*>(p);
-}
-template <bool NT>
-__device__ __forceinline__ uint2 kv_load8(const char* p) {
-  if (NT) {
-    const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
-    return make_uint2(v.x, v.y);
-  }
-  return *reinterpret_cast<const uint2*>(p);
-}
-
 // LDS floats of one workgroup: the per-wave p tiles during the segment loop,
 // reused afterwards for the cross-wave merge (m, l and acc of every wave).
 template <int M>
@@ -481,7 +458,7 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
       const int hh = h * p.G + n % p.G;
       p.out[p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d] = f32_to_bf16(A / L);
     } else {
-      float* part = p.partial + ((grp * p.splits + split) * kMaxRows + n) * kPartStride;
+      float* part = p.partial + ((grp * p.splits + split) * p.prow + n) * kPartStride;
       part[2 + d] = A;
       if (d == 0) {
         part[0] = mt;
@@ -491,44 +468,464 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
   }
 }
 
-// Merge the split partials: one workgroup per (KV head, layer x group, row),
-// one thread per output dim.  Runs after attend_kernel on the same stream, so
-// the partials are visible without device-scope fences.
-__global__ __launch_bounds__(kHeadDim) void attend_merge_kernel(const AttendParams p) {
-  const int h = blockIdx.x;
-  const int layer = blockIdx.y / p.nqg;
-  const int qg = blockIdx.y % p.nqg;
-  const int n = blockIdx.z;
-  const int d = threadIdx.x;
+// The wide few-query kernel: up to 32 query rows (two 16-column MFMA tiles)
+// per (layer, KV head, query group), for verify-sized chunks (6 tokens x 4
+// heads = 24 rows), which the 16-row kernel would split into two groups that
+// each read every selected block.  Same segments, masks, split partials and
+// numerics as attend_kernel's 4-row form: Q.K^T and P.V on the matrix cores,
+// P as bf16 hi + lo parts (fp32-accurate P.V), int8 widened exactly with the
+// scales folded into the query operand / p.  Registers: K (64) and the
+// accumulators (32 logits, 64 O^T) are live together, so V is loaded once
+// the Q.K^T products have consumed K (V's latency overlaps the softmax), and
+// the query operands are read from LDS per product instead of held.
+template <int FMT>
+__global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const AttendParams p) {
+  constexpr int NCT = kWideRows / 16;   // MFMA column tiles
+  constexpr bool kI8 = FMT != NKV_KV_BF16;
+  constexpr int kQCopies = FMT == NKV_KV_INT8_CHANNEL ? 2 : 1;
+#ifndef NKV_WIDE_PREFETCH_K
+#define NKV_WIDE_PREFETCH_K 0
+#endif
+  constexpr bool kPrefetchK = NKV_WIDE_PREFETCH_K;
+  // V tiles of the four waves (16 KiB each), reused for the cross-wave merge
+  __shared__ __attribute__((aligned(16))) char s_v[kAttendWaves * kVTileBytes];
+  // B operands: [copy][ct][s][lane] (copy 1: the K-scaled query of int8
+  // per-channel history); after the segment loop, the merge's m and l
+  __shared__ __attribute__((aligned(16))) bf16x8 s_q[kQCopies][NCT][4][kWave];
+  static_assert(sizeof(s_q) >= 2 * kAttendWaves * kWideRows * sizeof(float), "m, l fit the operand area");
+  float (*s_ml)[kAttendWaves][kWideRows] = reinterpret_cast<float (*)[kAttendWaves][kWideRows]>(&s_q[0][0][0][0]);
+
+  const int split = blockIdx.x;
+  const int h = blockIdx.y;
+  const int layer = blockIdx.z / p.nqg;
+  const int qg = blockIdx.z % p.nqg;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int ln = lane & 15;
+  const int lg = lane >> 4;
   const int hq = p.hkv * p.G;
   const int q0 = qg * p.qpg;
   const int rows = min(p.qpg, p.tq - q0) * p.G;
-  if (n >= rows) return;
-  const int64_t grp = (static_cast<int64_t>(layer) * p.hkv + h) * p.nqg + qg;
-  const float* base = p.partial + (grp * p.splits * kMaxRows + n) * kPartStride;
-  const int64_t sstride = static_cast<int64_t>(kMaxRows) * kPartStride;
-  float mt = -INFINITY;
-#pragma unroll 8
-  for (int s = 0; s < p.splits; ++s) mt = fmaxf(mt, base[s * sstride]);
-  float L = 0.0f, A = 0.0f;
-#pragma unroll 8
-  for (int s = 0; s < p.splits; ++s) {
-    const float* ps = base + s * sstride;
-    const float ms = ps[0];
-    const float sw = (ms == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ms - mt);
-    L += ps[1] * sw;
-    A += ps[2 + d] * sw;
+
+  int write_slot = p.write_slot, ring_base = p.ring_base;
+  if (p.ring_start != nullptr) {
+    write_slot = static_cast<int>(static_cast<uint32_t>(p.ring_start[layer]) % static_cast<uint32_t>(p.R));
+    ring_base = write_slot + 1 == p.R ? 0 : write_slot + 1;
   }
-  const int t = q0 + n / p.G;
-  const int hh = h * p.G + n % p.G;
-  p.out[p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d] = f32_to_bf16(A / L);
+  if (p.zero_keys != nullptr && split == 0 && h == 0 && qg == 0) {
+    uint32_t* zk = p.zero_keys + static_cast<int64_t>(layer) * p.zero_n;
+    for (int i = threadIdx.x; i < p.zero_n; i += kAttendThreads) zk[i] = 0u;
+  }
+  if (write_slot >= 0 && split == 0 && qg == 0 && wave == 0 && lane < 32) {
+    const int which = lane >> 4;
+    const int c = lane & 15;
+    const uint4* src = reinterpret_cast<const uint4*>(
+        (which ? p.v_new : p.k_new) + p.kv_ls * layer + static_cast<int64_t>(h) * kHeadDim);
+    uint4* dst = reinterpret_cast<uint4*>((which ? p.rec_v : p.rec_k) + p.rec_ls * layer +
+                                         (static_cast<int64_t>(h) * p.R + write_slot) * kHeadDim);
+    dst[c] = src[c];
+  }
+
+  // ---- query operands into LDS: wave w fills column tile ct = w & 1, dim
+  // chunks s = 2 (w >> 1) + {0, 1} (row n = 16 ct + ln, dims 32 s + 8 lg) --
+  {
+    const int ct = wave & 1;
+    const int n = 16 * ct + ln;
+    const bool ok = n < rows;
+    const int t = q0 + (ok ? n / p.G : 0);
+    const int hh = h * p.G + n % p.G;
+#pragma unroll
+    for (int si = 0; si < 2; ++si) {
+      const int s = 2 * (wave >> 1) + si;
+      const int d0 = s * 32 + lg * 8;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (ok) v = *reinterpret_cast<const uint4*>(p.q + p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d0);
+      s_q[0][ct][s][lane] = as_bf16x8(v);
+      if constexpr (FMT == NKV_KV_INT8_CHANNEL) {
+        const float* ks = p.k_scale + static_cast<int64_t>(layer) * p.hkv * kHeadDim + h * kHeadDim + d0;
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a = bf16_lo(w[i]) * ks[2 * i];
+          const float b = bf16_hi(w[i]) * ks[2 * i + 1];
+          o[i] = static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+        }
+        s_q[kQCopies - 1][ct][s][lane] = as_bf16x8(make_uint4(o[0], o[1], o[2], o[3]));
+      }
+    }
+  }
+  __syncthreads();
+
+  // per column tile: row n = 16 ct + ln
+  bool row_ok[NCT];
+  int my_t[NCT];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    const int n = 16 * ct + ln;
+    row_ok[ct] = n < rows;
+    my_t[ct] = q0 + (row_ok[ct] ? n / p.G : 0);
+  }
+  float m_run[NCT], l_run[NCT];
+  f32x4 oacc[8][NCT];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    m_run[ct] = -INFINITY;
+    l_run[ct] = 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) oacc[dt][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  char* my_v = s_v + wave * kVTileBytes;
+  const int vw = lg * 256 + ((ln ^ (2 * lg)) << 4);
+  int vtr[4];
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4)
+    vtr[q4] = (4 * lg + (ln >> 2)) * 256 + ((2 * (q4 ^ (ln >> 2)) + ((ln & 3) >> 1)) << 4) + 8 * (ln & 1);
+  const int nwaves = p.splits * kAttendWaves;
+
+  // A history segment whose id lies outside the history attends nothing (a
+  // fully masked segment would leave m, l and acc as they are): passed over.
+  auto skip_empty = [&](int sidx, int end) {
+    while (sidx < end && sidx < p.n_hist) {
+      const int blk = p.ids[static_cast<int64_t>(layer) * p.ids_ls + sidx];
+      if (blk >= 0 && blk < p.cap) break;
+      sidx += nwaves;
+    }
+    return sidx;
+  };
+
+  // The wave's segments sidx, sidx + nwaves, ... below `end`, all int8
+  // history (int8 tag) or all bf16.  K of the next segment is loaded while
+  // the current one's P.V runs (its registers are free once Q.K^T consumed
+  // them); V of a segment is loaded after its Q.K^T, overlapping the softmax.
+  // Returns the first index at or past `end`.
+  auto run_phase = [&](int sidx, int end, auto int8_tag) __attribute__((always_inline)) {
+    constexpr bool int8_seg = decltype(int8_tag)::value;
+    typedef typename std::conditional<int8_seg, uint2, uint4>::type KReg;
+    const int qsel = (int8_seg && FMT == NKV_KV_INT8_CHANNEL) ? kQCopies - 1 : 0;
+    KReg ka[4][4];
+    auto load_k = [&](const Seg& g) __attribute__((always_inline)) {
+      const int last = g.len - 1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (int8_seg) {
+          const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 8;
+#pragma unroll
+          for (int s = 0; s < 4; ++s) ka[i][s] = kv_load8<false>(rp + s * 32);
+        } else {
+          const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 16;
+#pragma unroll
+          for (int s = 0; s < 4; ++s) ka[i][s] = kv_load16<false>(rp + s * 64);
+        }
+      }
+    };
+    sidx = skip_empty(sidx, end);
+    if (sidx >= end) return sidx;
+    Seg g = make_seg<FMT>(p, layer, h, sidx);
+    if (kPrefetchK) load_k(g);
+    while (true) {
+      const int last = g.len - 1;
+      if (!kPrefetchK) load_k(g);
+      // ---- S^T = K . Q^T on the matrix cores ---------------------------------
+      f32x4 c[4][NCT];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) c[i][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        bf16x8 bq[NCT];
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) bq[ct] = s_q[qsel][ct][s][lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          bf16x8 a;
+          if constexpr (int8_seg)
+            a = as_bf16x8(i8x8_to_bf16x8(ka[i][s].x, ka[i][s].y));
+          else
+            a = as_bf16x8(ka[i][s]);
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) c[i][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bq[ct], c[i][ct], 0, 0, 0);
+        }
+      }
+      // V after the products: lane (lg, ln) loads dims [8 ln, +8) of key 4 j + lg
+      __builtin_amdgcn_sched_barrier(0);
+      uint4 va[16];
+      if constexpr (int8_seg) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const uint2 r = kv_load8<false>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 8);
+          va[j] = make_uint4(r.x, r.y, 0u, 0u);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) va[j] = kv_load16<false>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 16);
+      }
+
+      // ---- masking, scale, online softmax per column tile ------------------
+      // c[i][ct][e]: key 16 i + 4 lg + e, row 16 ct + ln
+      float vs_blk = 1.0f;
+      if (FMT == NKV_KV_INT8_CHANNEL && int8_seg)
+        vs_blk = p.v_scale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap + g.blk];
+      // Visibility, branch-free: key tk of the segment is visible to column
+      // tile ct iff d = 4 lg + (16 i + e) - thr[ct] <= 0, where thr[ct] is the
+      // last visible key (-1: none; the row's validity, the per-query history
+      // flags and the chunk's causal edge folded in); a ring piece also needs
+      // the slot's logical position in the window: x(tk) - (rec_len - 1) <= 0.
+      int base[NCT];
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        int thr = g.vlen - 1;
+        if (g.type == kSegChunk) thr = min(thr, my_t[ct] - g.off);
+        if (g.type == kSegHist && p.allowed != nullptr &&
+            p.allowed[p.allowed_ls * layer + static_cast<int64_t>(my_t[ct]) * p.n_hist + g.u] == 0)
+          thr = -1;
+        if (!row_ok[ct]) thr = -1;
+        base[ct] = 4 * lg - thr;
+      }
+      // ring piece: x = (slot - ring_base - rec_lo) mod R for slot off + key
+      int ra = 0;
+      const bool ring = g.type == kSegRecent;
+      if (ring) {
+        ra = (g.off - ring_base - p.rec_lo) % p.R;
+        ra = ra < 0 ? ra + p.R : ra;
+      }
+      float ktsc[4][4];
+      if constexpr (FMT == NKV_KV_INT8_TOKEN && int8_seg) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            ktsc[i][e] = f16_bits_to_f32(p.k_tscale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap * kBlock +
+                                                    static_cast<int64_t>(g.blk) * kBlock + i * 16 + lg * 4 + e]);
+      }
+      float alpha[NCT];
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            bool ok = base[ct] + (16 * i + e) <= 0;
+            if (ring) {
+              int x = ra + 16 * i + 4 * lg + e;
+              x -= p.R & ((p.R - 1 - x) >> 31);
+              ok = ok && x < p.rec_len;
+            }
+            float v = c[i][ct][e];
+            if constexpr (FMT == NKV_KV_INT8_TOKEN && int8_seg) v *= ktsc[i][e];
+            v = ok ? v * p.scale_log2 : -INFINITY;
+            c[i][ct][e] = v;
+            cmax = fmaxf(cmax, v);
+          }
+        }
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        const float m_new = fmaxf(m_run[ct], cmax);
+        alpha[ct] = (m_new == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_run[ct] - m_new);
+        float lsum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int tk = i * 16 + lg * 4 + e;
+            const float x = c[i][ct][e];
+            const float pe = (x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(x - m_new);
+            lsum += pe;
+            float pv = pe * vs_blk;
+            if (FMT == NKV_KV_INT8_TOKEN && int8_seg)
+              pv *= f16_bits_to_f32(p.v_tscale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap * kBlock +
+                                               static_cast<int64_t>(g.blk) * kBlock + tk]);
+            c[i][ct][e] = pv;
+          }
+        }
+        l_run[ct] = l_run[ct] * alpha[ct] + lsum;
+        m_run[ct] = m_new;
+      }
+
+      // ---- V to LDS, the next segment's K loads, O^T += V^T . P^T ----------
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) oacc[dt][ct] *= alpha[ct];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint4 vb = int8_seg ? i8x8_to_bf16x8(va[j].x, va[j].y) : va[j];
+        *reinterpret_cast<uint4*>(my_v + j * 1024 + vw) = vb;
+      }
+      wave_lds_sync();
+      // (the scheduling barrier keeps the next K loads after the V stores, so
+      // the two register sets are never live together)
+      __builtin_amdgcn_sched_barrier(0);
+      const int snext = skip_empty(sidx + nwaves, end);
+      const bool more = snext < end;
+      Seg gn = g;
+      if (more) {
+        gn = make_seg<FMT>(p, layer, h, snext);
+        if (kPrefetchK) load_k(gn);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+        bf16x8 bp[NCT], bl[NCT];
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) {
+          const float v8[8] = {c[2 * k2][ct][0], c[2 * k2][ct][1], c[2 * k2][ct][2], c[2 * k2][ct][3],
+                               c[2 * k2 + 1][ct][0], c[2 * k2 + 1][ct][1], c[2 * k2 + 1][ct][2], c[2 * k2 + 1][ct][3]};
+          uint32_t hw[4], lw[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            hw[i] = stage::pack_bf16(v8[2 * i], v8[2 * i + 1]);
+            lw[i] = stage::pack_bf16(v8[2 * i] - __uint_as_float(hw[i] << 16),
+                                     v8[2 * i + 1] - __uint_as_float(hw[i] & 0xffff0000u));
+          }
+          bp[ct] = as_bf16x8(make_uint4(hw[0], hw[1], hw[2], hw[3]));
+          bl[ct] = as_bf16x8(make_uint4(lw[0], lw[1], lw[2], lw[3]));
+        }
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const char* vp = my_v + vtr[dt & 3] + (dt >> 2) * 128 + k2 * 8192;
+          const stage::i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((stage::lds_i16x4*)(vp));
+          const stage::i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((stage::lds_i16x4*)(vp + 4096));
+          const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) {
+            oacc[dt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[ct], oacc[dt][ct], 0, 0, 0);
+            oacc[dt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bl[ct], oacc[dt][ct], 0, 0, 0);
+          }
+        }
+      }
+      wave_lds_sync();   // the next segment overwrites the V tile
+      if (!more) return snext;
+      sidx = snext;
+      g = gn;
+    }
+  };
+  int sidx = split * kAttendWaves + wave;
+  if (kI8) sidx = run_phase(sidx, p.n_hist, std::true_type{});
+  run_phase(sidx, p.nseg, std::false_type{});
+
+  // ---- merge the 4 wavefronts in LDS (reusing the V tiles) -----------------
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    l_run[ct] += __shfl_xor(l_run[ct], 16);
+    l_run[ct] += __shfl_xor(l_run[ct], 32);
+  }
+  __syncthreads();   // every wave is done with its V tile and the query operands
+  float* s_acc = reinterpret_cast<float*>(s_v);   // [waves][32][128]
+  if (lg == 0) {
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      s_ml[0][wave][16 * ct + ln] = m_run[ct];
+      s_ml[1][wave][16 * ct + ln] = l_run[ct];
+    }
+  }
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      *reinterpret_cast<f32x4*>(s_acc + ((wave * kWideRows + 16 * ct + ln) * kHeadDim) + 16 * dt + 4 * lg) =
+          oacc[dt][ct];
+  __syncthreads();
+
+  const int64_t grp = (static_cast<int64_t>(layer) * p.hkv + h) * p.nqg + qg;
+  for (int idx = threadIdx.x; idx < kWideRows * kHeadDim; idx += kAttendThreads) {
+    const int n = idx / kHeadDim, d = idx % kHeadDim;
+    if (n >= rows) continue;
+    float mt = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kAttendWaves; ++w) mt = fmaxf(mt, s_ml[0][w][n]);
+    float L = 0.0f, A = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttendWaves; ++w) {
+      const float mw = s_ml[0][w][n];
+      const float sw = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - mt);
+      L += s_ml[1][w][n] * sw;
+      A += s_acc[(w * kWideRows + n) * kHeadDim + d] * sw;
+    }
+    if (p.splits == 1) {
+      const int t = q0 + n / p.G;
+      const int hh = h * p.G + n % p.G;
+      p.out[p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d] = f32_to_bf16(A / L);
+    } else {
+      float* part = p.partial + ((grp * p.splits + split) * p.prow + n) * kPartStride;
+      part[2 + d] = A;
+      if (d == 0) {
+        part[0] = mt;
+        part[1] = L;
+      }
+    }
+  }
+}
+
+// Merge the split partials: one workgroup per (KV head, layer x group, 4
+// rows), 64 threads per row with 2 output dims each.  Every load of a
+// thread (each split's m, l and its two acc values) is issued before the
+// first is used, so the merge is one memory round trip.  Runs after the
+// attention on the same stream, so the partials are visible without
+// device-scope fences.
+constexpr int kMergeRows = 4;
+constexpr int kMergeThreads = kMergeRows * 64;
+__global__ __launch_bounds__(kMergeThreads) void attend_merge_kernel(const AttendParams p) {
+  const int h = blockIdx.x;
+  const int layer = blockIdx.y / p.nqg;
+  const int qg = blockIdx.y % p.nqg;
+  const int n = blockIdx.z * kMergeRows + (threadIdx.x >> 6);
+  const int d0 = (threadIdx.x & 63) * 2;
+  const int hq = p.hkv * p.G;
+  const int q0 = qg * p.qpg;
+  const int rows = min(p.qpg, p.tq - q0) * p.G;
   // device-ring decode: the attention has read this layer's ring start, so
   // one thread of the layer's first merge workgroup moves it one slot
-  if (p.ring_start != nullptr && h == 0 && qg == 0 && n == 0 && d == 0) {
+  if (p.ring_start != nullptr && h == 0 && qg == 0 && blockIdx.z == 0 && threadIdx.x == 0) {
     int32_t* rs = const_cast<int32_t*>(p.ring_start) + layer;
     const int v = static_cast<int>(static_cast<uint32_t>(*rs) % static_cast<uint32_t>(p.R));
     *rs = v + 1 == p.R ? 0 : v + 1;
   }
+  if (n >= rows) return;
+  const int64_t grp = (static_cast<int64_t>(layer) * p.hkv + h) * p.nqg + qg;
+  const float* base = p.partial + (grp * p.splits * p.prow + n) * kPartStride;
+  const int64_t sstride = static_cast<int64_t>(p.prow) * kPartStride;
+  float L = 0.0f, A0 = 0.0f, A1 = 0.0f;
+  // up to 8 splits at a time: all their loads in flight together
+  float mt = -INFINITY;
+  for (int s0 = 0; s0 < p.splits; s0 += 8) {
+    float m[8], l[8];
+    float2 a[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int s = min(s0 + i, p.splits - 1);
+      const float* ps = base + s * sstride;
+      m[i] = ps[0];
+      l[i] = ps[1];
+      // the record is [m, l, acc[128]] at an even float offset: 8-byte loads
+      a[i] = *reinterpret_cast<const float2*>(ps + 2 + d0);
+    }
+    float mb = mt;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (s0 + i < p.splits) mb = fmaxf(mb, m[i]);
+    // rescale what the earlier batches summed to the new reference max
+    const float r = (mt == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mt - mb);
+    L *= r;
+    A0 *= r;
+    A1 *= r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (s0 + i >= p.splits) break;
+      const float sw = (m[i] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m[i] - mb);
+      L += l[i] * sw;
+      A0 += a[i].x * sw;
+      A1 += a[i].y * sw;
+    }
+    mt = mb;
+  }
+  const int t = q0 + n / p.G;
+  const int hh = h * p.G + n % p.G;
+  *reinterpret_cast<uint32_t*>(p.out + p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d0) =
+      static_cast<uint32_t>(f32_to_bf16(A0 / L)) | (static_cast<uint32_t>(f32_to_bf16(A1 / L)) << 16);
 }
 
 // Device-ring decode: every layer's ring start moves one slot (mod R) once
@@ -547,12 +944,25 @@ int launch_fmt(int M, dim3 grid, hipStream_t s, const AttendParams& p) {
     case 4: hipLaunchKernelGGL((attend_kernel<FMT, 4, PACKED>), grid, dim3(kAttendThreads), 0, s, p); return 0;
     case 8: hipLaunchKernelGGL((attend_kernel<FMT, 8, PACKED>), grid, dim3(kAttendThreads), 0, s, p); return 0;
     case 16: hipLaunchKernelGGL((attend_kernel<FMT, 16, PACKED>), grid, dim3(kAttendThreads), 0, s, p); return 0;
+    case kWideRows:
+      if (PACKED) return -1;
+      hipLaunchKernelGGL((attend_wide_kernel<FMT>), grid, dim3(kAttendThreads), 0, s, p);
+      return 0;
     default: return -1;
   }
 }
 
-// Query rows per group and the template row count for a given (tq, G).
+// Query rows per group and the kernel's row count for a given (tq, G): one
+// 16-row MFMA tile when the chunk's rows fit it, else groups of two tiles
+// (the wide kernel).
 void group_shape(int tq, int G, int* qpg, int* M) {
+  if (tq * G > kMaxRows) {
+    int per = kWideRows / G;
+    if (per > tq) per = tq;
+    *qpg = per;
+    *M = kWideRows;
+    return;
+  }
   int per = kMaxRows / G;          // queries that fit one MFMA tile
   if (per > tq) per = tq;
   *qpg = per;
@@ -569,6 +979,7 @@ int launch_grouped(int hkv, int kv_format, int num_layers, int tq, AttendParams&
   group_shape(tq, p.G, &qpg, &M);
   p.qpg = qpg;
   p.nqg = (tq + qpg - 1) / qpg;
+  p.prow = M > kMaxRows ? kWideRows : kMaxRows;
   dim3 grid(p.splits, hkv, num_layers * p.nqg);
   int bad = 0;
   const bool packed = p.tok_mask != nullptr || p.causal_off != 0;
@@ -583,7 +994,8 @@ int launch_grouped(int hkv, int kv_format, int num_layers, int tq, AttendParams&
   }
   NKV_CHECK_SUPPORTED(bad == 0, "nkv_attend: unsupported row count %d / kv_format %d", M, kv_format);
   if (p.splits > 1)
-    hipLaunchKernelGGL(attend_merge_kernel, dim3(hkv, num_layers * p.nqg, qpg * p.G), dim3(kHeadDim), 0, s, p);
+    hipLaunchKernelGGL(attend_merge_kernel, dim3(hkv, num_layers * p.nqg, (qpg * p.G + kMergeRows - 1) / kMergeRows),
+                       dim3(kMergeThreads), 0, s, p);
   return NKV_OK;
 }
 
@@ -597,7 +1009,8 @@ extern "C" int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads,
   int qpg, M;
   group_shape(tq, num_heads / num_kv_heads, &qpg, &M);
   const int64_t nqg = (tq + qpg - 1) / qpg;
-  return static_cast<int64_t>(num_layers) * num_kv_heads * nqg * splits * kMaxRows * kPartStride;
+  const int prow = M > kMaxRows ? kWideRows : kMaxRows;
+  return static_cast<int64_t>(num_layers) * num_kv_heads * nqg * splits * prow * kPartStride;
 }
 
 namespace nkv {

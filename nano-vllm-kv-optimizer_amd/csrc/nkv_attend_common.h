@@ -17,6 +17,7 @@ constexpr int kAttendThreads = kAttendWaves * kWave;
 constexpr int kPRow = 20;        // floats per key row of the p tile in LDS (16 rows + pad)
 constexpr int kPartStride = 130; // floats per partial row: m, l, acc[128]
 constexpr int kMaxRows = 16;     // MFMA N: query rows per group
+constexpr int kWideRows = 32;    // query rows per group of the two-tile (wide) few-query kernel
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -73,6 +74,9 @@ struct AttendParams {
   // ids[layer][tile * ids_tile_ls + i]
   int64_t ids_tile_ls;
   int sel_tile;
+  // few-query kernels: partial records per (group, split) -- the group's row
+  // capacity (kMaxRows, or kWideRows for the wide kernel)
+  int prow;
 };
 
 __device__ __forceinline__ void wave_lds_sync() {
@@ -82,6 +86,29 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+
+// K/V loads.  NT: non-temporal (a decode step reads each selected block once,
+// so the stream should not evict the lines that are reused: the next step's
+// representatives, queries, ids, partials).
+template <bool NT>
+__device__ __forceinline__ uint4 kv_load16(const char* p) {
+  if (NT) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  }
+  return *reinterpret_cast<const uint4*>(p);
+}
+template <bool NT>
+__device__ __forceinline__ uint2 kv_load8(const char* p) {
+  if (NT) {
+    const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+    return make_uint2(v.x, v.y);
+  }
+  return *reinterpret_cast<const uint2*>(p);
+}
 
 // Max / sum of x over the four 16-lane rows of the wavefront (lanes l, l ^ 16,
 // l ^ 32, l ^ 48), the result in every lane.  gfx950's row swaps

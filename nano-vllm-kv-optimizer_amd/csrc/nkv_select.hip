@@ -594,46 +594,54 @@ __global__ __launch_bounds__(kWave) void topk_wave_kernel(
 constexpr int kUnionThreads = 256;
 constexpr int kUnionMax = 4096;  // tq * k_eff ids per layer
 
-// Union of one layer's per-query selections (one workgroup per layer): the
-// tq x k_eff ids are sorted in LDS (bitonic), the first id of every run of
-// equal ids is kept at its workgroup prefix-count position, and each query's
-// ids are located in the union by binary search to set its mask row.
+// Union of one layer's per-query selections (one workgroup per layer),
+// through a bitmap of block ids in LDS: every selected id sets its bit, a
+// prefix count over the bitmap words gives each set bit its position in the
+// ascending union, and each query's ids find their mask columns by the same
+// count.  Five barriers, no sort.  Ids are block ids of nkv_select (below
+// kMaxSelectBlocks); any other value is left out of the union and the mask.
+constexpr int kUnionWords = kMaxSelectBlocks / 32;
 __global__ __launch_bounds__(kUnionThreads) void union_kernel(
     const int32_t* __restrict__ ids, int tq, int k, int k_eff, int umax, int32_t* __restrict__ out_union,
     int32_t* __restrict__ out_count, uint8_t* __restrict__ out_allowed) {
-  __shared__ int32_t a[kUnionMax];
-  __shared__ int32_t u[kUnionMax];
+  __shared__ uint32_t bits[kUnionWords];
+  __shared__ int32_t pre[kUnionWords];     // set bits in the words before
   __shared__ int32_t wsum[kUnionThreads / kWave];
-  __shared__ int32_t s_total;
+  __shared__ int32_t s_max;
   const int layer = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = tq * k_eff;
-  int n2 = 1;
-  while (n2 < n) n2 <<= 1;
   const int32_t* src = ids + static_cast<int64_t>(layer) * tq * k;
-  for (int i = tid; i < n2; i += kUnionThreads) a[i] = i < n ? src[(i / k_eff) * k + i % k_eff] : INT32_MAX;
-  __syncthreads();
-  for (int size = 2; size <= n2; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = tid; i < (n2 >> 1); i += kUnionThreads) {
-        const int lo = 2 * i - (i & (stride - 1));
-        const int hi = lo + stride;
-        const bool asc = (lo & size) == 0;
-        const int32_t x = a[lo], y = a[hi];
-        if (asc ? (x > y) : (x < y)) {
-          a[lo] = y;
-          a[hi] = x;
-        }
-      }
-      __syncthreads();
-    }
+  auto id_at = [&](int i) { return src[(i / k_eff) * k + i % k_eff]; };
+  auto valid = [](int32_t id) { return id >= 0 && id < kMaxSelectBlocks; };
+
+  // the largest id bounds the words to clear and count
+  int32_t mx = -1;
+  for (int i = tid; i < n; i += kUnionThreads) {
+    const int32_t id = id_at(i);
+    if (valid(id)) mx = max(mx, id);
   }
-  // thread t keeps the run starts of [t * per, (t + 1) * per)
-  const int per = (n + kUnionThreads - 1) / kUnionThreads;
-  const int i0 = min(tid * per, n), i1 = min(i0 + per, n);
+  for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o));
+  if (tid == 0) s_max = -1;
+  __syncthreads();
+  if (lane == 0) atomicMax(&s_max, mx);
+  __syncthreads();
+  const int nwords = (s_max + 32) >> 5;   // 0 when no id is valid
+  for (int w = tid; w < nwords; w += kUnionThreads) bits[w] = 0u;
+  __syncthreads();
+  for (int i = tid; i < n; i += kUnionThreads) {
+    const int32_t id = id_at(i);
+    if (valid(id)) atomicOr(&bits[id >> 5], 1u << (id & 31));
+  }
+  __syncthreads();
+
+  // exclusive prefix count of set bits over the words (thread t owns a
+  // contiguous run of words)
+  const int per = (nwords + kUnionThreads - 1) / kUnionThreads;
+  const int w0 = min(tid * per, nwords), w1 = min(w0 + per, nwords);
   int cnt = 0;
-  for (int i = i0; i < i1; ++i) cnt += (i == 0 || a[i] != a[i - 1]);
+  for (int w = w0; w < w1; ++w) cnt += __popc(bits[w]);
   int incl = cnt;
   for (int o = 1; o < kWave; o <<= 1) {
     const int t = __shfl_up(incl, o);
@@ -643,28 +651,38 @@ __global__ __launch_bounds__(kUnionThreads) void union_kernel(
   __syncthreads();
   int base = 0;
   for (int w = 0; w < wave; ++w) base += wsum[w];
-  int pos = base + incl - cnt;
-  for (int i = i0; i < i1; ++i)
-    if (i == 0 || a[i] != a[i - 1]) u[pos++] = a[i];
-  if (tid == kUnionThreads - 1) s_total = base + incl;
+  int run = base + incl - cnt;
+  for (int w = w0; w < w1; ++w) {
+    pre[w] = run;
+    run += __popc(bits[w]);
+  }
+  int U = 0;
+  for (int w = 0; w < kUnionThreads / kWave; ++w) U += wsum[w];
   __syncthreads();
-  const int U = s_total;
+
+  // the union, ascending, then -1
   int32_t* ou = out_union + static_cast<int64_t>(layer) * umax;
-  for (int i = tid; i < umax; i += kUnionThreads) ou[i] = i < U ? u[i] : -1;
+  for (int w = tid; w < nwords; w += kUnionThreads) {
+    uint32_t b = bits[w];
+    int pos = pre[w];
+    while (b != 0u) {
+      const int bit = __builtin_ctz(b);
+      ou[pos++] = 32 * w + bit;
+      b &= b - 1u;
+    }
+  }
+  for (int i = U + tid; i < umax; i += kUnionThreads) ou[i] = -1;
   if (tid == 0) out_count[layer] = U;
+
+  // mask rows: zeros, then each query's ids at their union positions
   uint8_t* oa = out_allowed + static_cast<int64_t>(layer) * tq * umax;
   for (int i = tid; i < tq * umax; i += kUnionThreads) oa[i] = 0;
   __syncthreads();  // the zeros are written before the ones
   for (int i = tid; i < n; i += kUnionThreads) {
-    const int t = i / k_eff;
-    const int32_t id = src[t * k + i % k_eff];
-    int lo = 0, hi = U;  // first union entry >= id (the id itself)
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (u[mid] < id) lo = mid + 1;
-      else hi = mid;
-    }
-    oa[static_cast<int64_t>(t) * umax + lo] = 1;
+    const int32_t id = id_at(i);
+    if (!valid(id)) continue;
+    const int pos = pre[id >> 5] + __popc(bits[id >> 5] & ((1u << (id & 31)) - 1u));
+    oa[static_cast<int64_t>(i / k_eff) * umax + pos] = 1;
   }
 }
 

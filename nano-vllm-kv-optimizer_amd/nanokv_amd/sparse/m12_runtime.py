@@ -33,6 +33,18 @@ import torch
 from .. import _lib
 from ..store import SparseKVStore, packed_attention, query_summaries, tile_summaries
 
+# Query rows per group of the few-query kernels: one 16-column MFMA tile, or
+# two (the wide kernel) once a chunk's rows exceed one tile.
+TILE_ROWS = 16
+WIDE_ROWS = 32
+
+
+def few_query_group(tq: int, g: int) -> int:
+    """Queries per group of the few-query attention (the C side's group_shape)."""
+    rows = WIDE_ROWS if tq * g > TILE_ROWS else TILE_ROWS
+    return min(tq, max(1, rows // g))
+
+
 # ---------------------------------------------------------------------------
 # Host-side helpers (same contracts as the reference's module functions)
 # ---------------------------------------------------------------------------
@@ -98,8 +110,9 @@ class M12Config:
     (prefill / verify chunks of at least this many queries use the
     matrix-core kernel, shorter ones the few-query kernel; None = automatic:
     the matrix-core kernel as soon as the chunk's query rows, tokens x heads
-    per KV head, exceed the few-query kernel's 16-row group, which it would
-    otherwise split, reading every block once per group), ``history_tier``
+    per KV head, exceed the few-query kernels' widest group of 32 rows, which
+    they would otherwise split, reading every block once per group),
+    ``history_tier``
 ("hbm": the whole history in HBM; "host": hist_k / hist_v in pinned host
 memory, read in place by the same kernels over the host link, the
 reference's offload mode without its gather and H2D copy).  ``use_index_select``,
@@ -394,7 +407,7 @@ class _SparseCore:
         scale = cfg.scale if scale is None else scale
         nl, tq = q.shape[0], q.shape[1]
         g = cfg.num_heads // cfg.num_kv_heads
-        qpg = min(tq, max(1, 16 // g))
+        qpg = few_query_group(tq, g)
         nqg = -(-tq // qpg)
         R = cfg.recent_tokens
         nseg = n_hist + -(-sink_len // 64) + (-(-R // 64) if rec_len else 0) + -(-n_chunk // 64)
@@ -515,7 +528,7 @@ class _SparseCore:
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
         tq, g = q.shape[1], cfg.num_heads // cfg.num_kv_heads
         ids = ids.contiguous()
-        if tq <= tile and not (tq * g > 16 if cfg.mfma_chunk_min_tokens is None else tq >= cfg.mfma_chunk_min_tokens):
+        if tq <= tile and not self._uses_mfma(tq):
             return self.chunk_attend(q, k, v, ids, ids.shape[1] * ids.shape[2], n_hist, scale=scale)
         sink_len = min(cfg.sink_tokens, self.valid_len)
         _, off, ln = prefill_recent_slice(self.valid_len, cfg.sink_tokens, cfg.recent_tokens)
@@ -530,6 +543,15 @@ class _SparseCore:
                                         tile, n_hist, sink_len, self.ring_start, off, ln, scale, out, splits, part)
         return out, sink_len, ln
 
+    def _uses_mfma(self, tq: int) -> bool:
+        """Whether a chunk of tq queries takes the matrix-core kernel: its query
+        rows (tq x heads per KV head) exceed the widest few-query group, or
+        cfg.mfma_chunk_min_tokens says so."""
+        cfg = self.cfg
+        if cfg.mfma_chunk_min_tokens is not None:
+            return tq >= cfg.mfma_chunk_min_tokens
+        return tq * (cfg.num_heads // cfg.num_kv_heads) > WIDE_ROWS
+
     def chunk_attend(self, q, k, v, ids, ids_stride, n_hist, allowed=None, allowed_stride=0,
                      scale=None):
         """[selected | sink | previous recent | chunk (causal)] (m12_runtime.py:592-639, :725-758).
@@ -543,8 +565,8 @@ class _SparseCore:
         sink_len = min(cfg.sink_tokens, self.valid_len)
         _, off, ln = prefill_recent_slice(self.valid_len, cfg.sink_tokens, cfg.recent_tokens)
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-        tq, g = q.shape[1], cfg.num_heads // cfg.num_kv_heads
-        if (tq * g > 16 if cfg.mfma_chunk_min_tokens is None else tq >= cfg.mfma_chunk_min_tokens):
+        tq = q.shape[1]
+        if self._uses_mfma(tq):
             out = torch.empty_like(q)
             B = cfg.block_size
             nseg = n_hist + -(-sink_len // B) + (-(-cfg.recent_tokens // B) if ln else 0) + -(-tq // B)
@@ -611,6 +633,14 @@ class M12LayerRuntime:
         # gather_sort and query windows keep the regular path
         self.device_ring = False
         self.last_verify_timings: dict = {}
+        # selector graph (use_graph): one captured score + top-k per sequence
+        # and shape; _reps_version moves whenever representatives are rebuilt
+        self._selector_graph = None
+        self._selector_graph_key = None
+        self._selector_graph_q = None
+        self._selector_graph_outputs = None
+        self._selector_graph_keep = None
+        self._reps_version = 0
         self.selector_graph_setup_ms = 0.0
         self.selector_graph_builds = 0
         self.profile_cuda_stages = False
@@ -690,6 +720,7 @@ class M12LayerRuntime:
         self.ids_history.clear()
         self.q_history.clear()
         self._q_window.clear()
+        self._clear_selector_graph()
         self.selector_graph_setup_ms = 0.0
         self.selector_graph_builds = 0
 
@@ -784,10 +815,18 @@ class M12LayerRuntime:
         """k_blocks [N, B, Hkv, D] -> reps_gpu[:, start:start+N] (m12_runtime.py:354-395)."""
         kb = self._as_bf16(k_blocks[:nblocks], "k_blocks")
         n, b, hkv, d = kb.shape
+        self._reps_changed()
         self.store.build_reps(self.store_layer, kb.reshape(1, n * b, hkv, d), start)
 
     def _store_kv(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        self._reps_changed()
         self._core.store_kv(self._as_bf16(k, "k").unsqueeze(0), self._as_bf16(v, "v").unsqueeze(0))
+
+    def _reps_changed(self) -> None:
+        """Representatives are about to be rebuilt: a captured selector graph is
+        dropped (m12_runtime.py:362-363)."""
+        self._clear_selector_graph()
+        self._reps_version += 1
 
     def prefill_first(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> dict:
         """Store the first chunk; its dense attention is the caller's (m12_runtime.py:518-523)."""
@@ -815,17 +854,81 @@ class M12LayerRuntime:
         return out[0]
 
     # -- selection -------------------------------------------------------------------
-    def _select_dev(self, q3: torch.Tensor, requested: int, order: int):
+    def _select_dev(self, q3: torch.Tensor, requested: int, order: int, use_graph: bool = False):
+        if use_graph:
+            return self._graph_select(q3, requested, order)
         ids, vals, k = self._core.select(q3.unsqueeze(0), requested, order=order)
         return ids, vals, k
+
+    # -- selector graph (m12_runtime.py:294-299, :901-957) -------------------------
+    def _clear_selector_graph(self) -> None:
+        self._selector_graph = None
+        self._selector_graph_key = None
+        self._selector_graph_q = None
+        self._selector_graph_outputs = None
+        self._selector_graph_keep = None
+
+    def _graph_select(self, q3: torch.Tensor, requested: int, order: int):
+        """The score + top-k launches captured once in a HIP graph and replayed.
+
+        A capture serves one (history length, budget, protected set within the
+        history, query shape, id order, representatives' storage and version);
+        any change captures anew (one graph per runtime, as m12_runtime.py:
+        916-957 keeps), counted in selector_graph_builds with its set-up time
+        in selector_graph_setup_ms.  The representatives are read through the
+        same pointer on every replay, so in-place edits are seen.  Returns the
+        graph's own (ids, vals) buffers, rewritten by the next replay, and k.
+        Same kernels and results as the eager selection (neither clears memory
+        with a memset: the top-k leaves the score keys zero)."""
+        nb = self.nblocks_filled
+        if nb <= 0:
+            raise ValueError("selection needs at least one history block")
+        prot_ids = tuple(sorted(p for p in self.protected_blocks if 0 <= p < nb))
+        key = (nb, int(requested), prot_ids, tuple(q3.shape), q3.dtype, q3.device, int(order),
+               self.reps_gpu.data_ptr(), self._reps_version)
+        if key != self._selector_graph_key:
+            self._clear_selector_graph()
+            started = perf_counter()
+            dev = q3.device
+            static_q = q3.detach().clone()
+            side = torch.cuda.Stream(device=dev)
+            side.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(side):
+                # the eager run allocates every workspace (and the protected
+                # list) the capture then records, so nothing is allocated
+                # inside it
+                self._core.select(static_q.unsqueeze(0), requested, order=order, ws="/graph")
+            side.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(side):
+                graph.capture_begin()
+                try:
+                    ids, vals, k = self._core.select(static_q.unsqueeze(0), requested, order=order,
+                                                     ws="/graph")
+                finally:
+                    graph.capture_end()
+            torch.cuda.current_stream(dev).wait_stream(side)
+            self._selector_graph = graph
+            self._selector_graph_q = static_q
+            self._selector_graph_outputs = (ids, vals, k)
+            # the buffers the graph reads and writes stay alive with it
+            self._selector_graph_keep = (self._core.protected_dev()[0], dict(self._core._ws))
+            self._selector_graph_key = key
+            self.selector_graph_setup_ms += (perf_counter() - started) * 1000.0
+            self.selector_graph_builds += 1
+        self._selector_graph_q.copy_(q3)
+        self._selector_graph.replay()
+        return self._selector_graph_outputs
 
     def _gpu_select(self, q: torch.Tensor, *, dynamic: bool = False, budget: int | None = None,
                     use_graph: bool = False, use_static_mask: bool = False,
                     use_relative: bool = False):
         """Block scores + Top-K; returns (block_ids_cpu [K] int64, info).
 
-        Reference: m12_runtime.py:959-1055.  The graph and static-mask options
-        select the same kernel (one score launch + one Top-K launch).
+        Reference: m12_runtime.py:959-1055.  With use_graph and
+        cfg.selector_cuda_graph the two launches (score, Top-K) replay from a
+        captured HIP graph (_graph_select); the static-mask option selects the
+        same launches (the protected list is cached on the device either way).
         """
         cfg = self.cfg
         if q.ndim == 2:
@@ -836,7 +939,8 @@ class M12LayerRuntime:
             raise ValueError("relative-threshold selection requires the flat GPU path")
         requested_k = cfg.top_k_blocks if budget is None else budget
         t_enq = perf_counter()
-        ids_cpu, vals_cpu, k = self._select_host(q, requested_k, use_relative)
+        ids_cpu, vals_cpu, k = self._select_host(q, requested_k, use_relative,
+                                                 use_graph=use_graph and cfg.selector_cuda_graph)
         t_d2h = perf_counter()
         chosen = k
         if dynamic and cfg.dynamic_top_k and k == requested_k:
@@ -852,11 +956,11 @@ class M12LayerRuntime:
             "n_query_summaries": q.shape[0],
         }
 
-    def _select_host(self, q: torch.Tensor, requested_k: int, use_relative: bool):
+    def _select_host(self, q: torch.Tensor, requested_k: int, use_relative: bool, use_graph: bool = False):
         """Selected ids and scores on the host (score-desc order)."""
         cfg = self.cfg
         if not use_relative:
-            ids, vals, k = self._select_dev(q, requested_k, _lib.NKV_ORDER_SCORE_DESC)
+            ids, vals, k = self._select_dev(q, requested_k, _lib.NKV_ORDER_SCORE_DESC, use_graph=use_graph)
             return ids[0, 0, :k].to("cpu", torch.int64), vals[0, 0, :k].cpu(), k
         # relative threshold (m12_runtime.py:1015-1031): keep candidates within
         # ln(a)/scale of the best among the top `cap`, or top-k in union mode.
@@ -947,7 +1051,7 @@ class M12LayerRuntime:
         override = self._select_override()
         host_rule = cfg.decode_relative_a is not None or cfg.dynamic_top_k or override is not None
         if (self.device_ring and self.device_ring_ready() and override is None
-                and not self.profile_cuda_stages):
+                and not self.profile_cuda_stages and not cfg.selector_cuda_graph):
             return self._decode_ring(q, k, v, requested, t0)
         # the recent append runs inside the attention launch (the new token is
         # written to the ring slot it frees), so its event pair spans nothing
@@ -962,6 +1066,8 @@ class M12LayerRuntime:
                     use_relative=cfg.decode_relative_a is not None))
             elif host_rule:
                 ids_cpu, info = self._gpu_select(q_route, dynamic=cfg.dynamic_top_k, budget=requested,
+                                                 use_graph=cfg.selector_cuda_graph,
+                                                 use_static_mask=cfg.selector_static_mask,
                                                  use_relative=cfg.decode_relative_a is not None)
             if host_rule:
                 if cfg.gather_sort and ids_cpu.numel() > 1:
@@ -971,7 +1077,8 @@ class M12LayerRuntime:
                 stride = n_hist
             else:
                 order = _lib.NKV_ORDER_ID_ASC if cfg.gather_sort else _lib.NKV_ORDER_SCORE_DESC
-                ids_dev, _, n_hist = self._select_dev(q_route, requested, order)
+                ids_dev, _, n_hist = self._select_dev(q_route, requested, order,
+                                                      use_graph=cfg.selector_cuda_graph)
                 stride = ids_dev.shape[-1]
         self._event_end(ev)
         selector_ms = (perf_counter() - t0) * 1000.0

@@ -91,10 +91,40 @@ def test_planted_query_chunk_attends_planted_blocks():
     assert set(planted) <= set(rt.last_prefill_block_ids.tolist())
 
 
+@pytest.mark.parametrize("fmt", ["bf16", "int8", "int8_token"])
+def test_chunks_on_the_wide_few_query_kernel_match_oracle(fmt):
+    """Chunks forced onto the few-query kernel (mfma_chunk_min_tokens above
+    them): its wide form takes 32 query rows per group, so 7 tokens x 4 heads
+    are one group, 100 tokens 13 groups and 37 tokens 5 with a ragged last
+    one.  fp32 P.V, so bf16 history meets the tight bar; int8 history folds
+    the K scale into the query operand / the logits (rel 2^-6)."""
+    quant = fmt != "bf16"
+    layout = "token" if fmt == "int8_token" else "channel_block"
+    rt, ob = _pair(4096, layout=layout, quant_history=quant, mfma_chunk_min_tokens=10000)
+    k0, v0 = _rand((2000, 8, 128), 13, 0.09), _rand((2000, 8, 128), 14, 0.09)
+    rt.prefill_first(None, k0.cuda(), v0.cuda())
+    ob.store_kv(to_np(k0), to_np(v0), with_reps=False)
+    _sync(rt, ob, layout == "token")
+    tol = dict(rel=2.0 ** -6, abs_tol=2e-4) if quant else {}
+    for i, T in enumerate((7, 100, 37)):
+        print(f"[wide few-query {fmt}] chunk {i}: T={T}", flush=True)
+        q = _rand((T, 32, 128), 90 + i)
+        k, v = _rand((T, 8, 128), 93 + i, 0.09), _rand((T, 8, 128), 96 + i, 0.09)
+        out = rt.prefill_chunk(q.cuda(), k.cuda(), v.cuda())
+        ids_or, o_ref = ob.prefill_chunk(to_np(q), to_np(k), to_np(v))
+        _sync(rt, ob, layout == "token")
+        assert rt.last_prefill_block_ids.tolist() == ids_or.tolist()
+        worst = assert_close_bf16(to_np(out), o_ref, **tol)
+        print(f"  max |err| {worst:.3e}", flush=True)
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "wide"])
 @pytest.mark.parametrize("lossless", [False, True])
-def test_verify_through_mfma_kernel_with_rotated_ring(lossless):
-    """Verify chunks routed to the matrix-core kernel after decode steps rotated the ring."""
-    rt, ob = _pair(8192 + 128, top_k_blocks=16, mfma_chunk_min_tokens=1)
+def test_verify_with_rotated_ring(lossless, kernel):
+    """Verify chunks after decode steps rotated the ring, on the matrix-core
+    kernel (forced) and on the few-query kernel's wide form (the automatic
+    choice for 6 tokens x 4 heads)."""
+    rt, ob = _pair(8192 + 128, top_k_blocks=16, mfma_chunk_min_tokens=1 if kernel == "mfma" else None)
     k0, v0 = _rand((8192, 8, 128), 50, 0.09), _rand((8192, 8, 128), 51, 0.09)
     rt.prefill_first(None, k0.cuda(), v0.cuda())
     ob.store_kv(to_np(k0), to_np(v0), with_reps=False)
@@ -111,8 +141,8 @@ def test_verify_through_mfma_kernel_with_rotated_ring(lossless):
         out = rt.verify_tokens(q.cuda(), k.cuda(), v.cuda())
         ids_or, o_ref = ob.verify_tokens(to_np(q), to_np(k), to_np(v), lossless=lossless)
         assert rt.last_verify_block_ids.tolist() == ids_or.tolist()
-        worst = assert_close_bf16(to_np(out), o_ref, **PREFILL_TOL)
-        print(f"[verify mfma lossless={lossless}] round {rnd}: max |err| {worst:.3e}", flush=True)
+        worst = assert_close_bf16(to_np(out), o_ref, **(PREFILL_TOL if kernel == "mfma" else {}))
+        print(f"[verify {kernel} lossless={lossless}] round {rnd}: max |err| {worst:.3e}", flush=True)
         rt.commit_verified(accept)
         ob.commit_verified(accept)
 

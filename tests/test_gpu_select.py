@@ -182,6 +182,7 @@ def test_select_rejects_empty_history():
     (2, 6, 32, 29, 4000, 1),    # k_eff < k, few duplicates
     (1, 1, 8, 8, 100, 2),       # one query: the union is its sorted ids
     (2, 16, 256, 256, 9000, 3), # the largest supported union (4096 ids)
+    (2, 4, 64, 64, 12288, 4),   # ids up to the largest block id a selection returns
 ])
 def test_select_union_matches_unique_and_searchsorted(L, tq, k, k_eff, hi, seed):
     """nkv_select_union against the reference's host ops (m12_runtime.py:1057-1087):

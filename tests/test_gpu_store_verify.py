@@ -119,10 +119,11 @@ def test_small_chunks_exercise_recent_carry():
 @pytest.mark.parametrize("lossless", [False, True])
 @pytest.mark.parametrize("quant", [False, True])
 def test_verify_commit_rollback_then_decode(lossless, quant, kernel):
-    """6-token verify through the matrix-core kernel (the automatic choice: 24
-    query rows exceed one 16-row group) and through the few-query kernel."""
+    """6-token verify through the few-query kernel (the automatic choice: its
+    wide form takes the 24 query rows as one 32-row group) and through the
+    matrix-core kernel (forced with mfma_chunk_min_tokens=1)."""
     rt, ob = _pair(16384 + 64, quant_history=quant,
-                   mfma_chunk_min_tokens=None if kernel == "mfma" else 64)
+                   mfma_chunk_min_tokens=1 if kernel == "mfma" else None)
     k0, v0 = _rand((16384, 8, 128), 140, 0.09), _rand((16384, 8, 128), 141, 0.09)
     rt.prefill_first(None, k0.cuda(), v0.cuda())
     ob.store_kv(to_np(k0), to_np(v0), with_reps=False)

@@ -118,6 +118,8 @@ VERIFY_CASES = [
     (16, 16, 4, 5000, 2, 16, False, 31),   # G = 1, 2 queries
     (64, 4, 2, 6000, 8, 32, True, 32),     # G = 16: 8 queries = 128 rows, matrix cores, per-query masks
     (32, 16, 8, 4000, 5, 24, True, 33),    # G = 2, r = 8: 10 rows on the few-query kernel
+    (32, 4, 4, 5000, 3, 32, True, 34),     # G = 8: 24 rows, the few-query kernel's wide form
+    (32, 8, 2, 6000, 7, 20, False, 35),    # G = 4: 28 rows (wide), shared selection
 ]
 
 

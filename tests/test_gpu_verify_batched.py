@@ -33,13 +33,14 @@ def _close(a, b, rel, abs_tol):
 @pytest.mark.parametrize("lossless", [True, False])
 @pytest.mark.parametrize("quant", [False, True])
 def test_batched_verify_matches_per_layer(lossless, quant, kernel):
-    """Through the matrix-core kernel (the automatic choice for 6 tokens: the
-    union's -1 padding is passed over) and the few-query kernel (per-layer
-    masks through allowed_layer_stride, padding skipped per wavefront)."""
+    """Through the matrix-core kernel (forced with mfma_chunk_min_tokens=1:
+    the union's -1 padding is passed over) and the few-query kernel (the
+    automatic choice for 6 tokens, its wide 32-row form; per-layer masks
+    through allowed_layer_stride, padding skipped per wavefront)."""
     from nanokv_amd.sparse import M12Config, M12LayerRuntime, M12ModelRuntime
     L, T, tq = 3, 16384, 6
     cfg = M12Config(max_model_len=T + 64, quant_history=quant,
-                    mfma_chunk_min_tokens=None if kernel == "mfma" else 64)
+                    mfma_chunk_min_tokens=1 if kernel == "mfma" else None)
     # verify outputs (see the module docstring); decode is the few-query kernel
     v_tol = (2 * PREFILL_TOL["rel"], 2 * PREFILL_TOL["abs_tol"]) if kernel == "mfma" else (2.0 ** -7, 1e-6)
     model = M12ModelRuntime(L, cfg)

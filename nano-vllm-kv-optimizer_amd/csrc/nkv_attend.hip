@@ -483,10 +483,6 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
   constexpr int NCT = kWideRows / 16;   // MFMA column tiles
   constexpr bool kI8 = FMT != NKV_KV_BF16;
   constexpr int kQCopies = FMT == NKV_KV_INT8_CHANNEL ? 2 : 1;
-#ifndef NKV_WIDE_PREFETCH_K
-#define NKV_WIDE_PREFETCH_K 0
-#endif
-  constexpr bool kPrefetchK = NKV_WIDE_PREFETCH_K;
   // V tiles of the four waves (16 KiB each), reused for the cross-wave merge
   __shared__ __attribute__((aligned(16))) char s_v[kAttendWaves * kVTileBytes];
   // B operands: [copy][ct][s][lane] (copy 1: the K-scaled query of int8
@@ -596,12 +592,21 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
   };
 
   // The wave's segments sidx, sidx + nwaves, ... below `end`, all int8
-  // history (int8 tag) or all bf16.  K of the next segment is loaded while
-  // the current one's P.V runs (its registers are free once Q.K^T consumed
-  // them); V of a segment is loaded after its Q.K^T, overlapping the softmax.
-  // Returns the first index at or past `end`.
+  // history (int8 tag) or all bf16.  Returns the first index at or past end.
+  // Two forms, chosen by measurement on the 36-layer 16K verify round:
+  //   registers (bf16 history, int8 history): K, then V once Q.K^T has
+  //   consumed K (the registers hold one of them), V written to the LDS tile
+  //   (int8 widened exactly on the way); 374 vs 387 us for bf16.
+  //   direct copies (the bf16 sink / recent / chunk segments of int8
+  //   history): V goes global -> LDS without registers, issued with K, and
+  //   the next segment's K loads go out once Q.K^T is done; 317 vs 335 us
+  //   for int8.
   auto run_phase = [&](int sidx, int end, auto int8_tag) __attribute__((always_inline)) {
     constexpr bool int8_seg = decltype(int8_tag)::value;
+    constexpr bool reg_v = int8_seg || FMT == NKV_KV_BF16;
+    // the next segment's K loaded once Q.K^T is done (the copy form, whose V
+    // holds no registers; measured no gain for int8 history's register form)
+    constexpr bool prefetch_k = !reg_v;
     typedef typename std::conditional<int8_seg, uint2, uint4>::type KReg;
     const int qsel = (int8_seg && FMT == NKV_KV_INT8_CHANNEL) ? kQCopies - 1 : 0;
     KReg ka[4][4];
@@ -620,13 +625,29 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
         }
       }
     };
+    // bf16 V of segment g -> this wave's V tile: copy j puts key 4 j + lg,
+    // chunk ln' ^ 2 lg at lane ln' of its 1 KiB, i.e. chunk c of key k at
+    // j * 1024 + lg * 256 + ((c ^ 2 lg) << 4), the layout the transposing
+    // reads expect; rows past the segment read as zero (bounded descriptor)
+    auto copy_v = [&](const Seg& g) __attribute__((always_inline)) {
+      const stage::rsrc_words rv = stage::rsrc_of(g.vbase, static_cast<uint32_t>(g.len * g.rowb));
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        stage::lds_copy16(rv, my_v + j * 1024, (4 * j + lg) * g.rowb + ((ln ^ (2 * lg)) << 4));
+    };
     sidx = skip_empty(sidx, end);
     if (sidx >= end) return sidx;
     Seg g = make_seg<FMT>(p, layer, h, sidx);
-    if (kPrefetchK) load_k(g);
+    if constexpr (prefetch_k) load_k(g);
+    if constexpr (!reg_v) copy_v(g);
     while (true) {
       const int last = g.len - 1;
-      if (!kPrefetchK) load_k(g);
+      if constexpr (!prefetch_k) load_k(g);
+      // the next segment (its id is a scalar load, in flight with K)
+      const int snext = skip_empty(sidx + nwaves, end);
+      const bool more = snext < end;
+      Seg gn = g;
+      if (more) gn = make_seg<FMT>(p, layer, h, snext);
       // ---- S^T = K . Q^T on the matrix cores ---------------------------------
       f32x4 c[4][NCT];
 #pragma unroll
@@ -649,19 +670,25 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
           for (int ct = 0; ct < NCT; ++ct) c[i][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bq[ct], c[i][ct], 0, 0, 0);
         }
       }
-      // V after the products: lane (lg, ln) loads dims [8 ln, +8) of key 4 j + lg
       __builtin_amdgcn_sched_barrier(0);
-      uint4 va[16];
+      // register form: V after the products (lane (lg, ln): dims [8 ln, +8)
+      // of key 4 j + lg)
+      uint4 va[reg_v ? 16 : 1];
       if constexpr (int8_seg) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           const uint2 r = kv_load8<false>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 8);
           va[j] = make_uint4(r.x, r.y, 0u, 0u);
         }
-      } else {
+      } else if constexpr (reg_v) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) va[j] = kv_load16<false>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 16);
       }
+      // the next segment's K, issued after this segment's V
+      if constexpr (prefetch_k) {
+        if (more) load_k(gn);
+      }
+      __builtin_amdgcn_sched_barrier(0);
 
       // ---- masking, scale, online softmax per column tile ------------------
       // c[i][ct][e]: key 16 i + 4 lg + e, row 16 ct + ln
@@ -745,28 +772,25 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
         m_run[ct] = m_new;
       }
 
-      // ---- V to LDS, the next segment's K loads, O^T += V^T . P^T ----------
+      // ---- V in the LDS tile, O^T += V^T . P^T -------------------------------
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) oacc[dt][ct] *= alpha[ct];
+      if constexpr (reg_v) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint4 vb = int8_seg ? i8x8_to_bf16x8(va[j].x, va[j].y) : va[j];
-        *reinterpret_cast<uint4*>(my_v + j * 1024 + vw) = vb;
+        for (int j = 0; j < 16; ++j)
+          *reinterpret_cast<uint4*>(my_v + j * 1024 + vw) = int8_seg ? i8x8_to_bf16x8(va[j].x, va[j].y) : va[j];
+        wave_lds_sync();
+      } else {
+        // the V copies have landed: they were issued before the next K loads
+        // (16 loads), which may stay in flight
+        if (more)
+          __builtin_amdgcn_s_waitcnt(0x4F70);   // vmcnt(16)
+        else
+          __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+        __builtin_amdgcn_wave_barrier();
       }
-      wave_lds_sync();
-      // (the scheduling barrier keeps the next K loads after the V stores, so
-      // the two register sets are never live together)
-      __builtin_amdgcn_sched_barrier(0);
-      const int snext = skip_empty(sidx + nwaves, end);
-      const bool more = snext < end;
-      Seg gn = g;
-      if (more) {
-        gn = make_seg<FMT>(p, layer, h, snext);
-        if (kPrefetchK) load_k(gn);
-      }
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2) {
         bf16x8 bp[NCT], bl[NCT];
@@ -797,10 +821,11 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
           }
         }
       }
-      wave_lds_sync();   // the next segment overwrites the V tile
+      wave_lds_sync();   // every read of the V tile is done before it is refilled
       if (!more) return snext;
       sidx = snext;
       g = gn;
+      if constexpr (!reg_v) copy_v(g);
     }
   };
   int sidx = split * kAttendWaves + wave;

@@ -59,6 +59,57 @@ __device__ __forceinline__ void dma_segment(const Seg& g, char* buf, int wave, i
   }
 }
 
+// Raw buffer descriptor words of bytes [base, base + bytes): reads at or past
+// `bytes` return zero.
+// The words are read from the first active lane: they are uniform by
+// construction, and the copy's descriptor operand must sit in SGPRs.
+typedef uint32_t rsrc_words __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ rsrc_words rsrc_of(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  auto uni = [](uint32_t x) { return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x))); };
+  return rsrc_words{uni(static_cast<uint32_t>(a)), uni(static_cast<uint32_t>(a >> 32) & 0xffffu), uni(bytes),
+                    static_cast<uint32_t>(kRsrcWord3)};
+}
+
+// One global -> LDS copy, 16 bytes a lane (buffer_load_dwordx4 ... lds): lane
+// u's bytes at `voffset` of the buffer land at LDS address lds + 16 u.  Issued
+// as inline assembly, so that the compiler (which counts such copies against
+// all of LDS) adds no waits of its own: the kernels order them with explicit
+// vmcnt waits.  The memory clobber keeps every LDS access on its side of the
+// copy.  M0 (the LDS base, read when the copy issues) is restored after it;
+// the s_nops cover the descriptor-write and M0-write hazards.
+__device__ __forceinline__ void lds_copy16(rsrc_words rsrc, const char* lds, int voffset) {
+  const uint32_t m0 = static_cast<uint32_t>(
+      __builtin_amdgcn_readfirstlane(static_cast<int>(reinterpret_cast<uintptr_t>((lds_void*)lds))));
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_nop 4\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(m0), "v"(voffset), "s"(rsrc)
+      : "memory");
+}
+// The same, 4 bytes a lane (buffer_load_dword ... lds): lane u lands at lds + 4 u.
+__device__ __forceinline__ void lds_copy4(rsrc_words rsrc, const char* lds, int voffset) {
+  const uint32_t m0 = static_cast<uint32_t>(
+      __builtin_amdgcn_readfirstlane(static_cast<int>(reinterpret_cast<uintptr_t>((lds_void*)lds))));
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_nop 4\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dword %2, %3, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(m0), "v"(voffset), "s"(rsrc)
+      : "memory");
+}
+
 // +inf when d <= 0 (key visible), -inf when d > 0: min(S, bound) masks S
 // without lane masks (no SGPR pairs).
 __device__ __forceinline__ float vis_bound(int d) {

@@ -398,6 +398,8 @@ def bench_verify(args, dev):
     L, T0, tq = args.layers, args.context, args.verify_tokens
     quant = args.kv_format != "bf16"
     extra = {} if args.mfma_chunk_min is None else {"mfma_chunk_min_tokens": args.mfma_chunk_min}
+    if args.splits is not None:
+        extra["attend_splits"] = args.splits
     cfg = M12Config(max_model_len=T0 + 64, top_k_blocks=args.top_k, quant_history=quant,
                     quant_scale_layout="token" if args.kv_format == "int8_token" else "channel_block",
                     **extra)

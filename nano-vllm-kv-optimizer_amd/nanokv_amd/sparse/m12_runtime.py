@@ -31,7 +31,7 @@ from time import perf_counter
 import torch
 
 from .. import _lib
-from ..store import SparseKVStore, packed_attention, query_summaries, tile_summaries
+from ..store import SparseKVStore, current_stream_ptr, packed_attention, query_summaries, tile_summaries
 
 # Query rows per group of the few-query kernels: one 16-column MFMA tile, or
 # two (the wide kernel) once a chunk's rows exceed one tile.
@@ -1492,7 +1492,7 @@ class M12ModelRuntime:
         cfg, core = self.cfg, self.core
         prot, n_prot = core.protected_dev()
         dev = self.store.device
-        cur = torch.cuda.current_stream(dev).cuda_stream
+        cur = current_stream_ptr(dev)
         key = (nb, core._prot_key, w["sink_len"], w["rec_len"] > 0, cur, cfg.top_k_blocks, cfg.decode_top_k_blocks,
                cfg.attend_splits, cfg.scale)
         plan = getattr(self, "_plan", None)

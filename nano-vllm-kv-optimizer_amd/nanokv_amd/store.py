@@ -43,8 +43,20 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def current_stream_ptr(device=None) -> int:
+    """Raw handle of the current stream of `device` (default: the current
+    device), without building a torch Stream object on every launch."""
+    if _raw_stream is not None:
+        idx = None if device is None else torch.device(device).index
+        return _raw_stream(torch.cuda.current_device() if idx is None else idx)
+    return torch.cuda.current_stream(device).cuda_stream
+
+
 def _stream():
-    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return ctypes.c_void_p(current_stream_ptr())
 
 
 class SparseKVStore:

@@ -159,3 +159,47 @@ def test_verify_sweep_against_oracle(hq, hkv, r, T, tq, top_k, lossless, seed):
     ids_or, _, o_ref = ob.decode(to_np(q), to_np(kn), to_np(vn))
     assert rt.last_block_ids.tolist() == ids_or.tolist()
     assert_close_bf16(to_np(out), o_ref)
+
+
+# (Hq, Hkv, history T, draft tokens, lossless, force the few-query kernels,
+# seed): verify shapes on the wide few-query kernel (two 16-column MFMA tiles
+# per group of up to 32 query rows) beyond the Qwen3-4B shape
+WIDE_CASES = [
+    (16, 16, 3000, 16, True, False, 51),   # G = 1: 16 rows, one tile (the 16-row kernel)
+    (16, 16, 3000, 20, False, False, 52),  # G = 1: 20 rows, one wide group, shared selection
+    (32, 16, 3500, 12, True, False, 53),   # G = 2: 24 rows, per-query masks
+    (64, 4, 2500, 2, True, False, 54),     # G = 16: 32 rows, a full wide group
+    (64, 4, 2500, 3, False, True, 55),     # G = 16: 48 rows, two wide groups (32 + 16), forced
+    (32, 32, 2000, 40, False, True, 56),   # G = 1: 40 rows, two wide groups (32 + 8), forced
+]
+
+
+@pytest.mark.parametrize("hq,hkv,T,tq,lossless,force,seed", WIDE_CASES)
+def test_verify_wide_kernel_shapes_against_oracle(hq, hkv, T, tq, lossless, force, seed):
+    """Verify rounds whose query rows take the wide few-query kernel (or, where
+    noted, are forced onto the few-query kernels), against the oracle: ids
+    bit-exact, outputs within the bf16 bar (fp32-accurate P.V)."""
+    from nanokv_amd.sparse import M12Config, M12LayerRuntime
+
+    print(f"case Hq={hq} Hkv={hkv} T={T} tq={tq} lossless={lossless} force={force}", flush=True)
+    top_k = 16
+    cfg = M12Config(max_model_len=T + 64, num_heads=hq, num_kv_heads=hkv, top_k_blocks=top_k,
+                    mfma_chunk_min_tokens=10000 if force else None)
+    rt = M12LayerRuntime(0, cfg)
+    ob = O.M12Oracle(O.OracleConfig(num_heads=hq, num_kv_heads=hkv, top_k_blocks=top_k))
+    g = torch.Generator().manual_seed(seed)
+    k = (torch.randn(T, hkv, D, generator=g) * 0.09).bfloat16()
+    v = (torch.randn(T, hkv, D, generator=g) * 0.09).bfloat16()
+    rt.prefill_first(None, k.cuda(), v.cuda())
+    ob.store_kv(to_np(k), to_np(v), with_reps=False)
+    nb = rt.nblocks_filled
+    ob.reps[:, :nb] = to_np(rt.reps_gpu[:, :nb])
+    rt.verify_lossless = lossless
+    q = torch.randn(tq, hq, D, generator=g).bfloat16()
+    kc = (torch.randn(tq, hkv, D, generator=g) * 0.09).bfloat16()
+    vc = (torch.randn(tq, hkv, D, generator=g) * 0.09).bfloat16()
+    out = rt.verify_tokens(q.cuda(), kc.cuda(), vc.cuda())
+    ids_or, o_ref = ob.verify_tokens(to_np(q), to_np(kc), to_np(vc), lossless=lossless)
+    assert rt.last_verify_block_ids.tolist() == ids_or.tolist()
+    worst = assert_close_bf16(to_np(out), o_ref)
+    print(f"  max |err| {worst:.2e}", flush=True)

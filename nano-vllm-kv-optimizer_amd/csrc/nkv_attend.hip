@@ -594,13 +594,14 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
   // The wave's segments sidx, sidx + nwaves, ... below `end`, all int8
   // history (int8 tag) or all bf16.  Returns the first index at or past end.
   // Two forms, chosen by measurement on the 36-layer 16K verify round:
-  //   registers (bf16 history, int8 history): K, then V once Q.K^T has
-  //   consumed K (the registers hold one of them), V written to the LDS tile
-  //   (int8 widened exactly on the way); 374 vs 387 us for bf16.
+  //   registers (bf16 history, int8 history): bf16 K, then V once Q.K^T has
+  //   consumed K (the registers hold one of them; 374 vs 387 us); int8 K and
+  //   V (8 bytes a lane and row) together.  V is written to the LDS tile
+  //   (int8 widened exactly on the way).
   //   direct copies (the bf16 sink / recent / chunk segments of int8
   //   history): V goes global -> LDS without registers, issued with K, and
-  //   the next segment's K loads go out once Q.K^T is done; 317 vs 335 us
-  //   for int8.
+  //   the next segment's K loads go out once Q.K^T is done (per-token int8
+  //   324 vs 338 us).
   auto run_phase = [&](int sidx, int end, auto int8_tag) __attribute__((always_inline)) {
     constexpr bool int8_seg = decltype(int8_tag)::value;
     constexpr bool reg_v = int8_seg || FMT == NKV_KV_BF16;
@@ -643,6 +644,13 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
     while (true) {
       const int last = g.len - 1;
       if constexpr (!prefetch_k) load_k(g);
+      // int8 history: V (8 bytes a lane and key row, 32 registers) goes out
+      // with K, so the segment's 16 KiB are in flight together
+      uint2 va8[int8_seg ? 16 : 1];
+      if constexpr (int8_seg) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) va8[j] = kv_load8<false>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 8);
+      }
       // the next segment (its id is a scalar load, in flight with K)
       const int snext = skip_empty(sidx + nwaves, end);
       const bool more = snext < end;
@@ -671,16 +679,10 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      // register form: V after the products (lane (lg, ln): dims [8 ln, +8)
-      // of key 4 j + lg)
-      uint4 va[reg_v ? 16 : 1];
-      if constexpr (int8_seg) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const uint2 r = kv_load8<false>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 8);
-          va[j] = make_uint4(r.x, r.y, 0u, 0u);
-        }
-      } else if constexpr (reg_v) {
+      // register form, bf16: V after the products (lane (lg, ln): dims
+      // [8 ln, +8) of key 4 j + lg)
+      uint4 va[reg_v && !int8_seg ? 16 : 1];
+      if constexpr (reg_v && !int8_seg) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) va[j] = kv_load16<false>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 16);
       }
@@ -780,7 +782,7 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
       if constexpr (reg_v) {
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-          *reinterpret_cast<uint4*>(my_v + j * 1024 + vw) = int8_seg ? i8x8_to_bf16x8(va[j].x, va[j].y) : va[j];
+          *reinterpret_cast<uint4*>(my_v + j * 1024 + vw) = int8_seg ? i8x8_to_bf16x8(va8[j].x, va8[j].y) : va[j];
         wave_lds_sync();
       } else {
         // the V copies have landed: they were issued before the next K loads

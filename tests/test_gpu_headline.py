@@ -61,3 +61,65 @@ def test_headline_36_layer_32k_step_matches_oracle(quant, splits_expected, rel, 
             worst = max(worst, assert_close_bf16(to_np(out[i]), o_ref, rel=rel, abs_tol=abs_tol))
     print(f"[headline 36L x 32K {'int8' if quant else 'bf16'}, {splits_expected} splits] "
           f"max |err| {worst:.3e}", flush=True)
+
+
+TV, TQ = 16384, 6
+
+
+@pytest.mark.parametrize("quant,rel,abs_tol", [
+    (False, 2.0 ** -7, 2e-5),
+    (True, 2.0 ** -6, 2e-4),
+])
+def test_verify_36_layer_16k_round_matches_oracle(quant, rel, abs_tol):
+    """The launch the verify benchmark times: M12ModelRuntime.verify(lossless)
+    over 36 layers of 16384-token histories, 6 draft tokens, the automatic
+    kernel choice (the wide few-query kernel, 5 splits), the benchmark's
+    histories (same seeds) and draft tokens of its shapes.  On four sampled
+    layers the union of the per-query selections must
+    equal the oracle's and the outputs must match the fp64 oracle
+    (m12_runtime.py:656-758, :1057-1087); then a commit and a decode step."""
+    from nanokv_amd import workload
+    from nanokv_amd.sparse import M12Config, M12ModelRuntime
+
+    dev = torch.device("cuda:0")
+    cfg = M12Config(max_model_len=TV + 64, top_k_blocks=32, quant_history=quant)
+    model = M12ModelRuntime(L, cfg, device=dev)
+    kh = torch.empty(L, TV, 8, 128, dtype=torch.bfloat16, device=dev)
+    vh = torch.empty_like(kh)
+    for i in range(L):
+        k, v, _, _ = workload.history(TV, SEED + i, device=dev)
+        kh[i].copy_(k)
+        vh[i].copy_(v)
+    model.prefill(kh, vh)
+    nb = model.nblocks_filled
+    assert nb == 256
+    oracles = {}
+    for i in SAMPLED:
+        ob = O.M12Oracle(O.OracleConfig(quant_history=quant))
+        ob.store_kv(to_np(kh[i]), to_np(vh[i]), with_reps=False)
+        ob.reps[:, :nb] = to_np(model.store.reps[i, :, :nb])
+        oracles[i] = ob
+    del kh, vh
+    g = torch.Generator(device=dev).manual_seed(SEED + 31)
+    q = torch.randn(L, TQ, 32, 128, generator=g, device=dev).to(torch.bfloat16)
+    k = (torch.randn(L, TQ, 8, 128, generator=g, device=dev) * 128 ** -0.5).to(torch.bfloat16)
+    v = (torch.randn(L, TQ, 8, 128, generator=g, device=dev) * 128 ** -0.5).to(torch.bfloat16)
+    out = model.verify(q, k, v, lossless=True)
+    union = model.last_union_dev.cpu()
+    count = model.last_union_count_dev.cpu()
+    worst = 0.0
+    for i, ob in oracles.items():
+        ids_or, o_ref = ob.verify_tokens(to_np(q[i]), to_np(k[i]), to_np(v[i]), lossless=True)
+        assert union[i, :int(count[i])].tolist() == ids_or.tolist(), f"layer {i}: union differs"
+        worst = max(worst, assert_close_bf16(to_np(out[i]), o_ref, rel=rel, abs_tol=abs_tol))
+    # accept 4 of the 6 tokens, then one decode step sees them in its window
+    model.commit_verified(4)
+    qs, ks, vs = workload.decode_inputs(1, SEED, device=dev, layers=L)
+    out = model.decode(qs[0], ks[0], vs[0])
+    ids = model.last_ids_dev[:, 0, :model.last_n_selected].cpu()
+    for i, ob in oracles.items():
+        ob.commit_verified(4)
+        ids_or, _, o_ref = ob.decode(to_np(qs[0, i]), to_np(ks[0, i]), to_np(vs[0, i]))
+        assert ids[i].tolist() == ids_or.tolist(), f"decode after verify, layer {i}: ids differ"
+        worst = max(worst, assert_close_bf16(to_np(out[i]), o_ref, rel=rel, abs_tol=abs_tol))
+    print(f"[verify 36L x 16K {'int8' if quant else 'bf16'}] max |err| {worst:.3e}", flush=True)

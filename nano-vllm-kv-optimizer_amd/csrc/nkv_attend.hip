@@ -126,23 +126,39 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
   const int my_t = q0 + (row_ok ? my_row / p.G : 0);
   const int my_hq = h * p.G + (my_row % p.G);
   bf16x8 bq[4], bqs[4];
+  // every load first (the query row, and for per-channel int8 the K scales
+  // of this lane's dims), then the scaled operands: a conversion between
+  // them would make each load a round trip of its own
+  uint4 qv[4];
+  float4 ksc[4][2];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const int d0 = s * 32 + lg * 8;
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    qv[s] = make_uint4(0u, 0u, 0u, 0u);
     if (row_ok) {
-      v = *reinterpret_cast<const uint4*>(
+      qv[s] = *reinterpret_cast<const uint4*>(
           p.q + p.q_ls * layer + (static_cast<int64_t>(my_t) * hq + my_hq) * kHeadDim + d0);
     }
+    if (FMT == NKV_KV_INT8_CHANNEL) {
+      const float4* ks = reinterpret_cast<const float4*>(
+          p.k_scale + static_cast<int64_t>(layer) * p.hkv * kHeadDim + h * kHeadDim + d0);
+      ksc[s][0] = ks[0];
+      ksc[s][1] = ks[1];
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const uint4 v = qv[s];
     bq[s] = as_bf16x8(v);
     if (FMT == NKV_KV_INT8_CHANNEL) {
-      const float* ks = p.k_scale + static_cast<int64_t>(layer) * p.hkv * kHeadDim + h * kHeadDim + d0;
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      const float sc[8] = {ksc[s][0].x, ksc[s][0].y, ksc[s][0].z, ksc[s][0].w,
+                           ksc[s][1].x, ksc[s][1].y, ksc[s][1].z, ksc[s][1].w};
       uint32_t o[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float a = bf16_lo(w[i]) * ks[2 * i];
-        const float b = bf16_hi(w[i]) * ks[2 * i + 1];
+        const float a = bf16_lo(w[i]) * sc[2 * i];
+        const float b = bf16_hi(w[i]) * sc[2 * i + 1];
         o[i] = static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
       }
       bqs[s] = as_bf16x8(make_uint4(o[0], o[1], o[2], o[3]));
@@ -175,12 +191,21 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
   for (int q4 = 0; q4 < 4; ++q4)
     vtr[q4] = (4 * lg + (ln >> 2)) * 256 + ((2 * (q4 ^ (ln >> 2)) + ((ln & 3) >> 1)) << 4) + 8 * (ln & 1);
   const int nwaves = p.splits * kAttendWaves;
-  // One segment of this wavefront.  int8 history segments (always the first
-  // n_hist segments) and bf16 segments are two instantiations of the body, run
-  // by two loops in segment order, so neither carries the other's registers.
-  auto segment = [&](const int sidx, auto int8_tag) __attribute__((always_inline)) {
+  // History block ids are read through the constant address space (scalar
+  // loads, counted by lgkmcnt), each one segment ahead: a vector load of the
+  // id would be waited for with vmcnt(0) before the segment's K / V loads
+  // could issue, one dependent round trip per segment.
+  typedef __attribute__((address_space(4))) const int32_t cint32;
+  typedef __attribute__((address_space(4))) const float cfloat;
+  const cint32* ids_l = (const cint32*)(p.ids + static_cast<int64_t>(layer) * p.ids_ls);
+  auto id_at = [&](int s) { return s < p.n_hist ? ids_l[s] : 0; };
+  // One segment of this wavefront (blk: its block id, for history segments).
+  // int8 history segments (always the first n_hist segments) and bf16
+  // segments are two instantiations of the body, run by two loops in segment
+  // order, so neither carries the other's registers.
+  auto segment = [&](const int sidx, const int blk, auto int8_tag) __attribute__((always_inline)) {
     constexpr bool int8_seg = decltype(int8_tag)::value;
-    const Seg g = make_seg<FMT>(p, layer, h, sidx);
+    const Seg g = make_seg_blk<FMT>(p, layer, h, sidx, blk);
     // an id outside the history attends nothing: no loads (a fully masked
     // segment would leave m, l and acc exactly as they are)
     if (g.type == kSegHist && g.vlen == 0) return;
@@ -200,6 +225,11 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
     constexpr bool kStream = (M == 4 && FMT == NKV_KV_BF16);
     f32x4 c[4];
     uint4 va[16];
+    // int8 history: the block's V scale (per-channel form, one scalar load)
+    // or the fp16 K and V scales of this lane's keys 16 i + 4 lg .. + 3
+    // (per-token form, 8-byte loads), issued with K and V
+    float vs_blk = 1.0f;
+    uint2 kts[4], vts[4];
     auto load_v = [&]() __attribute__((always_inline)) {
       if (int8_seg) {
 #pragma unroll
@@ -222,6 +252,16 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
         for (int s = 0; s < 4; ++s) ka[i][s] = kv_load8<kStream>(rp + s * 32);
       }
       if (kVEarly) load_v();
+      if (FMT == NKV_KV_INT8_CHANNEL)
+        vs_blk = ((const cfloat*)p.v_scale)[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap + g.blk];
+      if (FMT == NKV_KV_INT8_TOKEN) {
+        const int64_t tb = ((static_cast<int64_t>(layer) * p.hkv + h) * p.cap + g.blk) * kBlock + 4 * lg;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          kts[i] = *reinterpret_cast<const uint2*>(p.k_tscale + tb + 16 * i);
+          vts[i] = *reinterpret_cast<const uint2*>(p.v_tscale + tb + 16 * i);
+        }
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         c[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -282,9 +322,10 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
             ok = ok && (g.off + tk) <= my_t;
           }
         }
-        if (FMT == NKV_KV_INT8_TOKEN && int8_seg)
-          v *= f16_bits_to_f32(p.k_tscale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap * kBlock +
-                                          static_cast<int64_t>(g.blk) * kBlock + tk]);
+        if (FMT == NKV_KV_INT8_TOKEN && int8_seg) {
+          const uint32_t w = e < 2 ? kts[i].x : kts[i].y;
+          v *= f16_bits_to_f32(static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu)));
+        }
         v = ok ? v * p.scale_log2 : -INFINITY;
         x[i][e] = v;
         cmax = fmaxf(cmax, v);
@@ -294,9 +335,6 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
     cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
     const float m_new = fmaxf(m_run, cmax);
     const float alpha = (m_new == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-    float vs_blk = 1.0f;
-    if (FMT == NKV_KV_INT8_CHANNEL && int8_seg)
-      vs_blk = p.v_scale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap + g.blk];
     float lsum = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -306,9 +344,10 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
         const float pe = (x[i][e] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(x[i][e] - m_new);
         lsum += pe;
         float pv = pe * vs_blk;
-        if (FMT == NKV_KV_INT8_TOKEN && int8_seg)
-          pv *= f16_bits_to_f32(p.v_tscale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap * kBlock +
-                                           static_cast<int64_t>(g.blk) * kBlock + tk]);
+        if (FMT == NKV_KV_INT8_TOKEN && int8_seg) {
+          const uint32_t w = e < 2 ? vts[i].x : vts[i].y;
+          pv *= f16_bits_to_f32(static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu)));
+        }
         if (kMfmaPV)
           x[i][e] = pv;
         else
@@ -397,9 +436,18 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
     wave_lds_sync();
   };
   int sidx = split * kAttendWaves + wave;
+  int blk = id_at(sidx);
   if (FMT != NKV_KV_BF16)
-    for (; sidx < p.n_hist; sidx += nwaves) segment(sidx, std::true_type{});
-  for (; sidx < p.nseg; sidx += nwaves) segment(sidx, std::false_type{});
+    for (; sidx < p.n_hist; sidx += nwaves) {
+      const int nb = id_at(sidx + nwaves);   // in flight while this segment is attended
+      segment(sidx, blk, std::true_type{});
+      blk = nb;
+    }
+  for (; sidx < p.nseg; sidx += nwaves) {
+    const int nb = id_at(sidx + nwaves);
+    segment(sidx, blk, std::false_type{});
+    blk = nb;
+  }
 
   // ---- reduce the wave's state across lane groups --------------------------
   l_run += __shfl_xor(l_run, 16);
@@ -582,9 +630,15 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
 
   // A history segment whose id lies outside the history attends nothing (a
   // fully masked segment would leave m, l and acc as they are): passed over.
+  // The ids are read through the constant address space (scalar loads,
+  // counted by lgkmcnt): a vector load would be waited for with vmcnt(0),
+  // draining the current segment's loads with it.
+  typedef __attribute__((address_space(4))) const int32_t cint32;
+  typedef __attribute__((address_space(4))) const float cfloat;
+  const cint32* ids_l = (const cint32*)(p.ids + static_cast<int64_t>(layer) * p.ids_ls);
   auto skip_empty = [&](int sidx, int end) {
     while (sidx < end && sidx < p.n_hist) {
-      const int blk = p.ids[static_cast<int64_t>(layer) * p.ids_ls + sidx];
+      const int blk = ids_l[sidx];
       if (blk >= 0 && blk < p.cap) break;
       sidx += nwaves;
     }
@@ -645,11 +699,34 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
       const int last = g.len - 1;
       if constexpr (!prefetch_k) load_k(g);
       // int8 history: V (8 bytes a lane and key row, 32 registers) goes out
-      // with K, so the segment's 16 KiB are in flight together
+      // with K, so the segment's 16 KiB are in flight together, and so do the
+      // block's V scale (per-channel form, a scalar load) or the fp16 K and V
+      // scales of this lane's keys 16 i + 4 lg .. + 3 (per-token form)
       uint2 va8[int8_seg ? 16 : 1];
+      float vs_blk = 1.0f;
+      uint2 kts[4], vts[4];
       if constexpr (int8_seg) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) va8[j] = kv_load8<false>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 8);
+        if (FMT == NKV_KV_INT8_CHANNEL)
+          vs_blk = ((const cfloat*)p.v_scale)[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap + g.blk];
+        if (FMT == NKV_KV_INT8_TOKEN) {
+          const int64_t tb = ((static_cast<int64_t>(layer) * p.hkv + h) * p.cap + g.blk) * kBlock + 4 * lg;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            kts[i] = *reinterpret_cast<const uint2*>(p.k_tscale + tb + 16 * i);
+            vts[i] = *reinterpret_cast<const uint2*>(p.v_tscale + tb + 16 * i);
+          }
+        }
+      }
+      // per-query history flags of this segment (verify's union), loaded
+      // before the products so their wait is the loads' own
+      int hidden[NCT];
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        hidden[ct] = 0;
+        if (g.type == kSegHist && p.allowed != nullptr)
+          hidden[ct] = p.allowed[p.allowed_ls * layer + static_cast<int64_t>(my_t[ct]) * p.n_hist + g.u] == 0;
       }
       // the next segment (its id is a scalar load, in flight with K)
       const int snext = skip_empty(sidx + nwaves, end);
@@ -694,9 +771,6 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
 
       // ---- masking, scale, online softmax per column tile ------------------
       // c[i][ct][e]: key 16 i + 4 lg + e, row 16 ct + ln
-      float vs_blk = 1.0f;
-      if (FMT == NKV_KV_INT8_CHANNEL && int8_seg)
-        vs_blk = p.v_scale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap + g.blk];
       // Visibility, branch-free: key tk of the segment is visible to column
       // tile ct iff d = 4 lg + (16 i + e) - thr[ct] <= 0, where thr[ct] is the
       // last visible key (-1: none; the row's validity, the per-query history
@@ -707,9 +781,7 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
       for (int ct = 0; ct < NCT; ++ct) {
         int thr = g.vlen - 1;
         if (g.type == kSegChunk) thr = min(thr, my_t[ct] - g.off);
-        if (g.type == kSegHist && p.allowed != nullptr &&
-            p.allowed[p.allowed_ls * layer + static_cast<int64_t>(my_t[ct]) * p.n_hist + g.u] == 0)
-          thr = -1;
+        if (hidden[ct]) thr = -1;
         if (!row_ok[ct]) thr = -1;
         base[ct] = 4 * lg - thr;
       }
@@ -720,15 +792,11 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
         ra = (g.off - ring_base - p.rec_lo) % p.R;
         ra = ra < 0 ? ra + p.R : ra;
       }
-      float ktsc[4][4];
-      if constexpr (FMT == NKV_KV_INT8_TOKEN && int8_seg) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            ktsc[i][e] = f16_bits_to_f32(p.k_tscale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap * kBlock +
-                                                    static_cast<int64_t>(g.blk) * kBlock + i * 16 + lg * 4 + e]);
-      }
+      // fp16 scale of key 16 i + 4 lg + e from a lane's 8-byte load
+      auto tscale = [](const uint2 (&w)[4], int i, int e) {
+        const uint32_t x = e < 2 ? w[i].x : w[i].y;
+        return f16_bits_to_f32(static_cast<uint16_t>((e & 1) ? (x >> 16) : (x & 0xffffu)));
+      };
       float alpha[NCT];
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) {
@@ -744,7 +812,7 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
               ok = ok && x < p.rec_len;
             }
             float v = c[i][ct][e];
-            if constexpr (FMT == NKV_KV_INT8_TOKEN && int8_seg) v *= ktsc[i][e];
+            if constexpr (FMT == NKV_KV_INT8_TOKEN && int8_seg) v *= tscale(kts, i, e);
             v = ok ? v * p.scale_log2 : -INFINITY;
             c[i][ct][e] = v;
             cmax = fmaxf(cmax, v);
@@ -759,14 +827,11 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
         for (int i = 0; i < 4; ++i) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int tk = i * 16 + lg * 4 + e;
             const float x = c[i][ct][e];
             const float pe = (x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(x - m_new);
             lsum += pe;
             float pv = pe * vs_blk;
-            if (FMT == NKV_KV_INT8_TOKEN && int8_seg)
-              pv *= f16_bits_to_f32(p.v_tscale[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap * kBlock +
-                                               static_cast<int64_t>(g.blk) * kBlock + tk]);
+            if (FMT == NKV_KV_INT8_TOKEN && int8_seg) pv *= tscale(vts, i, e);
             c[i][ct][e] = pv;
           }
         }

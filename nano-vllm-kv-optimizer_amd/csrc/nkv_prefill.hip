@@ -535,8 +535,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
 
   // this tile's selected history blocks (per-query-tile selection: the ids
   // of the selection tile holding the workgroup's tokens)
-  const int32_t* ids_row = p.ids + static_cast<int64_t>(layer) * p.ids_ls +
-                           (p.sel_tile > 0 ? static_cast<int64_t>(t0 / p.sel_tile) * p.ids_tile_ls : 0);
+  // (read through the constant address space: scalar loads, counted by
+  // lgkmcnt -- a vector load here would be waited for with vmcnt(0) before
+  // the next segment's copies could issue)
+  typedef __attribute__((address_space(4))) const int32_t cint32;
+  const cint32* ids_row = (const cint32*)(p.ids + static_cast<int64_t>(layer) * p.ids_ls +
+                                          (p.sel_tile > 0 ? static_cast<int64_t>(t0 / p.sel_tile) * p.ids_tile_ls : 0));
   // the next segment at or after s that attends anything (its block id in
   // *blk): history ids outside [0, cap) (a union padded with -1) are passed
   // over, never staged

@@ -372,16 +372,17 @@ class _SparseCore:
         if self.cfg.attend_splits is not None:
             return self.cfg.attend_splits
         # Workgroups per launch measured best on the 36-layer 32K decode step
-        # (tok/s): bf16 ~1440 (5 splits 8850 vs 3 splits 8620), int8_token
-        # ~1440 (8770 vs 8660); per-block int8, whose segments carry half
-        # the bytes and no per-token scales, ~900 (3 splits 9040 vs 5
-        # splits 8730).  Never more than one segment per wavefront.
+        # (tok/s, splits 2 / 3 / 5 / 6 / 7 / 9): bf16 ~1440 (8382 / 8827 /
+        # 9261 / 9141 / 8992 / 8838); both int8 forms, whose segments carry
+        # half the bytes, ~900 (per-block 9434 / 10122 / 9792 / 9555 / 9347 /
+        # 8959, per-token 9378 / 9929 / 9831 / 9766 / 9615 / 9385).  Never
+        # more than one segment per wavefront.
         # Workgroups go round-robin over the 8 XCDs with the split index
         # fastest, so a split count with a factor 4 in common with 8 pins
         # the splits that carry an extra segment to the same XCDs (4 and 8
         # splits measured 5% and 14% slower than 5 in bf16): such counts
         # move up by one.
-        target = 900 if self.cfg.kv_format == "int8" else 1440
+        target = 1440 if self.cfg.kv_format == "bf16" else 900
         want = max(1, round(target / (self.store.num_kv_heads * self.nl * nqg)))
         cap = max(1, min(-(-nseg // 4), 64))
         s = min(want, cap)

@@ -57,7 +57,7 @@ def test_decode_split_choice():
     # 36 layers x 8 KV heads, top-32 + sink + 8 recent pieces = 41 segments
     assert _split_choice(41) == 5                              # ~1440 workgroups
     assert _split_choice(41, quant_history=True) == 3          # per-block int8: ~900
-    assert _split_choice(41, quant_history=True, quant_scale_layout="token") == 5
+    assert _split_choice(41, quant_history=True, quant_scale_layout="token") == 3   # per-token int8: ~900
     assert _split_choice(41, attend_splits=8) == 8             # explicit choice kept
     for layers in range(1, 80):
         for nseg in (1, 5, 16, 41, 300):

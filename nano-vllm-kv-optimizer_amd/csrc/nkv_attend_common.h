@@ -128,15 +128,19 @@ __device__ __forceinline__ float sum_over_rows(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// 8 signed bytes -> 8 bf16 (exact: |x| <= 127 has <= 7 significant bits).
+// 8 signed bytes -> 8 bf16 (exact: |x| <= 128 has <= 8 significant bits).
+// One byte-select conversion per value and one bf16 pack per pair
+// (v_cvt_f32_i32 with a sign-extended byte operand, v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint4 i8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t src = ((i < 2) ? lo : hi) >> ((i & 1) * 16);
     const float f0 = static_cast<float>(static_cast<int8_t>(src & 0xffu));
     const float f1 = static_cast<float>(static_cast<int8_t>((src >> 8) & 0xffu));
-    o[i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+    const bf16x2_t v = {static_cast<__bf16>(f0), static_cast<__bf16>(f1)};
+    o[i] = __builtin_bit_cast(uint32_t, v);
   }
   return make_uint4(o[0], o[1], o[2], o[3]);
 }

@@ -2,10 +2,11 @@
 
 M12ModelRuntime over 36 layers of 32768-token histories (512 blocks each)
 decodes through nkv_decode_step with the automatic attention split count
-(5 for bf16, 3 for the reference int8 scheme), the same seeds and inputs as
-bench.py's default line.  On four sampled layers the selected ids must equal
-the oracle's (value and order) and the outputs must match the fp64 oracle to
-about one bf16 ulp at every step (m12_runtime.py:1141-1346).
+(5 for bf16, 3 for either int8 scale layout), the same seeds and inputs as
+bench.py's default line and its int8 / int8_token lines.  On four sampled
+layers the selected ids must equal the oracle's (value and order) and the
+outputs must match the fp64 oracle to about one bf16 ulp at every step
+(m12_runtime.py:1141-1346).
 """
 
 import numpy as np
@@ -21,16 +22,39 @@ L, T, SEED, STEPS = 36, 32768, 2024, 3
 SAMPLED = (0, 13, 26, 35)
 
 
-@pytest.mark.parametrize("quant,splits_expected,rel,abs_tol", [
-    (False, 5, 2.0 ** -7, 2e-5),
-    (True, 3, 2.0 ** -6, 2e-4),
+def _oracle_for_layer(model, i, kh, vh, quant, layout):
+    """The oracle of layer i, holding the GPU's representatives.  For the
+    per-token fp16-scale layout it attends the dequantised history the GPU
+    stored, bf16(code * scale); the codes and scales themselves are checked
+    bit-exact against the oracle's quantiser by the single-layer per-token
+    decode test."""
+    st = model.store
+    nb = model.nblocks_filled
+    token = quant and layout == "token"
+    ob = O.M12Oracle(O.OracleConfig(quant_history=quant and not token))
+    ob.store_kv(to_np(kh[i]), to_np(vh[i]), with_reps=False)
+    ob.reps[:, :nb] = to_np(st.reps[i, :, :nb])
+    if token:
+        kq = st.hist_k[i, :, :nb].cpu().numpy().astype(np.float32)      # [H, nb, 64, D]
+        vq = st.hist_v[i, :, :nb].cpu().numpy().astype(np.float32)
+        ksc = st.k_tscale[i, :, :nb * 64].cpu().float().numpy().reshape(8, nb, 64, 1)
+        vsc = st.v_tscale[i, :, :nb * 64].cpu().float().numpy().reshape(8, nb, 64, 1)
+        ob.hist_k[:nb] = O.bf16_round(kq * ksc).transpose(1, 2, 0, 3)
+        ob.hist_v[:nb] = O.bf16_round(vq * vsc).transpose(1, 2, 0, 3)
+    return ob
+
+
+@pytest.mark.parametrize("quant,layout,splits_expected,rel,abs_tol", [
+    (False, "channel_block", 5, 2.0 ** -7, 2e-5),
+    (True, "channel_block", 3, 2.0 ** -6, 2e-4),
+    (True, "token", 3, 2.0 ** -6, 2e-4),
 ])
-def test_headline_36_layer_32k_step_matches_oracle(quant, splits_expected, rel, abs_tol):
+def test_headline_36_layer_32k_step_matches_oracle(quant, layout, splits_expected, rel, abs_tol):
     from nanokv_amd import workload
     from nanokv_amd.sparse import M12Config, M12ModelRuntime
 
     dev = torch.device("cuda:0")
-    cfg = M12Config(max_model_len=T, top_k_blocks=32, quant_history=quant)
+    cfg = M12Config(max_model_len=T, top_k_blocks=32, quant_history=quant, quant_scale_layout=layout)
     model = M12ModelRuntime(L, cfg, device=dev)
     kh = torch.empty(L, T, 8, 128, dtype=torch.bfloat16, device=dev)
     vh = torch.empty_like(kh)
@@ -41,12 +65,7 @@ def test_headline_36_layer_32k_step_matches_oracle(quant, splits_expected, rel, 
     model.prefill(kh, vh)
     nb = model.nblocks_filled
     assert nb == 512
-    oracles = {}
-    for i in SAMPLED:
-        ob = O.M12Oracle(O.OracleConfig(quant_history=quant))
-        ob.store_kv(to_np(kh[i]), to_np(vh[i]), with_reps=False)
-        ob.reps[:, :nb] = to_np(model.store.reps[i, :, :nb])
-        oracles[i] = ob
+    oracles = {i: _oracle_for_layer(model, i, kh, vh, quant, layout) for i in SAMPLED}
     del kh, vh
     n = model.core.effective_k(32)
     assert model.core.decode_splits(n) == splits_expected
@@ -59,18 +78,19 @@ def test_headline_36_layer_32k_step_matches_oracle(quant, splits_expected, rel, 
             ids_or, _, o_ref = ob.decode(to_np(qs[s, i]), to_np(ks[s, i]), to_np(vs[s, i]))
             assert ids[i].tolist() == ids_or.tolist(), f"step {s} layer {i}: ids differ"
             worst = max(worst, assert_close_bf16(to_np(out[i]), o_ref, rel=rel, abs_tol=abs_tol))
-    print(f"[headline 36L x 32K {'int8' if quant else 'bf16'}, {splits_expected} splits] "
+    print(f"[headline 36L x 32K {('int8 ' + layout) if quant else 'bf16'}, {splits_expected} splits] "
           f"max |err| {worst:.3e}", flush=True)
 
 
 TV, TQ = 16384, 6
 
 
-@pytest.mark.parametrize("quant,rel,abs_tol", [
-    (False, 2.0 ** -7, 2e-5),
-    (True, 2.0 ** -6, 2e-4),
+@pytest.mark.parametrize("quant,layout,rel,abs_tol", [
+    (False, "channel_block", 2.0 ** -7, 2e-5),
+    (True, "channel_block", 2.0 ** -6, 2e-4),
+    (True, "token", 2.0 ** -6, 2e-4),
 ])
-def test_verify_36_layer_16k_round_matches_oracle(quant, rel, abs_tol):
+def test_verify_36_layer_16k_round_matches_oracle(quant, layout, rel, abs_tol):
     """The launch the verify benchmark times: M12ModelRuntime.verify(lossless)
     over 36 layers of 16384-token histories, 6 draft tokens, the automatic
     kernel choice (the wide few-query kernel, 5 splits), the benchmark's
@@ -82,7 +102,8 @@ def test_verify_36_layer_16k_round_matches_oracle(quant, rel, abs_tol):
     from nanokv_amd.sparse import M12Config, M12ModelRuntime
 
     dev = torch.device("cuda:0")
-    cfg = M12Config(max_model_len=TV + 64, top_k_blocks=32, quant_history=quant)
+    cfg = M12Config(max_model_len=TV + 64, top_k_blocks=32, quant_history=quant,
+                    quant_scale_layout=layout)
     model = M12ModelRuntime(L, cfg, device=dev)
     kh = torch.empty(L, TV, 8, 128, dtype=torch.bfloat16, device=dev)
     vh = torch.empty_like(kh)
@@ -93,12 +114,7 @@ def test_verify_36_layer_16k_round_matches_oracle(quant, rel, abs_tol):
     model.prefill(kh, vh)
     nb = model.nblocks_filled
     assert nb == 256
-    oracles = {}
-    for i in SAMPLED:
-        ob = O.M12Oracle(O.OracleConfig(quant_history=quant))
-        ob.store_kv(to_np(kh[i]), to_np(vh[i]), with_reps=False)
-        ob.reps[:, :nb] = to_np(model.store.reps[i, :, :nb])
-        oracles[i] = ob
+    oracles = {i: _oracle_for_layer(model, i, kh, vh, quant, layout) for i in SAMPLED}
     del kh, vh
     g = torch.Generator(device=dev).manual_seed(SEED + 31)
     q = torch.randn(L, TQ, 32, 128, generator=g, device=dev).to(torch.bfloat16)
@@ -122,4 +138,4 @@ def test_verify_36_layer_16k_round_matches_oracle(quant, rel, abs_tol):
         ids_or, _, o_ref = ob.decode(to_np(qs[0, i]), to_np(ks[0, i]), to_np(vs[0, i]))
         assert ids[i].tolist() == ids_or.tolist(), f"decode after verify, layer {i}: ids differ"
         worst = max(worst, assert_close_bf16(to_np(out[i]), o_ref, rel=rel, abs_tol=abs_tol))
-    print(f"[verify 36L x 16K {'int8' if quant else 'bf16'}] max |err| {worst:.3e}", flush=True)
+    print(f"[verify 36L x 16K {('int8 ' + layout) if quant else 'bf16'}] max |err| {worst:.3e}", flush=True)

@@ -20,7 +20,9 @@
 // masked), so the waits count exactly.  Block maxima across the
 // r rows use lane shuffles; the maximum across KV heads is an atomicMax on
 // the order-preserving uint32 key of the score, which kernel 2 consumes and
-// resets to zero.
+// resets to zero.  Several queries (verify draft tokens, prefill tile
+// summaries) take score_multi_kernel instead: one workgroup per tile, the
+// query rows split over its four waves.
 //
 // Kernel 2 (topk_kernel) selects, per (layer[, query]), the k largest scores
 // with protected blocks forced to -inf: an LDS radix select over the 32-bit
@@ -430,6 +432,149 @@ __global__ __launch_bounds__(kScoreThreads) void score_kernel(
                    n_skip);
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(4))) const u32x4 cu32x4;  // read with scalar loads
+typedef __attribute__((address_space(4))) const int32_t cint32;
+
+// Multi-query form (nq >= 2: the draft tokens of a verify round, the tile
+// summaries of a prefill chunk).  One workgroup per (16-block tile, KV head,
+// layer): the 64 x 256 B tile is copied into LDS with coalesced 16-byte loads
+// (four per thread) and the nq * G query rows of the head are split over the
+// four waves, ceil(nq G / 4) rows each.  Every wave reads the whole tile from
+// LDS (one row per lane, widened to fp32 in registers) and computes its share
+// of the dots, QB query rows at a time: the same ascending-d fma chain from +0
+// as score_kernel (identical bits), with the query values in scalar
+// registers, so each wave's products are a quarter of the tile's and every
+// SIMD gets the same number of waves.  The bf16 tile (17 KiB) leaves room for
+// eight workgroups per CU, whose waves hide each other's scalar-load and LDS
+// latencies; each wave touches the cache lines of its query rows while the
+// tile loads are in flight, so the per-pass scalar loads hit the scalar
+// cache.  Maxima are taken over the order-preserving keys: a query whose rows
+// are split between two waves combines exactly through the atomicMax, and a
+// NaN dot makes the block's score NaN (numpy's max).
+template <int QB>
+__global__ __launch_bounds__(kScoreThreads) void score_multi_kernel(
+    const uint16_t* __restrict__ q, int64_t q_ls, int nq, int per_query, int log_g,
+    const uint16_t* __restrict__ reps, int64_t reps_ls, int hkv, int cap, int nblocks, int log_r,
+    uint32_t* __restrict__ keys) {
+  // row r, dims 8c .. 8c+7 at r * 17 + c: the one-chunk pad per row makes a
+  // lane-per-row ds_read_b128 conflict-free with an immediate offset per chunk
+  __shared__ uint4 tile[kWave * 17];
+  const int layer = blockIdx.y;
+  const int h = blockIdx.x % hkv;
+  const int R = 1 << log_r;
+  const int b0 = (blockIdx.x / hkv) * (kWave >> log_r);
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = 1 << log_g;
+  const int J = nq << log_g;  // query rows (n, g), j = n G + g
+  const int per = (J + kScoreWaves - 1) / kScoreWaves;
+  const int j0 = wave * per;
+  const int j1 = min(J, j0 + per);
+  const int hq = hkv << log_g;
+  const uint16_t* qL = q + static_cast<int64_t>(layer) * q_ls;
+  auto qrow = [&](int j) {
+    return reinterpret_cast<const char*>(
+        qL + (static_cast<int64_t>(j >> log_g) * hq + (h << log_g) + (j & (G - 1))) * kHeadDim);
+  };
+
+  {
+    // one dword of every 64-byte line of the wave's first QB query rows, read
+    // first so that the scalar misses overlap the tile loads
+    int32_t t[QB * 4];
+#pragma unroll
+    for (int i = 0; i < QB; ++i) {
+      const cint32* r = (const cint32*)qrow(min(j0 + i, max(j1, 1) - 1));
+#pragma unroll
+      for (int l = 0; l < 4; ++l) t[4 * i + l] = r[16 * l];
+    }
+    // chunk i = k * 256 + tid of the tile: row i / 16, dims 8 (i % 16) .. +7;
+    // rows past nblocks are clamped to the last valid row and zeroed
+    const uint4* src = reinterpret_cast<const uint4*>(
+        reps + static_cast<int64_t>(layer) * reps_ls + (static_cast<int64_t>(h) * cap + b0) * (R * kHeadDim));
+    const int last_row = ((nblocks - b0) << log_r) - 1;
+    uint4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = k * kScoreThreads + tid;
+      const int row = i >> 4;
+      v[k] = and_mask(src[min(row, last_row) * 16 + (i & 15)], row <= last_row);
+    }
+    int32_t x = 0;
+#pragma unroll
+    for (int i = 0; i < QB * 4; ++i) x ^= t[i];
+    asm volatile("" ::"s"(x));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = k * kScoreThreads + tid;
+      tile[(i >> 4) * 17 + (i & 15)] = v[k];
+    }
+  }
+  __syncthreads();
+
+  const int b = b0 + (lane >> log_r);
+  const bool owner = (lane & (R - 1)) == 0 && b < nblocks;
+  const uint4* my = tile + lane * 17;
+  const int64_t krow = static_cast<int64_t>(layer) * (per_query ? nq : 1);
+
+  // key maximum of the current query's rows in this lane, flushed (maximum
+  // over the r rows of the block, then atomicMax) when the query changes
+  uint32_t cur = 0u;
+  int cur_n = -1;
+  auto flush = [&](int n, uint32_t km) {
+    for (int o = 1; o < R; o <<= 1) km = max(km, static_cast<uint32_t>(__shfl_xor(static_cast<int>(km), o)));
+    if (owner) atomicMax(&keys[(krow + n) * nblocks + b], km);
+  };
+  for (int jg = j0; jg < j1; jg += QB) {
+    const char* qp[QB];
+#pragma unroll
+    for (int i = 0; i < QB; ++i) qp[i] = qrow(min(jg + i, j1 - 1));  // a short last group repeats its last row
+    float acc[QB];
+#pragma unroll
+    for (int i = 0; i < QB; ++i) acc[i] = 0.0f;
+    // 8 dims per pass: one 16-byte scalar load per query row at the shared
+    // byte offset `off` (kept opaque so that each load addresses row + off
+    // instead of stepping QB pointers), one row chunk from LDS
+    uint32_t off = 0;
+#pragma unroll 1
+    for (int c = 0; c < 16; ++c) {
+      asm volatile("" : "+s"(off));
+      const uint4 rv = my[c];
+      const float r[8] = {bf16_lo(rv.x), bf16_hi(rv.x), bf16_lo(rv.y), bf16_hi(rv.y),
+                          bf16_lo(rv.z), bf16_hi(rv.z), bf16_lo(rv.w), bf16_hi(rv.w)};
+#pragma unroll
+      for (int i = 0; i < QB; ++i) {
+        const u32x4 w = *(cu32x4*)(qp[i] + off);  // dims 8 c .. +7 of row jg + i
+        acc[i] = __builtin_fmaf(bf16_lo(w.x), r[0], acc[i]);
+        acc[i] = __builtin_fmaf(bf16_hi(w.x), r[1], acc[i]);
+        acc[i] = __builtin_fmaf(bf16_lo(w.y), r[2], acc[i]);
+        acc[i] = __builtin_fmaf(bf16_hi(w.y), r[3], acc[i]);
+        acc[i] = __builtin_fmaf(bf16_lo(w.z), r[4], acc[i]);
+        acc[i] = __builtin_fmaf(bf16_hi(w.z), r[5], acc[i]);
+        acc[i] = __builtin_fmaf(bf16_lo(w.w), r[6], acc[i]);
+        acc[i] = __builtin_fmaf(bf16_hi(w.w), r[7], acc[i]);
+      }
+      off += 16;
+    }
+#pragma unroll
+    for (int i = 0; i < QB; ++i) {
+      const int j = jg + i;
+      if (j >= j1) break;
+      const int n = per_query ? (j >> log_g) : 0;
+      const uint32_t key = score_key(acc[i]);
+      if (n != cur_n) {
+        if (cur_n >= 0) flush(cur_n, cur);
+        cur_n = n;
+        cur = key;
+      } else {
+        cur = max(cur, key);
+      }
+    }
+  }
+  if (cur_n >= 0) flush(cur_n, cur);
+}
+
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
     uint32_t* __restrict__ score_keys, int nblocks, const int32_t* __restrict__ prot,
     int nprot, int k_req, int order, int32_t* __restrict__ out_ids,
@@ -784,14 +929,35 @@ int select_impl(const nkv_store* st, int layer0, int num_layers, const uint16_t*
   a.keys = score_keys;
   a.skip_ids = step ? protected_ids : nullptr;
   a.n_skip = step ? n_protected : 0;
-  dim3 grid(((a.units / st->num_kv_heads + kScoreWaves - 1) / kScoreWaves) * st->num_kv_heads, num_layers);
+  const bool pow2 = (g & (g - 1)) == 0 && g <= 16 && (R & (R - 1)) == 0 && R <= 8;
+  NKV_CHECK_SUPPORTED(pow2, "nkv_select: unsupported (r=%d, G=%d)", R, g);
   int bad = 0;
-  switch (R) {
-    case 1: bad = dispatch_g<1>(g, grid, s, a); break;
-    case 2: bad = dispatch_g<2>(g, grid, s, a); break;
-    case 4: bad = dispatch_g<4>(g, grid, s, a); break;
-    case 8: bad = dispatch_g<8>(g, grid, s, a); break;
-    default: bad = -1;
+  if (nq >= 2 && nq * g >= 2 * kScoreWaves) {
+    // several queries: the workgroup-per-tile form, QB query rows per pass
+    const int per = (nq * g + kScoreWaves - 1) / kScoreWaves;
+    const int log_g = __builtin_ctz(g), log_r = __builtin_ctz(R);
+    const dim3 grid(((nblocks + TB - 1) / TB) * st->num_kv_heads, num_layers);
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, grid, dim3(kScoreThreads), 0, s, a.q, a.q_ls, a.nq, a.per_query, log_g, a.reps,
+                         a.reps_ls, a.hkv, a.cap, a.nblocks, log_r, a.keys);
+    };
+    // the pass width (2, 4 or 6 rows) that repeats the fewest rows in the
+    // last group, the wider on ties (8 rows would spill scalar registers)
+    int qb = 6;
+    for (const int w : {4, 2})
+      if ((per + w - 1) / w * w < (per + qb - 1) / qb * qb) qb = w;
+    if (qb == 2) go(score_multi_kernel<2>);
+    else if (qb == 4) go(score_multi_kernel<4>);
+    else go(score_multi_kernel<6>);
+  } else {
+    dim3 grid(((a.units / st->num_kv_heads + kScoreWaves - 1) / kScoreWaves) * st->num_kv_heads, num_layers);
+    switch (R) {
+      case 1: bad = dispatch_g<1>(g, grid, s, a); break;
+      case 2: bad = dispatch_g<2>(g, grid, s, a); break;
+      case 4: bad = dispatch_g<4>(g, grid, s, a); break;
+      case 8: bad = dispatch_g<8>(g, grid, s, a); break;
+      default: bad = -1;
+    }
   }
   NKV_CHECK_SUPPORTED(bad == 0, "nkv_select: unsupported (r=%d, G=%d)", R, g);
   rc = launch_status("nkv_select/score");

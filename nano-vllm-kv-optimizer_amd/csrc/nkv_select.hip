@@ -41,6 +41,7 @@ constexpr int kTopkThreads = 256;
 constexpr int kMaxTopk = 1024;
 constexpr int kMaxSelectBlocks = 12288;  // keys + masks + sort buffer stay under 64 KiB of LDS
 constexpr uint32_t kNegInfKey = 0x007fffffu;  // score_key(-inf)
+constexpr uint32_t kNaNKey = 0xffc00000u;     // score_key(NaN), above score_key(+inf)
 
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
@@ -368,7 +369,7 @@ __device__ __forceinline__ void score_dots(
   const int h = unit % hkv;
   const int b = (unit / hkv) * TB + lane / R;
   const uint16_t* qL = q + static_cast<int64_t>(layer) * q_ls;
-  float best = -INFINITY;
+  uint32_t best = 0u;  // below every key score_key() produces
   for (int n = 0; n < nq; ++n) {
     if (n > 0) t.qc.load(qL, hkv * G, h, n, lane);
     float acc[G];
@@ -390,16 +391,23 @@ __device__ __forceinline__ void score_dots(
         t.qc.fma_chunk(rv, hf * 8 + c, acc);
       }
     }
+    // the lane's maximum over its G dots, NaN if any of them is NaN (the
+    // oracle's numpy max), then the key maximum over the block's r rows
     float m = acc[0];
+    bool nan = __builtin_isnan(acc[0]);
 #pragma unroll
-    for (int g = 1; g < G; ++g) m = fmaxf(m, acc[g]);
+    for (int g = 1; g < G; ++g) {
+      m = fmaxf(m, acc[g]);
+      nan |= __builtin_isnan(acc[g]);
+    }
+    uint32_t km = nan ? kNaNKey : score_key(m);
 #pragma unroll
-    for (int o = 1; o < R; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    for (int o = 1; o < R; o <<= 1) km = max(km, static_cast<uint32_t>(__shfl_xor(static_cast<int>(km), o)));
     if (per_query) {
       if ((lane % R) == 0 && b < nblocks)
-        atomicMax(&keys[(static_cast<int64_t>(layer) * nqo + n) * nblocks + b], score_key(m));
+        atomicMax(&keys[(static_cast<int64_t>(layer) * nqo + n) * nblocks + b], km);
     } else {
-      best = fmaxf(best, m);
+      best = max(best, km);
     }
   }
   if (!per_query) {
@@ -408,7 +416,7 @@ __device__ __forceinline__ void score_dots(
     bool skip = false;
     for (int i = 0; i < n_skip; ++i) skip |= skip_ids[i] == b;
     if ((lane % R) == 0 && b < nblocks && !skip)
-      atomicMax(&keys[static_cast<int64_t>(layer) * nblocks + b], score_key(best));
+      atomicMax(&keys[static_cast<int64_t>(layer) * nblocks + b], best);
   }
 }
 

@@ -1,15 +1,14 @@
 """The multi-query scorer (nkv_select with nq >= 2 queries and nq * G >= 8
 query rows: verify draft tokens, prefill tile summaries) against the oracle.
 
-Each workgroup widens one 16-block tile to fp32 in LDS and splits the
-nq * G query rows of its KV head over four waves, so one query's rows can be
-scored by two waves and combined by the atomicMax on the order-preserving
-key.  Scores must be bit-identical to the oracle's sequential-fma dots
+Each workgroup copies one 16-block tile into LDS and splits the nq * G
+query rows of its KV head over four waves, so one query's rows can be scored
+by two waves and combined by the atomicMax on the order-preserving key.  Scores must be bit-identical to the oracle's sequential-fma dots
 (m12_runtime.py:999-1003 and :1068-1072, the shared and per-query maxima),
 and the per-query / shared Top-K ids identical, over GQA ratios 1-16, r 1-8,
 ragged tiles, several layers and query-row counts that leave a short last
-group.  A NaN representative makes its block's score NaN, as numpy's max
-over the dots does (NaN sorts above +inf).
+group.  In both scorer forms a NaN representative makes its block's score
+NaN, as numpy's max over the dots does (NaN sorts above +inf).
 """
 
 import numpy as np
@@ -77,10 +76,11 @@ def test_multi_query_scores_and_ids_bit_exact(G, r, nq, nb, per_query, L, seed):
             assert ids[l, t].tolist() == ids_or.tolist(), f"layer {l} row {t}: ids differ"
 
 
-@pytest.mark.parametrize("per_query", [True, False])
-def test_multi_query_nan_representative_makes_the_block_score_nan(per_query):
-    torch.manual_seed(4200)
-    G, r, nq, nb = 4, 4, 6, 48
+@pytest.mark.parametrize("nq,per_query", [(6, True), (6, False), (1, False), (1, True), (2, False)])
+def test_nan_representative_makes_the_block_score_nan(nq, per_query):
+    """Both scorer forms (one query: score_kernel; several: score_multi_kernel)."""
+    torch.manual_seed(4200 + nq)
+    G, r, nb = 4, 4, 48
     st = _store(1, G, r, nb)
     reps = (torch.randn(1, HKV, nb, r, D) / D ** 0.5).to(torch.bfloat16)
     reps[0, 3, 17, 2, 40] = float("nan")     # one element of one representative of block 17

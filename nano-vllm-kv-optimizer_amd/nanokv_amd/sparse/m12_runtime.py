@@ -368,7 +368,9 @@ class _SparseCore:
         return ids, vals, self.effective_k(requested)
 
     # -- attention ------------------------------------------------------------
-    def _splits(self, nseg: int, nqg: int) -> int:
+    def _splits(self, nseg: int, nqg: int, rows: int = 4) -> int:
+        """Attention split count for nseg segments per (layer, KV head, query
+        group); rows = query rows per group (17-32: the wide few-query kernel)."""
         if self.cfg.attend_splits is not None:
             return self.cfg.attend_splits
         # Workgroups per launch measured best on the 36-layer 32K decode step
@@ -382,7 +384,11 @@ class _SparseCore:
         # the splits that carry an extra segment to the same XCDs (4 and 8
         # splits measured 5% and 14% slower than 5 in bf16): such counts
         # move up by one.
-        target = 1440 if self.cfg.kv_format == "bf16" else 900
+        # The wide few-query kernel (verify's draft tokens, 17-32 rows a
+        # group) holds two workgroups per CU: ~900 as well (36-layer 16K
+        # verify, 6 tokens, bf16, us per round at splits 1 / 2 / 3 / 4 / 5 / 6
+        # / 7 / 9: 372 / 398 / 344.7 / 370 / 353 / 367 / 363 / 380).
+        target = 1440 if self.cfg.kv_format == "bf16" and rows <= 16 else 900
         want = max(1, round(target / (self.store.num_kv_heads * self.nl * nqg)))
         cap = max(1, min(-(-nseg // 4), 64))
         s = min(want, cap)
@@ -412,7 +418,7 @@ class _SparseCore:
         nqg = -(-tq // qpg)
         R = cfg.recent_tokens
         nseg = n_hist + -(-sink_len // 64) + (-(-R // 64) if rec_len else 0) + -(-n_chunk // 64)
-        splits = self._splits(nseg, nqg)
+        splits = self._splits(nseg, nqg, min(qpg, tq) * g)
         if out is None:
             out = torch.empty_like(q)
         part = self._buf("partial" + ws, self.store.attend_workspace_floats(nl, tq, splits), torch.float32)

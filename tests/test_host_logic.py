@@ -47,10 +47,10 @@ def test_kv_format_mapping():
     assert rt.M12Config(quant_history=True, quant_scale_layout="token").kv_format == "int8_token"
 
 
-def _split_choice(nseg, layers=36, kv_heads=8, nqg=1, **cfg):
+def _split_choice(nseg, layers=36, kv_heads=8, nqg=1, rows=4, **cfg):
     from types import SimpleNamespace
     me = SimpleNamespace(cfg=rt.M12Config(**cfg), store=SimpleNamespace(num_kv_heads=kv_heads), nl=layers)
-    return rt._SparseCore._splits(me, nseg, nqg)
+    return rt._SparseCore._splits(me, nseg, nqg, rows)
 
 
 def test_decode_split_choice():
@@ -59,6 +59,11 @@ def test_decode_split_choice():
     assert _split_choice(41, quant_history=True) == 3          # per-block int8: ~900
     assert _split_choice(41, quant_history=True, quant_scale_layout="token") == 3   # per-token int8: ~900
     assert _split_choice(41, attend_splits=8) == 8             # explicit choice kept
+    # verify: 6 draft tokens x 4 heads = 24 rows on the wide kernel, 16K history
+    # (139 union blocks + sink + 8 recent pieces + the draft chunk = 149 segments)
+    assert _split_choice(149, rows=24) == 3                     # bf16: ~900 as well
+    assert _split_choice(149, rows=24, quant_history=True) == 3
+    assert _split_choice(149, rows=16) == 5                     # the 16-row kernel keeps ~1440
     for layers in range(1, 80):
         for nseg in (1, 5, 16, 41, 300):
             s = _split_choice(nseg, layers=layers)

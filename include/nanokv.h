@@ -92,7 +92,8 @@ const char* nkv_last_error(void);
  * q        : bf16 [num_layers][nq][Hq][D], layer stride q_layer_stride elements.
  * score[b] = max over (n<nq, h, g, j<r) of the fp32 dot q[n][h*G+g] . reps[h][b][j],
  *            each dot accumulated in ascending d with fma from +0
- *            (per_query=0); per n when per_query=1.
+ *            (per_query=0); per n when per_query=1.  A NaN dot makes the
+ *            score NaN, which ranks above +inf; -0 ranks as +0.
  * Protected ids (device int32 list, shared by all layers; ids outside
  * [0, nblocks) are ignored) are scored -inf.  k_eff = min(k, max(1, nblocks
  * - |protected in range|)) ids are returned per (layer[, n]), ordered by

@@ -278,12 +278,10 @@ struct OperandOffsets {
 struct Col {
   float nm;
   float thr;
-  float l;
 };
 __device__ __forceinline__ void col_init(Col& c) {
   c.nm = 0.0f;
   c.thr = -INFINITY;
-  c.l = 0.0f;
 }
 __device__ __forceinline__ float col_max(const Col& c) { return c.thr == -INFINITY ? -INFINITY : -c.nm; }
 
@@ -298,14 +296,15 @@ __device__ __forceinline__ float col_max(const Col& c) { return c.thr == -INFINI
 //   * O^T += V^T . P^T: A = 16 dims x 32 keys from two transposing LDS reads
 //     (ds_read_b64_tr_b16), B = the lane's own probabilities rounded to bf16
 //     (the 32-key contraction index is ordered as the S^T accumulator holds
-//     the keys, so P never leaves the registers); l accumulates the same
-//     bf16-rounded probabilities (one dot2 per pair), so numerator and
-//     denominator see the same P.
+//     the keys, so P never leaves the registers); the row sums l are one
+//     more product per 32 keys, of the same bf16-rounded P with a constant
+//     all-ones A operand (every accumulator row holds the column's sum), so
+//     numerator and denominator see the same P.
 template <bool PACKED, int NCT, int KT>
 __device__ __forceinline__ void attend_segment(const AttendParams& p, const Seg& cur, const char* buf, bool mask,
                                                int lg, const OperandOffsets& off, const bf16x8 (&bq)[NCT][4],
                                                const int (&tcol)[NCT], const int (&allow)[NCT],
-                                               f32x4 (&acc)[8][NCT], Col (&col)[NCT]) {
+                                               f32x4 (&acc)[8][NCT], f32x4 (&lsum)[NCT], Col (&col)[NCT]) {
   // Operand reads run two products ahead through a ring of three registers;
   // the scheduling barriers keep that order (left to itself the scheduler may
   // sink each read onto its product and wait out the full LDS latency).
@@ -384,7 +383,7 @@ __device__ __forceinline__ void attend_segment(const AttendParams& p, const Seg&
         rescale = rescale || alpha[ct] != 1.0f;
         col[ct].nm = -m_use;
         col[ct].thr = m_new == -INFINITY ? -INFINITY : (m_new + 8.0f) / p.scale_log2;
-        col[ct].l *= alpha[ct];
+        lsum[ct] *= alpha[ct];
       }
       if (__any(rescale)) {
 #pragma unroll
@@ -417,14 +416,8 @@ __device__ __forceinline__ void attend_segment(const AttendParams& p, const Seg&
                               pack_bf16(a1[2], a1[3])};
         bp[ct] = __builtin_bit_cast(bf16x8, w);
         if (dt == 0) {
-          const bf16x2 one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
-          // (each word is copied out first: clang's __builtin_bit_cast of a
-          // vector element reads element 0)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t we = w[e];
-            col[ct].l = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, we), one, col[ct].l, false);
-          }
+          const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+          lsum[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, bp[ct], lsum[ct], 0, 0, 0);
         }
       }
       if (i + 2 < kV) va[(i + 2) % 3] = read_v(k2_0 + (i + 2) / 8, (i + 2) % 8);
@@ -490,6 +483,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
   for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) acc[dt][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4 lsum[NCT];   // row sums: every row of a column's accumulator holds its sum
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) lsum[ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   Col cs[NCT];   // per-column softmax state
 #pragma unroll
   for (int ct = 0; ct < NCT; ++ct) col_init(cs[ct]);
@@ -581,7 +577,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
     }
 
     attend_segment<PACKED, NCT, NCT == 2 ? 4 : 2>(p, cur, buf, needs_mask<PACKED>(p, cur, t0), lg, off, bq, tcol,
-                                                 allow_cur, acc, cs);
+                                                 allow_cur, acc, lsum, cs);
 
     if (more)
       finish_stage(nxt, other);
@@ -598,7 +594,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const AttendPara
   // ---- normalise and store: acc[dt][ct][i] = dim 16 dt + 4 lg + i -----------
 #pragma unroll
   for (int ct = 0; ct < NCT; ++ct) {
-    const float l = sum_over_rows(cs[ct].l);
+    const float l = lsum[ct][0];
     const int t = tcol[ct];
     if (p.splits > 1) {
       // this split's (m, l, acc) of the column, merged by prefill_merge_kernel

@@ -465,13 +465,14 @@ __global__ __launch_bounds__(kScoreThreads) void score_multi_kernel(
     const uint16_t* __restrict__ q, int64_t q_ls, int nq, int per_query, int log_g,
     const uint16_t* __restrict__ reps, int64_t reps_ls, int hkv, int cap, int nblocks, int log_r,
     uint32_t* __restrict__ keys) {
-  // row r, dims 8c .. 8c+7 at r * 17 + c: the one-chunk pad per row makes a
-  // lane-per-row ds_read_b128 conflict-free with an immediate offset per chunk
-  __shared__ uint4 tile[kWave * 17];
+  // row r (0 .. 127), dims 8c .. 8c+7 at r * 17 + c: the one-chunk pad per row
+  // makes a lane-per-row ds_read_b128 conflict-free with an immediate offset
+  __shared__ uint4 tile[2 * kWave * 17];
   const int layer = blockIdx.y;
   const int h = blockIdx.x % hkv;
   const int R = 1 << log_r;
-  const int b0 = (blockIdx.x / hkv) * (kWave >> log_r);
+  const int TB = kWave >> log_r;  // blocks per 64 rows
+  const int b0 = (blockIdx.x / hkv) * 2 * TB;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -497,14 +498,14 @@ __global__ __launch_bounds__(kScoreThreads) void score_multi_kernel(
 #pragma unroll
       for (int l = 0; l < 4; ++l) t[4 * i + l] = r[16 * l];
     }
-    // chunk i = k * 256 + tid of the tile: row i / 16, dims 8 (i % 16) .. +7;
-    // rows past nblocks are clamped to the last valid row and zeroed
+    // chunk i = k * 256 + tid of the 128 rows: row i / 16, dims 8 (i % 16)
+    // .. +7; rows past nblocks are clamped to the last valid row and zeroed
     const uint4* src = reinterpret_cast<const uint4*>(
         reps + static_cast<int64_t>(layer) * reps_ls + (static_cast<int64_t>(h) * cap + b0) * (R * kHeadDim));
     const int last_row = ((nblocks - b0) << log_r) - 1;
-    uint4 v[4];
+    uint4 v[8];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < 8; ++k) {
       const int i = k * kScoreThreads + tid;
       const int row = i >> 4;
       v[k] = and_mask(src[min(row, last_row) * 16 + (i & 15)], row <= last_row);
@@ -514,54 +515,64 @@ __global__ __launch_bounds__(kScoreThreads) void score_multi_kernel(
     for (int i = 0; i < QB * 4; ++i) x ^= t[i];
     asm volatile("" ::"s"(x));
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < 8; ++k) {
       const int i = k * kScoreThreads + tid;
       tile[(i >> 4) * 17 + (i & 15)] = v[k];
     }
   }
   __syncthreads();
 
+  // lane l owns rows l (block b0 + l / r) and 64 + l (TB blocks further)
   const int b = b0 + (lane >> log_r);
-  const bool owner = (lane & (R - 1)) == 0 && b < nblocks;
-  const uint4* my = tile + lane * 17;
+  const bool own0 = (lane & (R - 1)) == 0 && b < nblocks;
+  const bool own1 = (lane & (R - 1)) == 0 && b + TB < nblocks;
+  const uint4* my0 = tile + lane * 17;
+  const uint4* my1 = tile + (lane + kWave) * 17;
   const int64_t krow = static_cast<int64_t>(layer) * (per_query ? nq : 1);
 
-  // key maximum of the current query's rows in this lane, flushed (maximum
-  // over the r rows of the block, then atomicMax) when the query changes
-  uint32_t cur = 0u;
+  // key maxima of the current query's rows in this lane (both rows), flushed
+  // (maximum over the r rows of each block, then atomicMax) when the query
+  // changes
+  uint32_t cur0 = 0u, cur1 = 0u;
   int cur_n = -1;
-  auto flush = [&](int n, uint32_t km) {
-    for (int o = 1; o < R; o <<= 1) km = max(km, static_cast<uint32_t>(__shfl_xor(static_cast<int>(km), o)));
-    if (owner) atomicMax(&keys[(krow + n) * nblocks + b], km);
+  auto flush = [&](int n, uint32_t k0, uint32_t k1) {
+    for (int o = 1; o < R; o <<= 1) {
+      k0 = max(k0, static_cast<uint32_t>(__shfl_xor(static_cast<int>(k0), o)));
+      k1 = max(k1, static_cast<uint32_t>(__shfl_xor(static_cast<int>(k1), o)));
+    }
+    if (own0) atomicMax(&keys[(krow + n) * nblocks + b], k0);
+    if (own1) atomicMax(&keys[(krow + n) * nblocks + b + TB], k1);
   };
   for (int jg = j0; jg < j1; jg += QB) {
     const char* qp[QB];
 #pragma unroll
     for (int i = 0; i < QB; ++i) qp[i] = qrow(min(jg + i, j1 - 1));  // a short last group repeats its last row
-    float acc[QB];
+    float acc0[QB], acc1[QB];
 #pragma unroll
-    for (int i = 0; i < QB; ++i) acc[i] = 0.0f;
+    for (int i = 0; i < QB; ++i) acc0[i] = acc1[i] = 0.0f;
     // 8 dims per pass: one 16-byte scalar load per query row at the shared
     // byte offset `off` (kept opaque so that each load addresses row + off
-    // instead of stepping QB pointers), one row chunk from LDS
+    // instead of stepping QB pointers), one chunk of each of the lane's rows
+    // from LDS; every unpacked query value feeds two products
     uint32_t off = 0;
 #pragma unroll 1
     for (int c = 0; c < 16; ++c) {
       asm volatile("" : "+s"(off));
-      const uint4 rv = my[c];
-      const float r[8] = {bf16_lo(rv.x), bf16_hi(rv.x), bf16_lo(rv.y), bf16_hi(rv.y),
-                          bf16_lo(rv.z), bf16_hi(rv.z), bf16_lo(rv.w), bf16_hi(rv.w)};
+      const uint4 va = my0[c], vb = my1[c];
+      const float ra[8] = {bf16_lo(va.x), bf16_hi(va.x), bf16_lo(va.y), bf16_hi(va.y),
+                           bf16_lo(va.z), bf16_hi(va.z), bf16_lo(va.w), bf16_hi(va.w)};
+      const float rb[8] = {bf16_lo(vb.x), bf16_hi(vb.x), bf16_lo(vb.y), bf16_hi(vb.y),
+                           bf16_lo(vb.z), bf16_hi(vb.z), bf16_lo(vb.w), bf16_hi(vb.w)};
 #pragma unroll
       for (int i = 0; i < QB; ++i) {
         const u32x4 w = *(cu32x4*)(qp[i] + off);  // dims 8 c .. +7 of row jg + i
-        acc[i] = __builtin_fmaf(bf16_lo(w.x), r[0], acc[i]);
-        acc[i] = __builtin_fmaf(bf16_hi(w.x), r[1], acc[i]);
-        acc[i] = __builtin_fmaf(bf16_lo(w.y), r[2], acc[i]);
-        acc[i] = __builtin_fmaf(bf16_hi(w.y), r[3], acc[i]);
-        acc[i] = __builtin_fmaf(bf16_lo(w.z), r[4], acc[i]);
-        acc[i] = __builtin_fmaf(bf16_hi(w.z), r[5], acc[i]);
-        acc[i] = __builtin_fmaf(bf16_lo(w.w), r[6], acc[i]);
-        acc[i] = __builtin_fmaf(bf16_hi(w.w), r[7], acc[i]);
+        const float qf[8] = {bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y),
+                             bf16_lo(w.z), bf16_hi(w.z), bf16_lo(w.w), bf16_hi(w.w)};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          acc0[i] = __builtin_fmaf(qf[e], ra[e], acc0[i]);
+          acc1[i] = __builtin_fmaf(qf[e], rb[e], acc1[i]);
+        }
       }
       off += 16;
     }
@@ -570,17 +581,19 @@ __global__ __launch_bounds__(kScoreThreads) void score_multi_kernel(
       const int j = jg + i;
       if (j >= j1) break;
       const int n = per_query ? (j >> log_g) : 0;
-      const uint32_t key = score_key(acc[i]);
+      const uint32_t k0 = score_key(acc0[i]), k1 = score_key(acc1[i]);
       if (n != cur_n) {
-        if (cur_n >= 0) flush(cur_n, cur);
+        if (cur_n >= 0) flush(cur_n, cur0, cur1);
         cur_n = n;
-        cur = key;
+        cur0 = k0;
+        cur1 = k1;
       } else {
-        cur = max(cur, key);
+        cur0 = max(cur0, k0);
+        cur1 = max(cur1, k1);
       }
     }
   }
-  if (cur_n >= 0) flush(cur_n, cur);
+  if (cur_n >= 0) flush(cur_n, cur0, cur1);
 }
 
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
@@ -944,7 +957,7 @@ int select_impl(const nkv_store* st, int layer0, int num_layers, const uint16_t*
     // several queries: the workgroup-per-tile form, QB query rows per pass
     const int per = (nq * g + kScoreWaves - 1) / kScoreWaves;
     const int log_g = __builtin_ctz(g), log_r = __builtin_ctz(R);
-    const dim3 grid(((nblocks + TB - 1) / TB) * st->num_kv_heads, num_layers);
+    const dim3 grid(((nblocks + 2 * TB - 1) / (2 * TB)) * st->num_kv_heads, num_layers);  // 128 rows each
     auto go = [&](auto kern) {
       hipLaunchKernelGGL(kern, grid, dim3(kScoreThreads), 0, s, a.q, a.q_ls, a.nq, a.per_query, log_g, a.reps,
                          a.reps_ls, a.hkv, a.cap, a.nblocks, log_r, a.keys);

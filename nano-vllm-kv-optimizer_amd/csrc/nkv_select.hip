@@ -21,8 +21,8 @@
 // r rows use lane shuffles; the maximum across KV heads is an atomicMax on
 // the order-preserving uint32 key of the score, which kernel 2 consumes and
 // resets to zero.  Several queries (verify draft tokens, prefill tile
-// summaries) take score_multi_kernel instead: one workgroup per tile, the
-// query rows split over its four waves.
+// summaries) take score_multi_kernel instead: one workgroup per two tiles,
+// the query rows split over its four waves.
 //
 // Kernel 2 (topk_kernel) selects, per (layer[, query]), the k largest scores
 // with protected blocks forced to -inf: an LDS radix select over the 32-bit
@@ -445,21 +445,23 @@ typedef __attribute__((address_space(4))) const u32x4 cu32x4;  // read with scal
 typedef __attribute__((address_space(4))) const int32_t cint32;
 
 // Multi-query form (nq >= 2: the draft tokens of a verify round, the tile
-// summaries of a prefill chunk).  One workgroup per (16-block tile, KV head,
-// layer): the 64 x 256 B tile is copied into LDS with coalesced 16-byte loads
-// (four per thread) and the nq * G query rows of the head are split over the
-// four waves, ceil(nq G / 4) rows each.  Every wave reads the whole tile from
-// LDS (one row per lane, widened to fp32 in registers) and computes its share
-// of the dots, QB query rows at a time: the same ascending-d fma chain from +0
-// as score_kernel (identical bits), with the query values in scalar
-// registers, so each wave's products are a quarter of the tile's and every
-// SIMD gets the same number of waves.  The bf16 tile (17 KiB) leaves room for
-// eight workgroups per CU, whose waves hide each other's scalar-load and LDS
-// latencies; each wave touches the cache lines of its query rows while the
-// tile loads are in flight, so the per-pass scalar loads hit the scalar
-// cache.  Maxima are taken over the order-preserving keys: a query whose rows
-// are split between two waves combines exactly through the atomicMax, and a
-// NaN dot makes the block's score NaN (numpy's max).
+// summaries of a prefill chunk).  One workgroup per (32-block pair of tiles,
+// KV head, layer): the 128 x 256 B of representative rows are copied into LDS
+// with coalesced 16-byte loads (eight per thread) and the nq * G query rows
+// of the head are split over the four waves, ceil(nq G / 4) rows each.  Every
+// wave reads all the rows from LDS -- lane l owns rows l and 64 + l, widened
+// to fp32 in registers -- and computes its share of the dots, QB query rows
+// at a time: the same ascending-d fma chain from +0 as score_kernel
+// (identical bits), with the query values in scalar registers, each unpacked
+// value feeding both rows' products (the bf16 unpack is one scalar
+// instruction per value, which with one row per lane contended with the
+// vector products for issue).  Each wave's products are a quarter of the
+// workgroup's and every SIMD gets the same number of waves; each wave
+// touches the cache lines of its first query rows while the row loads are in
+// flight, so the per-pass scalar loads hit the scalar cache.  Maxima are taken
+// over the order-preserving keys: a query whose rows are split between two
+// waves combines exactly through the atomicMax, and a NaN dot makes the
+// block's score NaN (numpy's max).
 template <int QB>
 __global__ __launch_bounds__(kScoreThreads) void score_multi_kernel(
     const uint16_t* __restrict__ q, int64_t q_ls, int nq, int per_query, int log_g,

@@ -1,9 +1,10 @@
 """The multi-query scorer (nkv_select with nq >= 2 queries and nq * G >= 8
 query rows: verify draft tokens, prefill tile summaries) against the oracle.
 
-Each workgroup copies one 16-block tile into LDS and splits the nq * G
-query rows of its KV head over four waves, so one query's rows can be scored
-by two waves and combined by the atomicMax on the order-preserving key.  Scores must be bit-identical to the oracle's sequential-fma dots
+Each workgroup copies 32 blocks of representative rows into LDS (two rows
+a lane) and splits the nq * G query rows of its KV head over four waves, so
+one query's rows can be scored by two waves and combined by the atomicMax on
+the order-preserving key.  Scores must be bit-identical to the oracle's sequential-fma dots
 (m12_runtime.py:999-1003 and :1068-1072, the shared and per-query maxima),
 and the per-query / shared Top-K ids identical, over GQA ratios 1-16, r 1-8,
 ragged tiles, several layers and query-row counts that leave a short last

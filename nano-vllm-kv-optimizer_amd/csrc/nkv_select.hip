@@ -385,10 +385,21 @@ __device__ __forceinline__ void score_dots(
         my[row * 8 + (col ^ (row & 7))] = t.v[hf * 8 + c];
       }
       wave_lds_sync();
+      // two chunks per iteration for G <= 4 (the next chunk's reads issue
+      // before the current products: decode step +0.3-0.9%); with more query
+      // rows the second chunk's scalar operands would spill
+      if constexpr (G <= 4) {
+#pragma unroll 2
+        for (int c = 0; c < 8; ++c) {
+          const uint4 rv = my[lane * 8 + (c ^ (lane & 7))];
+          t.qc.fma_chunk(rv, hf * 8 + c, acc);
+        }
+      } else {
 #pragma unroll 1
-      for (int c = 0; c < 8; ++c) {
-        const uint4 rv = my[lane * 8 + (c ^ (lane & 7))];
-        t.qc.fma_chunk(rv, hf * 8 + c, acc);
+        for (int c = 0; c < 8; ++c) {
+          const uint4 rv = my[lane * 8 + (c ^ (lane & 7))];
+          t.qc.fma_chunk(rv, hf * 8 + c, acc);
+        }
       }
     }
     // the lane's maximum over its G dots, NaN if any of them is NaN (the

@@ -448,6 +448,18 @@ def attention_bf16_probs(q, k, v, scale: float, mask=None) -> np.ndarray:
     return out.reshape(tq, hq, d)
 
 
+def lossless_history_mask(allowed, block_size: int, s_len: int) -> np.ndarray:
+    """Per-query mask of lossless verify (m12_runtime.py:746-748): True =
+    disallowed.  allowed [Tq, U] says query t may read union block j; block j
+    occupies packed keys [j*B, (j+1)*B), so its flag repeats B times along the
+    key axis; keys past the U*B history tokens (sink, recent, chunk) are not
+    masked here."""
+    allowed = np.asarray(allowed, dtype=bool)
+    m = np.zeros((allowed.shape[0], s_len), dtype=bool)
+    m[:, :allowed.shape[1] * block_size] = ~np.repeat(allowed, block_size, axis=1)
+    return m
+
+
 def causal_mask(tq: int, s_len: int, causal_from: int, attn_mask=None) -> np.ndarray:
     """mask[t, s] = (s >= t + causal_from + 1) & (s >= causal_from), OR attn_mask.
 
@@ -676,6 +688,20 @@ class M12Oracle:
         return ids, np.concatenate(outs)
 
     # -- decode (m12_runtime.py:1141-1346) ---------------------------------
+    def route_query(self, q0):
+        """Decode routing query (m12_runtime.py:1176-1189): with a window W > 1
+        the current query joins the last W queries and the route is their
+        mean (the current query alone while the window holds one); attention
+        still uses the current query.  q0: [Hq, D]."""
+        W = self.cfg.decode_query_window
+        if W <= 1:
+            return q0
+        self.q_window.append(np.array(q0, F32))
+        del self.q_window[:-W]
+        if len(self.q_window) == 1:
+            return self.q_window[0]
+        return query_summaries(np.stack(self.q_window), 1)[0]
+
     def decode(self, q, k, v, budget=None):
         c = self.cfg
         q = np.asarray(q, F32)
@@ -684,14 +710,7 @@ class M12Oracle:
         self.recent_v[:-1] = self.recent_v[1:].copy()
         self.recent_k[-1] = np.asarray(k, F32)[0]
         self.recent_v[-1] = np.asarray(v, F32)[0]
-        # routing query: the mean of the last decode_query_window queries
-        # (m12_runtime.py:1176-1189); attention below uses the current q
-        q_route = q[0]
-        if c.decode_query_window > 1:
-            self.q_window.append(q[0].copy())
-            del self.q_window[:-c.decode_query_window]
-            if len(self.q_window) > 1:
-                q_route = query_summaries(np.stack(self.q_window), 1)[0]
+        q_route = self.route_query(q[0])
         req = c.top_k_blocks if (budget is None and c.decode_top_k_blocks is None) else (
             c.decode_top_k_blocks if budget is None else budget)
         if c.decode_relative_a is not None:
@@ -725,10 +744,7 @@ class M12Oracle:
         off = pk.shape[0]
         pk = np.concatenate([pk, np.asarray(k, F32)])
         pv = np.concatenate([pv, np.asarray(v, F32)])
-        attn_mask = None
-        if lossless:
-            attn_mask = np.zeros((tq, pk.shape[0]), dtype=bool)
-            attn_mask[:, :sel_tokens] = ~np.repeat(allowed, c.block_size, axis=1)
+        attn_mask = lossless_history_mask(allowed, c.block_size, pk.shape[0]) if lossless else None
         mask = causal_mask(tq, pk.shape[0], off, attn_mask)
         o = attention_fp64(q, pk, pv, c.scale, mask)
         self.pending = (np.asarray(k, F32), np.asarray(v, F32))

@@ -239,6 +239,8 @@ def test_prefill_4096_chunk_on_32k_history_full_size():
     (4096, 300, 64, 8, False),     # 5 tiles, the last one short
     (8192, 512, 64, 32, False),    # 8 full tiles
     (8192, 512, 128, 32, True),    # all layers at once, 4 tiles of 128
+    (8192, 600, 96, 32, False),    # 192-column kernel: two 48-token workgroups per tile, the last tile short
+    (8192, 768, 192, 16, True),    # 192-column kernel, all layers, four workgroups per tile
 ])
 def test_prefill_per_tile_selection_matches_oracle(T0, T, tile, top_k, model):
     """prefill_selection="tile": one Top-K per tile of queries from the tile's
@@ -271,3 +273,65 @@ def test_prefill_per_tile_selection_matches_oracle(T0, T, tile, top_k, model):
         ids_or, o_ref = ob.prefill_chunk_tiled(to_np(q[i]), to_np(k[i]), to_np(v[i]), tile)
         assert ids_all[i].tolist() == ids_or.tolist(), f"layer {i}: tile ids differ"
         assert_close_bf16(to_np(out[i]), o_ref, **PREFILL_TOL)
+
+
+def test_prefill_per_tile_selection_full_size_36_layers():
+    """The launch `bench.py --workload prefill --prefill-selection tile` times:
+    a 4096-token chunk of each of 36 layers against its 32K bf16 history, one
+    Top-32 per 64-query tile (64 tiles per layer), then the matrix-core
+    attention with each tile's own blocks.  Sampled layers: per-tile ids exact
+    against the oracle's selection over the GPU representatives, every row
+    against a float32 torch reference of the tile's packed keys, and sampled
+    rows (tile edges, the diagonal, the last row) against the fp64 oracle."""
+    from nanokv_amd import workload
+    from nanokv_amd.sparse import M12Config, M12ModelRuntime
+    L, T0, T, tile, K, seed = 36, 32768, 4096, 64, 32, 1234
+    cfg = M12Config(max_model_len=T0 + T, top_k_blocks=K, prefill_selection="tile",
+                    prefill_selection_tile=tile)
+    model = M12ModelRuntime(L, cfg)
+    kh = torch.empty(L, T0, 8, 128, dtype=torch.bfloat16, device="cuda")
+    vh = torch.empty_like(kh)
+    for i in range(L):
+        k, v, _, _ = workload.history(T0, seed + i, device="cuda")
+        kh[i].copy_(k)
+        vh[i].copy_(v)
+    model.prefill(kh, vh)
+    q, k, v = workload.prefill_chunk_inputs(T, seed, device="cuda", layers=L)
+    core = model.core
+    print("[tile prefill 36 x 32K] selection + attention launch", flush=True)
+    ids, n = core.select_tiles(q, K, tile)
+    out, _, _ = core.chunk_attend_tiled(q, k, v, ids, tile, n)
+    torch.cuda.synchronize()
+    nb0 = T0 // 64
+    assert n == K and ids.shape[:2] == (L, T // tile)
+    prot = O.protected_blocks_after_store(nb0, cfg.recent_tokens, 64)
+    _, roff, rlen = O.prefill_recent_slice(T0, cfg.sink_tokens, cfg.recent_tokens)
+    off = K * 64 + cfg.sink_tokens + rlen
+    for layer in (0, 17, 35):
+        reps = to_np(model.store.reps[layer, :, :nb0])
+        qn = to_np(q[layer])
+        ids_l = ids[layer].cpu()
+        kb = kh[layer].view(nb0, 64, 8, 128)
+        vb = vh[layer].view(nb0, 64, 8, 128)
+        prior_k = torch.cat([kh[layer, :cfg.sink_tokens], kh[layer, T0 - 512 + roff:T0 - 512 + roff + rlen]])
+        prior_v = torch.cat([vh[layer, :cfg.sink_tokens], vh[layer, T0 - 512 + roff:T0 - 512 + roff + rlen]])
+        worst32 = 0.0
+        for ti in range(T // tile):
+            t0, t1 = ti * tile, (ti + 1) * tile
+            qs = O.query_summaries(qn[t0:t1], 1)
+            ids_or, _ = O.select_blocks(qs, reps, nb0, 8, prot, K)
+            assert ids_l[ti, :n].tolist() == ids_or.tolist(), f"layer {layer} tile {ti}: ids differ"
+            idx = ids_l[ti, :n].to("cuda", torch.int64)
+            pk = torch.cat([kb[idx].reshape(-1, 8, 128), prior_k, k[layer, :t1]])
+            pv = torch.cat([vb[idx].reshape(-1, 8, 128), prior_v, v[layer, :t1]])
+            ref32 = _torch_reference(q[layer, t0:t1], pk, pv, off + t0, cfg.scale)
+            worst32 = max(worst32, (out[layer, t0:t1].float() - ref32).abs().max().item())
+            rows = [r for r in (0, 63, 64, 2047, 2048, 4095) if t0 <= r < t1]
+            if rows:
+                pkn, pvn = to_np(pk), to_np(pv)
+                for r in rows:
+                    o_ref = O.attention_fp64(qn[r:r + 1], pkn[:off + r + 1], pvn[:off + r + 1], cfg.scale)
+                    assert_close_bf16(to_np(out[layer, r:r + 1]), o_ref, **PREFILL_TOL)
+        print(f"[tile prefill 36 x 32K] layer {layer}: 64 tiles' ids exact, "
+              f"max |err| vs fp32 torch {worst32:.3e}", flush=True)
+        assert worst32 <= 2e-3

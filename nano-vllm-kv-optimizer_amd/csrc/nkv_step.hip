@@ -37,9 +37,10 @@ constexpr int kMaxScratchDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 // The device address of this GPU's `scratch` (the host-side name is only a
-// stand-in for the symbol), looked up once per device with the device
-// current; the first lookup also clears the key region on `s` with a fill
-// kernel (every later call leaves the keys it used at zero).
+// stand-in for the symbol), looked up with the device current until one
+// look-up succeeds; that look-up also clears the key region on `s` with a
+// fill kernel (every later call leaves the keys it used at zero).  A failed
+// set-up leaves the slot empty, so the next call tries again.
 __global__ void zero_words_kernel(uint32_t* p, int64_t n) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x)
@@ -47,9 +48,8 @@ __global__ void zero_words_kernel(uint32_t* p, int64_t n) {
 }
 
 struct ScratchSlot {
-  std::once_flag once;
-  void* ptr = nullptr;
-  hipError_t err = hipSuccess;
+  std::mutex mu;
+  void* ptr = nullptr;   // set (under mu) only once the look-up and the clear were enqueued
 };
 ScratchSlot g_scratch[kMaxScratchDevices];
 
@@ -63,20 +63,35 @@ int scratch_address(hipStream_t s, char** out) {
   NKV_CHECK_SUPPORTED(dev >= 0 && dev < kMaxScratchDevices, "nkv_decode_step_noalloc: device %d beyond %d", dev,
                       kMaxScratchDevices);
   ScratchSlot& slot = g_scratch[dev];
-  std::call_once(slot.once, [&] {
-    void* p = nullptr;
-    slot.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (slot.err != hipSuccess) return;
-    hipLaunchKernelGGL(zero_words_kernel, dim3(256), dim3(256), 0, s, static_cast<uint32_t*>(p), kScratchKeys);
-    slot.err = hipGetLastError();
-    if (slot.err == hipSuccess) slot.ptr = p;
-  });
+  std::lock_guard<std::mutex> lock(slot.mu);
   if (slot.ptr == nullptr) {
-    set_error("nkv_decode_step_noalloc: scratch set-up failed: %s", hipGetErrorString(slot.err));
-    return NKV_ERR_HIP;
+    void* p = nullptr;
+    hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err == hipSuccess) {
+      hipLaunchKernelGGL(zero_words_kernel, dim3(256), dim3(256), 0, s, static_cast<uint32_t*>(p), kScratchKeys);
+      err = hipGetLastError();
+    }
+    if (err != hipSuccess) {
+      set_error("nkv_decode_step_noalloc: scratch set-up failed: %s", hipGetErrorString(err));
+      return NKV_ERR_HIP;
+    }
+    slot.ptr = p;
   }
   *out = static_cast<char*>(slot.ptr);
   return NKV_OK;
+}
+
+// After a failed launch part-way through a range (NKV_ERR_HIP: the
+// arguments were checked and a scorer may have run), the range's score keys
+// may hold the scorer's maxima: clear them on the range's stream, so the
+// workspace is zero for the next call as the entry points promise.  An
+// argument error returns before anything is enqueued and clears nothing.
+int clear_keys_after_failure(int rc, uint32_t* keys, int64_t n, hipStream_t s) {
+  if (rc == NKV_ERR_HIP) {
+    hipLaunchKernelGGL(zero_words_kernel, dim3(256), dim3(256), 0, s, keys, n);
+    (void)hipGetLastError();
+  }
+  return rc;
 }
 
 // Events of this host thread for the current device, created on first use
@@ -181,15 +196,16 @@ extern "C" int nkv_decode_step(const nkv_store* st, int layer0, int num_layers, 
     }
     // the selection's step form leaves the keys for the attention launch to clear
     uint32_t* keys = score_keys + static_cast<int64_t>(l0) * nblocks;
+    const int64_t nkeys = static_cast<int64_t>(nl) * nblocks;
     rc = select_impl(st, layer0 + l0, nl, q + l0 * q_ls, q_ls, 1, 0, nblocks, protected_ids, n_protected, k,
                      NKV_ORDER_SCORE_DESC, keys, nullptr, out_ids + static_cast<int64_t>(l0) * k, nullptr, true, sr);
-    if (rc != NKV_OK) return rc;
+    if (rc != NKV_OK) return clear_keys_after_failure(rc, keys, nkeys, reinterpret_cast<hipStream_t>(sr));
     const bool step_keys = select_step_form(1, n_protected, nblocks);
     rc = attend_impl(st, layer0 + l0, nl, q + l0 * q_ls, q_ls, 1, k_new + l0 * kv_ls, v_new + l0 * kv_ls, kv_ls,
                      1, write_slot, out_ids + static_cast<int64_t>(l0) * k, k, n_hist, nullptr, 0, sink_len,
                      ring_base, rec_lo, rec_len, scale, splits, partial_ws ? partial_ws + r * ws_range : nullptr,
                      out + l0 * q_ls, step_keys ? keys : nullptr, nblocks, sr);
-    if (rc != NKV_OK) return rc;
+    if (rc != NKV_OK) return clear_keys_after_failure(rc, keys, nkeys, reinterpret_cast<hipStream_t>(sr));
     if (r > 0) {
       const hipError_t e = hipEventRecord(ev[r], reinterpret_cast<hipStream_t>(sr));
       if (e != hipSuccess) return hip_fail(e, "nkv_decode_step: hipEventRecord");

@@ -11,9 +11,7 @@ import ctypes
 import os
 
 LIB_NAME = "libnanokv.so"
-# NANOKV_LIB may point at another build of the same library (A/B timing).
-LIB_PATH = os.environ.get("NANOKV_LIB") or os.path.join(
-    os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 NKV_OK = 0
 NKV_ERR_ARG = 1

@@ -767,10 +767,17 @@ class M12LayerRuntime:
         by assigning one, tests/test_m14_prefill_layout.py:76), else None."""
         return self.__dict__.get("_gpu_select")
 
-    @staticmethod
-    def _ids_from_override(result) -> torch.Tensor:
+    def _ids_from_override(self, result) -> torch.Tensor:
+        """Block ids an override returned, as a flat CPU int64 tensor.  Every id
+        must name a filled history block: the kernels read blocks in place, so an
+        id past the filled history (or negative) is refused here rather than
+        attended as unwritten memory or skipped."""
         ids = result[0] if isinstance(result, tuple) else result
-        return torch.as_tensor(ids).to("cpu", torch.int64).flatten()
+        ids = torch.as_tensor(ids).to("cpu", torch.int64).flatten()
+        if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= self.nblocks_filled):
+            raise ValueError(f"_gpu_select override returned block ids outside [0, {self.nblocks_filled}) "
+                             f"(min {int(ids.min())}, max {int(ids.max())})")
+        return ids
 
     # -- exact attention over caller-packed K/V (m12_runtime.py:845-896) -------------
     def _fused_attention(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, hist_len: int,
@@ -1245,8 +1252,10 @@ class M12LayerRuntime:
             ids = ids_dev.to(torch.int64)
             if st.history_tier == "host":
                 ids = ids.cpu()
-            sel_k = st.hist_k[L][:, ids].permute(1, 2, 0, 3).reshape(-1, hkv, D)
-            sel_v = st.hist_v[L][:, ids].permute(1, 2, 0, 3).reshape(-1, hkv, D)
+            # contiguous before pinning: pin_memory keeps a view's strides, and
+            # a later .contiguous() would make a pageable copy
+            sel_k = st.hist_k[L][:, ids].permute(1, 2, 0, 3).reshape(-1, hkv, D).contiguous()
+            sel_v = st.hist_v[L][:, ids].permute(1, 2, 0, 3).reshape(-1, hkv, D).contiguous()
             if st.history_tier == "host":
                 sel_k, sel_v = sel_k.pin_memory(), sel_v.pin_memory()
             sink_len = min(cfg.sink_tokens, self.valid_len)
@@ -1256,7 +1265,7 @@ class M12LayerRuntime:
                     st.sink_v[L][:, :sink_len].permute(1, 0, 2).contiguous())
             recent = (st.recent_k[L][:, slots].permute(1, 0, 2).contiguous(),
                       st.recent_v[L][:, slots].permute(1, 0, 2).contiguous())
-            invocation = adapter.prepare(q, sel_k.contiguous(), sel_v.contiguous(), sink, recent, (k, v))
+            invocation = adapter.prepare(q, sel_k, sel_v, sink, recent, (k, v))
         with self._profile_range("prefill_attention"):
             return adapter.attend(invocation)
 
@@ -1501,7 +1510,7 @@ class M12ModelRuntime:
         dev = self.store.device
         cur = current_stream_ptr(dev)
         key = (nb, core._prot_key, w["sink_len"], w["rec_len"] > 0, cur, cfg.top_k_blocks, cfg.decode_top_k_blocks,
-               cfg.attend_splits, cfg.scale)
+               cfg.attend_splits, cfg.scale, self.layer_streams)
         plan = getattr(self, "_plan", None)
         if plan is not None and plan["key"] == key:
             return plan

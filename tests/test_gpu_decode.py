@@ -224,9 +224,12 @@ def test_layer_streams_identical_to_one_stream(streams):
     many.prefill(k, v)
     qs, ks, vs = workload.decode_inputs(steps, 11, layers=L)
     for s in range(steps):
+        if s == steps - 1:
+            many.layer_streams = 1           # a changed count takes effect on the next step
         q, kk, vv = qs[s].cuda(), ks[s].cuda(), vs[s].cuda()
         o1 = one.decode(q, kk, vv)
         o2 = many.decode(q, kk, vv)
+        assert many._plan["nstreams"] == many.layer_streams
         assert one.last_n_selected == many.last_n_selected
         n = one.last_n_selected
         assert torch.equal(one.last_ids_dev[:, :, :n], many.last_ids_dev[:, :, :n])

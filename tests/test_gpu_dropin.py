@@ -98,6 +98,21 @@ def test_prefill_chunk_with_forced_ids_equals_full_history_attention():
     assert rt.last_prefill_block_ids.tolist() == [1, 2, 3, 4, 5, 6]
 
 
+@pytest.mark.parametrize("bad", [[1, 8], [-1, 2], [3, 100]])
+def test_selector_override_ids_outside_the_history_are_refused(bad):
+    """Ids an override returns must name filled blocks (8 here): the kernels
+    read blocks in place, so an id past the history or a negative one raises."""
+    rt = _runtime()
+    g, _, _ = _history(rt, 512, 17)
+    rt._gpu_select = lambda _q, **kw: (torch.tensor(bad), {"n_selected": len(bad)})
+    q1 = _rand(g, 64, HQ, D)
+    kv = _rand(g, 64, HKV, D, scale=D ** -0.5)
+    with pytest.raises(ValueError, match="outside"):
+        rt.prefill_chunk(q1.cuda(), kv.cuda(), kv.cuda(), torch.device("cuda"))
+    with pytest.raises(ValueError, match="outside"):
+        rt.decode(q1[:1].cuda(), kv[:1].cuda(), kv[:1].cuda())
+
+
 def test_decode_and_verify_honour_a_selector_override():
     from nanokv_amd import workload
     from nanokv_amd.sparse import M12Config, M12LayerRuntime
@@ -224,3 +239,69 @@ def test_prefill_adapter_and_backend_errors():
     _history(rt2, 256, 92)
     with pytest.raises(ValueError, match="unknown prefill attention backend"):
         rt2.prefill_chunk(x, kv, kv, torch.device("cuda"))
+
+
+@pytest.mark.parametrize("tier", ["hbm", "host"])
+def test_shipped_segmented_prefill_adapter_matches_oracle(tier):
+    """The library's SegmentedPrefillAdapter (segmented_prefill_adapter.py:50-159)
+    set as cfg.prefill_adapter and shared by two layers, as ModelRunner shares
+    one adapter across all layers (model_runner.py:134-175): the runtime
+    selects, prepare() packs [selected | sink | recent | chunk] into the
+    shared scratch and attend() runs the packed matrix-core attention.  Ids
+    exact and outputs against the oracle's prefill_chunk, over two chunks per
+    layer; the HBM tier hands device tensors, the host tier pinned ones."""
+    from nanokv_amd.sparse import M12Config, M12LayerRuntime
+    from nanokv_amd.sparse.segmented_prefill_adapter import SegmentedPrefillAdapter
+    adapter = SegmentedPrefillAdapter("flash_reuse", D ** -0.5, (HQ, HKV, D, torch.bfloat16))
+    cfg = M12Config(max_model_len=8192, top_k_blocks=8, prefill_adapter=adapter, history_tier=tier)
+    layers = [M12LayerRuntime(i, cfg) for i in range(2)]
+    oracles = [O.M12Oracle(O.OracleConfig(top_k_blocks=8)) for _ in range(2)]
+    g = torch.Generator().manual_seed(4242)
+    for rt, ob in zip(layers, oracles):
+        k0, v0 = _rand(g, 3000, HKV, D, scale=D ** -0.5), _rand(g, 3000, HKV, D, scale=D ** -0.5)
+        rt.prefill_first(None, k0.cuda(), v0.cuda())
+        ob.store_kv(to_np(k0), to_np(v0), with_reps=False)
+    calls, biggest = 0, 0
+    for T in (300, 129):
+        for i, (rt, ob) in enumerate(zip(layers, oracles)):
+            nb = rt.nblocks_filled
+            ob.reps[:, :nb] = to_np(rt.reps_gpu[:, :nb])
+            q = _rand(g, T, HQ, D)
+            k, v = _rand(g, T, HKV, D, scale=D ** -0.5), _rand(g, T, HKV, D, scale=D ** -0.5)
+            print(f"[adapter {tier}] layer {i} chunk of {T}", flush=True)
+            out = rt.prefill_chunk(q.cuda(), k.cuda(), v.cuda(), torch.device("cuda"))
+            ids_or, o_ref = ob.prefill_chunk(to_np(q), to_np(k), to_np(v))
+            assert rt.last_prefill_block_ids.tolist() == ids_or.tolist()
+            worst = assert_close_bf16(to_np(out), o_ref, **PREFILL_TOL)
+            print(f"  max |err| {worst:.3e}", flush=True)
+            calls += 1
+            biggest = max(biggest, 8 * 64 + 64 + 512 + T)
+    st = adapter.stats()
+    assert st["fa2_calls"] == calls and st["direct_calls"] == 0
+    assert st["pack_capacity"] == biggest
+    assert st["shared_scratch_bytes"] == 2 * biggest * HKV * D * 2
+
+
+def test_shipped_adapter_rejects_pageable_staging_and_foreign_streams():
+    """segmented_prefill_adapter.py:72-77, :100-101: pageable host staging and a
+    stream other than the one the adapter was built on are refused."""
+    from nanokv_amd.sparse.segmented_prefill_adapter import SegmentedPrefillAdapter
+    adapter = SegmentedPrefillAdapter("flash_reuse", D ** -0.5, (HQ, HKV, D, torch.bfloat16))
+    q = torch.zeros(40, HQ, D, dtype=torch.bfloat16, device="cuda")
+    seg = torch.zeros(64, HKV, D, dtype=torch.bfloat16, device="cuda")
+    cur = torch.zeros(40, HKV, D, dtype=torch.bfloat16, device="cuda")
+    pageable = torch.zeros(128, HKV, D, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="selected CPU staging must be pinned"):
+        adapter.prepare(q, pageable, pageable, (seg, seg), (seg, seg), (cur, cur))
+    with pytest.raises(ValueError, match="inconsistent selected/current lengths"):
+        adapter.prepare(q, seg, seg, (seg, seg), (seg, seg), (seg, seg))
+    pinned = pageable.pin_memory()
+    inv = adapter.prepare(q, pinned, pinned, (seg, seg), (seg, seg), (cur, cur))
+    assert inv.packed[0].shape[0] == 128 + 64 + 64 + 40
+    other = torch.cuda.Stream()
+    with torch.cuda.stream(other):
+        with pytest.raises(ValueError, match="one CUDA device/stream"):
+            adapter.attend(inv)
+    out = adapter.attend(inv)
+    torch.cuda.synchronize()
+    assert out.shape == (40, HQ, D) and torch.isfinite(out.float()).all()

@@ -201,3 +201,13 @@ def test_attach_requires_attention_modules():
 
     with pytest.raises(ValueError, match="no attention modules"):
         A.attach_m12_runtimes(torch.nn.Linear(2, 2), rt.M12Config(max_model_len=1024))
+
+
+@pytest.mark.parametrize("backend,msg", [
+    ("flash", "expected explicit experimental backend"),       # segmented_prefill_adapter.py:60-61
+    ("operator", "does not ship"),
+])
+def test_segmented_prefill_adapter_backend_errors(backend, msg):
+    from nanokv_amd.sparse.segmented_prefill_adapter import SegmentedPrefillAdapter
+    with pytest.raises(ValueError, match=msg):
+        SegmentedPrefillAdapter(backend, 128 ** -0.5, (32, 8, 128, torch.bfloat16))

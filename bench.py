@@ -103,15 +103,25 @@ class DeviceEvents:
 
 
 def _cpu_model():
-    """The host CPU's model name (lscpu's "Model name", read from /proc/cpuinfo)."""
+    """The host CPU as /proc/cpuinfo names it: the model-name string (lscpu's
+    "Model name") with its family / model / stepping numbers, which identify
+    the part when a virtualised host reports a generic name."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break
+                key, _, val = line.partition(":")
+                fields[key.strip()] = val.strip()
     except OSError:
-        pass
-    return None
+        return None
+    name = fields.get("model name")
+    if name is None:
+        return None
+    ids = [f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields]
+    vendor = fields.get("vendor_id")
+    return f"{name} ({', '.join(([vendor] if vendor else []) + ids)})" if ids or vendor else name
 
 
 def cpu_baseline(model, args, qs, ks, vs, seconds):
@@ -148,6 +158,13 @@ def cpu_baseline(model, args, qs, ks, vs, seconds):
         s += 1
     times.sort()
     med_us = times[len(times) // 2] * 1e6
+    # the reference's own CPU-gather anchor, on the ids this run selected
+    from oracle.cpu_path import gather_anchor
+    groups = [model.last_ids_dev[i, 0, :model.last_n_selected].to("cpu", torch.int64)
+              for i in range(model.last_ids_dev.shape[0])]
+    counts = sorted({1, 2, 4, 8, min(os.cpu_count() or 1, torch.get_num_threads())})
+    anchor = gather_anchor(layers[0].flat_k, layers[0].flat_v, groups, threads=counts)
+    mib = 2 * groups[0].numel() * 64 * layers[0].flat_k.shape[1] * layers[0].flat_k.shape[2] * 2 / 2 ** 20
     return {
         "value": round(1e6 / (args.layers * med_us), 3),
         "unit": "tokens/s",
@@ -161,6 +178,15 @@ def cpu_baseline(model, args, qs, ks, vs, seconds):
         "sample": (f"{len(times)} layer-steps of the 32K workload ({n_sample} distinct layers, "
                    f"~{seconds:.0f} s): torch-CPU einsum scorer + topk + index_select gather + "
                    f"pack + fp32 einsum attention, median per layer-step x {args.layers} layers"),
+        "gather_anchor": {
+            "what": (f"reference CPU gather microbenchmark form (benchmark_m20_gather.py:88-99): "
+                     f"token-index index_select of {groups[0].numel()} selected blocks ({mib:.0f} MiB K+V) "
+                     f"from a pageable bf16 [{layers[0].nblocks}, 64, 8, 128] history into pinned staging, "
+                     f"cycling the {len(groups)} layers' ids of this run's last step; median us per gather"),
+            "us_by_threads": {str(n): round(t, 1) for n, t in anchor.items()},
+            "reference_us_by_threads": {"1": 871.77, "2": 632.35, "4": 378.28, "8": 315.31},
+            "reference_source": "docs/m20_gather_results.md:107-112 (RTX 3080 Laptop host CPU)",
+        },
     }
 
 

@@ -129,27 +129,34 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
   // every load first (the query row, and for per-channel int8 the K scales
   // of this lane's dims), then the scaled operands: a conversion between
   // them would make each load a round trip of its own
-  uint4 qv[4];
+  // int8 history segments take their keys as 16-byte loads of 32
+  // contiguous codes (dims [32 lg, +32) of a key row), so their MFMA step s
+  // contracts dims [32 lg + 8 s, +8): the int8 query operand bqs covers
+  // those dims (the contraction is over all 128 dims either way)
+  uint4 qv[4], qp[4];
   float4 ksc[4][2];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const int d0 = s * 32 + lg * 8;
+    const int dp = lg * 32 + s * 8;
     qv[s] = make_uint4(0u, 0u, 0u, 0u);
+    qp[s] = make_uint4(0u, 0u, 0u, 0u);
     if (row_ok) {
-      qv[s] = *reinterpret_cast<const uint4*>(
-          p.q + p.q_ls * layer + (static_cast<int64_t>(my_t) * hq + my_hq) * kHeadDim + d0);
+      const uint16_t* qrow = p.q + p.q_ls * layer + (static_cast<int64_t>(my_t) * hq + my_hq) * kHeadDim;
+      qv[s] = *reinterpret_cast<const uint4*>(qrow + d0);
+      if (FMT != NKV_KV_BF16) qp[s] = *reinterpret_cast<const uint4*>(qrow + dp);
     }
     if (FMT == NKV_KV_INT8_CHANNEL) {
       const float4* ks = reinterpret_cast<const float4*>(
-          p.k_scale + static_cast<int64_t>(layer) * p.hkv * kHeadDim + h * kHeadDim + d0);
+          p.k_scale + static_cast<int64_t>(layer) * p.hkv * kHeadDim + h * kHeadDim + dp);
       ksc[s][0] = ks[0];
       ksc[s][1] = ks[1];
     }
   }
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const uint4 v = qv[s];
-    bq[s] = as_bf16x8(v);
+    bq[s] = as_bf16x8(qv[s]);
+    const uint4 v = qp[s];
     if (FMT == NKV_KV_INT8_CHANNEL) {
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
       const float sc[8] = {ksc[s][0].x, ksc[s][0].y, ksc[s][0].z, ksc[s][0].w,
@@ -163,7 +170,7 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
       }
       bqs[s] = as_bf16x8(make_uint4(o[0], o[1], o[2], o[3]));
     } else {
-      bqs[s] = bq[s];
+      bqs[s] = FMT == NKV_KV_BF16 ? bq[s] : as_bf16x8(v);
     }
   }
 
@@ -231,7 +238,12 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
     float vs_blk = 1.0f;
     uint2 kts[4], vts[4];
     auto load_v = [&]() __attribute__((always_inline)) {
-      if (int8_seg) {
+      if (int8_seg && kMfmaPV) {
+        // 16 codes a lane: key 8 j + (lane >> 3), dims [16 (lane & 7), +16)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          va[j] = kv_load16<kStream>(g.vbase + min(8 * j + (lane >> 3), last) * g.rowb + (lane & 7) * 16);
+      } else if (int8_seg) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           const uint2 r = kv_load8<kStream>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 8);
@@ -244,12 +256,12 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
       }
     };
     if (int8_seg) {
-      uint2 ka[4][4];
+      uint4 kb[4][2];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 8;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) ka[i][s] = kv_load8<kStream>(rp + s * 32);
+        const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 32;
+        kb[i][0] = kv_load16<kStream>(rp);
+        kb[i][1] = kv_load16<kStream>(rp + 16);
       }
       if (kVEarly) load_v();
       if (FMT == NKV_KV_INT8_CHANNEL)
@@ -266,9 +278,12 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
       for (int i = 0; i < 4; ++i) {
         c[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          c[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(i8x8_to_bf16x8(ka[i][s].x, ka[i][s].y)),
-                                                          bqs[s], c[i], 0, 0, 0);
+        for (int s = 0; s < 4; ++s) {
+          const uint4 w = kb[i][s >> 1];
+          const uint32_t lo = (s & 1) ? w.z : w.x;
+          const uint32_t hi = (s & 1) ? w.w : w.y;
+          c[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(i8x8_to_bf16x8(lo, hi)), bqs[s], c[i], 0, 0, 0);
+        }
       }
     } else {
       uint4 ka[4][4];
@@ -366,10 +381,19 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
       // keeps fp32 accuracy.
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) oacc[dt] *= alpha;
+      if (int8_seg) {
+        // key 8 j + (lane >> 3): bf16 chunks 2 c and 2 c + 1 (c = lane & 7)
+        // at positions (2 c ^ 2 (key & 3)) and the next
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint4 vb = int8_seg ? i8x8_to_bf16x8(va[j].x, va[j].y) : va[j];
-        *reinterpret_cast<uint4*>(my_v + j * 1024 + vw) = vb;
+        for (int j = 0; j < 8; ++j) {
+          const int key = 8 * j + (lane >> 3);
+          char* dst = my_v + key * 256 + (((2 * (lane & 7)) ^ (2 * (key & 3))) << 4);
+          *reinterpret_cast<uint4*>(dst) = i8x8_to_bf16x8(va[j].x, va[j].y);
+          *reinterpret_cast<uint4*>(dst + 16) = i8x8_to_bf16x8(va[j].z, va[j].w);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) *reinterpret_cast<uint4*>(my_v + j * 1024 + vw) = va[j];
       }
       wave_lds_sync();
 #pragma unroll
@@ -530,11 +554,13 @@ template <int FMT>
 __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const AttendParams p) {
   constexpr int NCT = kWideRows / 16;   // MFMA column tiles
   constexpr bool kI8 = FMT != NKV_KV_BF16;
-  constexpr int kQCopies = FMT == NKV_KV_INT8_CHANNEL ? 2 : 1;
+  constexpr int kQCopies = kI8 ? 2 : 1;
   // V tiles of the four waves (16 KiB each), reused for the cross-wave merge
   __shared__ __attribute__((aligned(16))) char s_v[kAttendWaves * kVTileBytes];
-  // B operands: [copy][ct][s][lane] (copy 1: the K-scaled query of int8
-  // per-channel history); after the segment loop, the merge's m and l
+  // B operands: [copy][ct][s][lane] (copy 1, int8 history: the query over
+  // the dims its 16-byte key loads put in MFMA step s, [32 lg + 8 s, +8),
+  // K-scaled for per-channel scales); after the segment loop, the merge's m
+  // and l
   __shared__ __attribute__((aligned(16))) bf16x8 s_q[kQCopies][NCT][4][kWave];
   static_assert(sizeof(s_q) >= 2 * kAttendWaves * kWideRows * sizeof(float), "m, l fit the operand area");
   float (*s_ml)[kAttendWaves][kWideRows] = reinterpret_cast<float (*)[kAttendWaves][kWideRows]>(&s_q[0][0][0][0]);
@@ -582,20 +608,27 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
     for (int si = 0; si < 2; ++si) {
       const int s = 2 * (wave >> 1) + si;
       const int d0 = s * 32 + lg * 8;
+      const uint16_t* qrow = p.q + p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim;
       uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (ok) v = *reinterpret_cast<const uint4*>(p.q + p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d0);
+      if (ok) v = *reinterpret_cast<const uint4*>(qrow + d0);
       s_q[0][ct][s][lane] = as_bf16x8(v);
-      if constexpr (FMT == NKV_KV_INT8_CHANNEL) {
-        const float* ks = p.k_scale + static_cast<int64_t>(layer) * p.hkv * kHeadDim + h * kHeadDim + d0;
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-        uint32_t o[4];
+      if constexpr (kI8) {
+        const int dp = lg * 32 + s * 8;
+        uint4 vp = make_uint4(0u, 0u, 0u, 0u);
+        if (ok) vp = *reinterpret_cast<const uint4*>(qrow + dp);
+        if constexpr (FMT == NKV_KV_INT8_CHANNEL) {
+          const float* ks = p.k_scale + static_cast<int64_t>(layer) * p.hkv * kHeadDim + h * kHeadDim + dp;
+          const uint32_t w[4] = {vp.x, vp.y, vp.z, vp.w};
+          uint32_t o[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float a = bf16_lo(w[i]) * ks[2 * i];
-          const float b = bf16_hi(w[i]) * ks[2 * i + 1];
-          o[i] = static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+          for (int i = 0; i < 4; ++i) {
+            const float a = bf16_lo(w[i]) * ks[2 * i];
+            const float b = bf16_hi(w[i]) * ks[2 * i + 1];
+            o[i] = static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+          }
+          vp = make_uint4(o[0], o[1], o[2], o[3]);
         }
-        s_q[kQCopies - 1][ct][s][lane] = as_bf16x8(make_uint4(o[0], o[1], o[2], o[3]));
+        s_q[1][ct][s][lane] = as_bf16x8(vp);
       }
     }
   }
@@ -662,17 +695,18 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
     // the next segment's K loaded once Q.K^T is done (the copy form, whose V
     // holds no registers; measured no gain for int8 history's register form)
     constexpr bool prefetch_k = !reg_v;
-    typedef typename std::conditional<int8_seg, uint2, uint4>::type KReg;
-    const int qsel = (int8_seg && FMT == NKV_KV_INT8_CHANNEL) ? kQCopies - 1 : 0;
-    KReg ka[4][4];
+    const int qsel = int8_seg ? 1 : 0;
+    // bf16 keys: dims [32 s + 8 lg, +8) of key 16 i + ln in ka[i][s]; int8
+    // keys: 32 codes, dims [32 lg, +32), in ka[i][0..1] (16-byte loads)
+    uint4 ka[4][4];
     auto load_k = [&](const Seg& g) __attribute__((always_inline)) {
       const int last = g.len - 1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         if constexpr (int8_seg) {
-          const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 8;
-#pragma unroll
-          for (int s = 0; s < 4; ++s) ka[i][s] = kv_load8<false>(rp + s * 32);
+          const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 32;
+          ka[i][0] = kv_load16<false>(rp);
+          ka[i][1] = kv_load16<false>(rp + 16);
         } else {
           const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 16;
 #pragma unroll
@@ -702,12 +736,14 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
       // with K, so the segment's 16 KiB are in flight together, and so do the
       // block's V scale (per-channel form, a scalar load) or the fp16 K and V
       // scales of this lane's keys 16 i + 4 lg .. + 3 (per-token form)
-      uint2 va8[int8_seg ? 16 : 1];
+      // (int8 V: 16 codes a lane, key 8 j + (lane >> 3), dims [16 (lane & 7), +16))
+      uint4 va8[int8_seg ? 8 : 1];
       float vs_blk = 1.0f;
       uint2 kts[4], vts[4];
       if constexpr (int8_seg) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) va8[j] = kv_load8<false>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 8);
+        for (int j = 0; j < 8; ++j)
+          va8[j] = kv_load16<false>(g.vbase + min(8 * j + (lane >> 3), last) * g.rowb + (lane & 7) * 16);
         if (FMT == NKV_KV_INT8_CHANNEL)
           vs_blk = ((const cfloat*)p.v_scale)[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap + g.blk];
         if (FMT == NKV_KV_INT8_TOKEN) {
@@ -747,9 +783,10 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           bf16x8 a;
-          if constexpr (int8_seg)
-            a = as_bf16x8(i8x8_to_bf16x8(ka[i][s].x, ka[i][s].y));
-          else
+          if constexpr (int8_seg) {
+            const uint4 w = ka[i][s >> 1];
+            a = as_bf16x8(i8x8_to_bf16x8((s & 1) ? w.z : w.x, (s & 1) ? w.w : w.y));
+          } else
             a = as_bf16x8(ka[i][s]);
 #pragma unroll
           for (int ct = 0; ct < NCT; ++ct) c[i][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bq[ct], c[i][ct], 0, 0, 0);
@@ -844,10 +881,20 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
       for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) oacc[dt][ct] *= alpha[ct];
-      if constexpr (reg_v) {
+      if constexpr (reg_v && int8_seg) {
+        // key 8 j + (lane >> 3): bf16 chunks 2 c and 2 c + 1 (c = lane & 7)
+        // at positions (2 c ^ 2 (key & 3)) and the next
 #pragma unroll
-        for (int j = 0; j < 16; ++j)
-          *reinterpret_cast<uint4*>(my_v + j * 1024 + vw) = int8_seg ? i8x8_to_bf16x8(va8[j].x, va8[j].y) : va[j];
+        for (int j = 0; j < 8; ++j) {
+          const int key = 8 * j + (lane >> 3);
+          char* dst = my_v + key * 256 + (((2 * (lane & 7)) ^ (2 * (key & 3))) << 4);
+          *reinterpret_cast<uint4*>(dst) = i8x8_to_bf16x8(va8[j].x, va8[j].y);
+          *reinterpret_cast<uint4*>(dst + 16) = i8x8_to_bf16x8(va8[j].z, va8[j].w);
+        }
+        wave_lds_sync();
+      } else if constexpr (reg_v) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) *reinterpret_cast<uint4*>(my_v + j * 1024 + vw) = va[j];
         wave_lds_sync();
       } else {
         // the V copies have landed: they were issued before the next K loads

@@ -81,3 +81,40 @@ class CpuLayer:
         att = F.softmax(att, dim=-1)
         out = torch.einsum("thgs,shd->thgd", att, vf)
         return ids, out.reshape(1, hq, d).to(q.dtype)
+
+
+def gather_anchor(flat_k, flat_v, id_groups, threads=(1, 2, 4, 8), seconds_each=0.3, block_size=64):
+    """The reference's CPU gather microbenchmark (benchmarks/benchmark_m20_gather.py:88-99,
+    its "flat token-index" method): for each group of selected block ids,
+    token indices id * 64 + arange(64) gather K and V from the pageable
+    history [nb * 64, Hkv, D] into pinned staging with index_select -- 8 MiB
+    per group at 32 blocks, bf16 [*, 8, 128].  Returns {threads: median us
+    per gather}, cycling through the groups, ~seconds_each per thread count.
+    """
+    import time
+
+    n_tok = id_groups[0].numel() * block_size
+    pin = torch.cuda.is_available()
+    stage_k = torch.empty(n_tok, *flat_k.shape[1:], dtype=flat_k.dtype, pin_memory=pin)
+    stage_v = torch.empty_like(stage_k, pin_memory=pin)
+    ar = torch.arange(block_size, dtype=torch.long)
+    tok = [(ids.view(-1, 1) * block_size + ar).reshape(-1) for ids in id_groups]
+    saved = torch.get_num_threads()
+    out = {}
+    try:
+        for n in threads:
+            torch.set_num_threads(n)
+            times, i = [], 0
+            t_end = time.perf_counter() + seconds_each
+            while time.perf_counter() < t_end or len(times) < 5:
+                idx = tok[i % len(tok)]
+                t0 = time.perf_counter()
+                torch.index_select(flat_k, 0, idx, out=stage_k)
+                torch.index_select(flat_v, 0, idx, out=stage_v)
+                times.append(time.perf_counter() - t0)
+                i += 1
+            times.sort()
+            out[n] = times[len(times) // 2] * 1e6
+    finally:
+        torch.set_num_threads(saved)
+    return out

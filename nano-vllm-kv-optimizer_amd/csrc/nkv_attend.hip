@@ -39,6 +39,7 @@
 // Same result as the reference's gather + pack + fp32 einsum attention
 // (nanovllm/sparse/m12_runtime.py:1212-1320 and :845-896) up to fp32
 // summation order.
+#include <algorithm>
 #include <type_traits>
 
 #include "nkv_attend_common.h"
@@ -74,21 +75,30 @@ static_assert(2 * kAttendWaves * kMaxRows + kAttendWaves * 4 * kHeadDim <= kAtte
 // PACKED: caller-packed keys (nkv_attend_packed): the chunk's causal start is
 // causal_off and an optional per-token mask applies; its own instantiation,
 // so the decode and verify paths carry none of that code.
-template <int FMT, int M, bool PACKED>
+// STREAM: the stream form (see the end of the kernel); its own instantiation,
+// so the split form carries none of its loop.
+template <int FMT, int M, bool PACKED, bool STREAM = false>
 __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 1) void attend_kernel(const AttendParams p) {
   constexpr bool kMfmaPV = attend_mfma_pv<FMT, M>();
   __shared__ __attribute__((aligned(16))) float s_lds[kMfmaPV ? kAttendWaves * kVTileBytes / 4 : attend_lds_floats<M>()];
   __shared__ float s_alpha[kMfmaPV ? 1 : kAttendWaves][kMaxRows];
 
-  const int split = blockIdx.x;
-  const int h = blockIdx.y;
-  const int layer = blockIdx.z / p.nqg;
-  const int qg = blockIdx.z % p.nqg;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int ln = lane & 15;   // MFMA column / PV dim group
   const int lg = lane >> 4;   // MFMA row group / PV key residue
   const int hq = p.hkv * p.G;
+
+  // One (layer, KV head, query group): this wavefront attends its segments
+  // s_begin, s_begin + s_step, ... below s_end.  rec < 0 (split form): the
+  // four wavefronts then merge in LDS and the workgroup writes the output or
+  // its split partial; rec >= 0 (stream form): the wavefront writes its own
+  // partial record rec.  `duties`: this workgroup (split form: split 0) or
+  // wavefront (stream form: the one attending the group's first segment)
+  // also clears the layer's score keys and appends the decode token.
+  auto group = [&](const int layer, const int h, const int qg, const int s_begin, const int s_step, const int s_end,
+                   const bool duties, const int rec) __attribute__((always_inline)) {
+  constexpr bool stream = STREAM;
   const int q0 = qg * p.qpg;
   const int rows = min(p.qpg, p.tq - q0) * p.G;
 
@@ -102,14 +112,18 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
 
   // the decode step's score keys: read by its top-k launch, cleared here for
   // the next step's scoring (stream order makes both safe)
-  if (p.zero_keys != nullptr && split == 0 && h == 0 && qg == 0) {
+  if (p.zero_keys != nullptr && duties && h == 0 && qg == 0) {
     uint32_t* zk = p.zero_keys + static_cast<int64_t>(layer) * p.zero_n;
-    for (int i = threadIdx.x; i < p.zero_n; i += kAttendThreads) zk[i] = 0u;
+    if (stream) {
+      for (int i = lane; i < p.zero_n; i += kWave) zk[i] = 0u;
+    } else {
+      for (int i = threadIdx.x; i < p.zero_n; i += kAttendThreads) zk[i] = 0u;
+    }
   }
 
   // decode's shift+append: the new token (chunk token 0) also goes into the
   // freed ring slot, which no workgroup of this launch reads.
-  if (write_slot >= 0 && split == 0 && qg == 0 && wave == 0 && lane < 32) {
+  if (write_slot >= 0 && duties && qg == 0 && (stream || wave == 0) && lane < 32) {
     const int which = lane >> 4;
     const int c = lane & 15;
     const uint4* src = reinterpret_cast<const uint4*>(
@@ -126,26 +140,35 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
   const int my_t = q0 + (row_ok ? my_row / p.G : 0);
   const int my_hq = h * p.G + (my_row % p.G);
   bf16x8 bq[4], bqs[4];
-  // every load first (the query row, and for per-channel int8 the K scales
-  // of this lane's dims), then the scaled operands: a conversion between
-  // them would make each load a round trip of its own
   // int8 history segments take their keys as 16-byte loads of 32
   // contiguous codes (dims [32 lg, +32) of a key row), so their MFMA step s
   // contracts dims [32 lg + 8 s, +8): the int8 query operand bqs covers
-  // those dims (the contraction is over all 128 dims either way)
-  uint4 qv[4], qp[4];
+  // those dims (the contraction is over all 128 dims either way).  Its
+  // loads (the query row, and for per-channel int8 the K scales of this
+  // lane's dims) all issue before the scaled operands are formed: a
+  // conversion between them would make each load a round trip of its own.
+  // With int8 history the plain operand bq serves only the bf16 segments,
+  // which run after the int8 ones: it is loaded then (load_bq), so its
+  // registers are free during the int8 segments.
+  const uint16_t* my_qrow = p.q + p.q_ls * layer + (static_cast<int64_t>(my_t) * hq + my_hq) * kHeadDim;
+  auto load_bq = [&]() __attribute__((always_inline)) {
+    uint4 qv[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      qv[s] = make_uint4(0u, 0u, 0u, 0u);
+      if (row_ok) qv[s] = *reinterpret_cast<const uint4*>(my_qrow + s * 32 + lg * 8);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) bq[s] = as_bf16x8(qv[s]);
+  };
+  if (FMT == NKV_KV_BF16) load_bq();
+  uint4 qp[4];
   float4 ksc[4][2];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const int d0 = s * 32 + lg * 8;
-    const int dp = lg * 32 + s * 8;
-    qv[s] = make_uint4(0u, 0u, 0u, 0u);
+    const int dp = (s >> 1) * 64 + lg * 16 + (s & 1) * 8;
     qp[s] = make_uint4(0u, 0u, 0u, 0u);
-    if (row_ok) {
-      const uint16_t* qrow = p.q + p.q_ls * layer + (static_cast<int64_t>(my_t) * hq + my_hq) * kHeadDim;
-      qv[s] = *reinterpret_cast<const uint4*>(qrow + d0);
-      if (FMT != NKV_KV_BF16) qp[s] = *reinterpret_cast<const uint4*>(qrow + dp);
-    }
+    if (FMT != NKV_KV_BF16 && row_ok) qp[s] = *reinterpret_cast<const uint4*>(my_qrow + dp);
     if (FMT == NKV_KV_INT8_CHANNEL) {
       const float4* ks = reinterpret_cast<const float4*>(
           p.k_scale + static_cast<int64_t>(layer) * p.hkv * kHeadDim + h * kHeadDim + dp);
@@ -153,9 +176,12 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
       ksc[s][1] = ks[1];
     }
   }
+  // the int8 operand bqs: formed by the wave's first int8 segment once its
+  // key and value loads are in flight, so the wait for the query and scale
+  // loads does not hold them back
+  auto make_bqs = [&]() __attribute__((always_inline)) {
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    bq[s] = as_bf16x8(qv[s]);
     const uint4 v = qp[s];
     if (FMT == NKV_KV_INT8_CHANNEL) {
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -169,10 +195,11 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
         o[i] = static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
       }
       bqs[s] = as_bf16x8(make_uint4(o[0], o[1], o[2], o[3]));
-    } else {
-      bqs[s] = FMT == NKV_KV_BF16 ? bq[s] : as_bf16x8(v);
+    } else if (FMT != NKV_KV_BF16) {
+      bqs[s] = as_bf16x8(v);
     }
   }
+  };
 
   float m_run = -INFINITY;   // per query row (lane & 15); equal across lane groups
   float l_run = 0.0f;        // partial over this lane group's keys
@@ -197,7 +224,6 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
 #pragma unroll
   for (int q4 = 0; q4 < 4; ++q4)
     vtr[q4] = (4 * lg + (ln >> 2)) * 256 + ((2 * (q4 ^ (ln >> 2)) + ((ln & 3) >> 1)) << 4) + 8 * (ln & 1);
-  const int nwaves = p.splits * kAttendWaves;
   // History block ids are read through the constant address space (scalar
   // loads, counted by lgkmcnt), each one segment ahead: a vector load of the
   // id would be waited for with vmcnt(0) before the segment's K / V loads
@@ -210,8 +236,9 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
   // int8 history segments (always the first n_hist segments) and bf16
   // segments are two instantiations of the body, run by two loops in segment
   // order, so neither carries the other's registers.
-  auto segment = [&](const int sidx, const int blk, auto int8_tag) __attribute__((always_inline)) {
+  auto segment = [&](const int sidx, const int blk, auto int8_tag, auto first_tag) __attribute__((always_inline)) {
     constexpr bool int8_seg = decltype(int8_tag)::value;
+    constexpr bool first = decltype(first_tag)::value;
     const Seg g = make_seg_blk<FMT>(p, layer, h, sidx, blk);
     // an id outside the history attends nothing: no loads (a fully masked
     // segment would leave m, l and acc exactly as they are)
@@ -229,7 +256,7 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
     // block is read once per launch -> streamed past the caches (measured
     // +1-5% on the 32K bf16 step; slower for int8, whose 8-byte loads keep
     // the default policy)
-    constexpr bool kStream = (M == 4 && FMT == NKV_KV_BF16);
+    constexpr bool kStream = (M == 4);
     f32x4 c[4];
     uint4 va[16];
     // int8 history: the block's V scale (per-channel form, one scalar load)
@@ -259,9 +286,9 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
       uint4 kb[4][2];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 32;
+        const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 16;
         kb[i][0] = kv_load16<kStream>(rp);
-        kb[i][1] = kv_load16<kStream>(rp + 16);
+        kb[i][1] = kv_load16<kStream>(rp + 64);
       }
       if (kVEarly) load_v();
       if (FMT == NKV_KV_INT8_CHANNEL)
@@ -274,6 +301,7 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
           vts[i] = *reinterpret_cast<const uint2*>(p.v_tscale + tb + 16 * i);
         }
       }
+      if constexpr (first) make_bqs();
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         c[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -459,17 +487,31 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
     }
     wave_lds_sync();
   };
-  int sidx = split * kAttendWaves + wave;
+  int sidx = s_begin;
   int blk = id_at(sidx);
-  if (FMT != NKV_KV_BF16)
-    for (; sidx < p.n_hist; sidx += nwaves) {
-      const int nb = id_at(sidx + nwaves);   // in flight while this segment is attended
-      segment(sidx, blk, std::true_type{});
+  if constexpr (FMT != NKV_KV_BF16) {
+    const int i8_end = min(p.n_hist, s_end);
+    if (sidx < i8_end) {
+      const int nb = id_at(sidx + s_step);   // in flight while this segment is attended
+      // (an id outside the history attends nothing and issues no loads: bqs
+      // is then formed at once)
+      if (blk >= 0 && blk < p.cap)
+        segment(sidx, blk, std::true_type{}, std::true_type{});
+      else
+        make_bqs();
+      blk = nb;
+      sidx += s_step;
+    }
+    for (; sidx < i8_end; sidx += s_step) {
+      const int nb = id_at(sidx + s_step);
+      segment(sidx, blk, std::true_type{}, std::false_type{});
       blk = nb;
     }
-  for (; sidx < p.nseg; sidx += nwaves) {
-    const int nb = id_at(sidx + nwaves);
-    segment(sidx, blk, std::false_type{});
+    load_bq();
+  }
+  for (; sidx < s_end; sidx += s_step) {
+    const int nb = id_at(sidx + s_step);
+    segment(sidx, blk, std::false_type{}, std::false_type{});
     blk = nb;
   }
 
@@ -484,6 +526,22 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
         acc[n][e] += __shfl_xor(acc[n][e], 16);
         acc[n][e] += __shfl_xor(acc[n][e], 32);
       }
+  }
+
+  if constexpr (kMfmaPV && stream) {
+    // the wavefront's own partial record: m, l, acc of rows ln < rows
+    if (ln < rows) {
+      float* part = p.partial + (static_cast<int64_t>(rec) * p.prow + ln) * kPartStride;
+      if (lg == 0) {
+        part[0] = m_run;
+        part[1] = l_run;
+      }
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[2 + 16 * dt + 4 * lg + i] = oacc[dt][i];
+    }
+    return;
   }
 
   // ---- merge the 4 wavefronts in LDS (reusing the p tiles) -----------------
@@ -530,13 +588,36 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
       const int hh = h * p.G + n % p.G;
       p.out[p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d] = f32_to_bf16(A / L);
     } else {
-      float* part = p.partial + ((grp * p.splits + split) * p.prow + n) * kPartStride;
+      float* part = p.partial + ((grp * p.splits + s_begin / kAttendWaves) * p.prow + n) * kPartStride;
       part[2 + d] = A;
       if (d == 0) {
         part[0] = mt;
         part[1] = L;
       }
     }
+  }
+  };
+
+  if constexpr (STREAM && kMfmaPV && !PACKED) {
+    // Stream form: wavefront w attends items [w ipw, (w + 1) ipw) of the
+    // list of every group's segments (group g = (layer Hkv + h) nqg + qg owns
+    // items [g nseg, (g + 1) nseg)) and writes one partial record per group
+    // it touches, record w + g (distinct: a later wavefront never starts in
+    // an earlier group).  The host keeps the item count below 2^31.
+    const int w = static_cast<int>(blockIdx.x) * kAttendWaves + wave;
+    const int lo = w * p.stream_ipw;
+    const int hi = min(lo + p.stream_ipw, p.nlayers * p.hkv * p.nqg * p.nseg);
+#pragma unroll 1
+    for (int g = lo / p.nseg; g * p.nseg < hi; ++g) {
+      const int lh = g / p.nqg;
+      const int sb = max(lo - g * p.nseg, 0);
+      group(lh / p.hkv, lh % p.hkv, g % p.nqg, sb, 1, min(hi - g * p.nseg, p.nseg), sb == 0, w + g);
+    }
+  } else {
+    // split form: wavefront w of split s attends segments w + 4 s,
+    // w + 4 s + 4 splits, ...
+    group(blockIdx.z / p.nqg, blockIdx.y, blockIdx.z % p.nqg, blockIdx.x * kAttendWaves + wave,
+          p.splits * kAttendWaves, p.nseg, blockIdx.x == 0, -1);
   }
 }
 
@@ -613,7 +694,7 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
       if (ok) v = *reinterpret_cast<const uint4*>(qrow + d0);
       s_q[0][ct][s][lane] = as_bf16x8(v);
       if constexpr (kI8) {
-        const int dp = lg * 32 + s * 8;
+        const int dp = (s >> 1) * 64 + lg * 16 + (s & 1) * 8;
         uint4 vp = make_uint4(0u, 0u, 0u, 0u);
         if (ok) vp = *reinterpret_cast<const uint4*>(qrow + dp);
         if constexpr (FMT == NKV_KV_INT8_CHANNEL) {
@@ -704,9 +785,9 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         if constexpr (int8_seg) {
-          const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 32;
+          const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 16;
           ka[i][0] = kv_load16<false>(rp);
-          ka[i][1] = kv_load16<false>(rp + 16);
+          ka[i][1] = kv_load16<false>(rp + 64);
         } else {
           const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 16;
 #pragma unroll
@@ -943,7 +1024,7 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
     }
   };
   int sidx = split * kAttendWaves + wave;
-  if (kI8) sidx = run_phase(sidx, p.n_hist, std::true_type{});
+  if constexpr (kI8) sidx = run_phase(sidx, p.n_hist, std::true_type{});
   run_phase(sidx, p.nseg, std::false_type{});
 
   // ---- merge the 4 wavefronts in LDS (reusing the V tiles) -----------------
@@ -1025,17 +1106,27 @@ __global__ __launch_bounds__(kMergeThreads) void attend_merge_kernel(const Atten
   }
   if (n >= rows) return;
   const int64_t grp = (static_cast<int64_t>(layer) * p.hkv + h) * p.nqg + qg;
-  const float* base = p.partial + (grp * p.splits * p.prow + n) * kPartStride;
+  // split form: records grp * splits .. + splits - 1; stream form: the
+  // wavefronts wf .. wl whose item ranges meet the group's, records w + grp
+  int64_t first = grp * p.splits;
+  int nrec = p.splits;
+  if (p.stream_ipw > 0) {
+    const int64_t wf = grp * p.nseg / p.stream_ipw;
+    const int64_t wl = ((grp + 1) * p.nseg - 1) / p.stream_ipw;
+    first = wf + grp;
+    nrec = static_cast<int>(wl - wf + 1);
+  }
+  const float* base = p.partial + (first * p.prow + n) * kPartStride;
   const int64_t sstride = static_cast<int64_t>(p.prow) * kPartStride;
   float L = 0.0f, A0 = 0.0f, A1 = 0.0f;
-  // up to 8 splits at a time: all their loads in flight together
+  // up to 8 records at a time: all their loads in flight together
   float mt = -INFINITY;
-  for (int s0 = 0; s0 < p.splits; s0 += 8) {
+  for (int s0 = 0; s0 < nrec; s0 += 8) {
     float m[8], l[8];
     float2 a[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int s = min(s0 + i, p.splits - 1);
+      const int s = min(s0 + i, nrec - 1);
       const float* ps = base + s * sstride;
       m[i] = ps[0];
       l[i] = ps[1];
@@ -1045,7 +1136,7 @@ __global__ __launch_bounds__(kMergeThreads) void attend_merge_kernel(const Atten
     float mb = mt;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      if (s0 + i < p.splits) mb = fmaxf(mb, m[i]);
+      if (s0 + i < nrec) mb = fmaxf(mb, m[i]);
     // rescale what the earlier batches summed to the new reference max
     const float r = (mt == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mt - mb);
     L *= r;
@@ -1053,7 +1144,7 @@ __global__ __launch_bounds__(kMergeThreads) void attend_merge_kernel(const Atten
     A1 *= r;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      if (s0 + i >= p.splits) break;
+      if (s0 + i >= nrec) break;
       const float sw = (m[i] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m[i] - mb);
       L += l[i] * sw;
       A0 += a[i].x * sw;
@@ -1079,6 +1170,11 @@ __global__ __launch_bounds__(kWave) void ring_advance_kernel(int32_t* ring_start
 
 template <int FMT, bool PACKED = false>
 int launch_fmt(int M, dim3 grid, hipStream_t s, const AttendParams& p) {
+  if (p.stream_ipw > 0) {
+    if (M != 4 || PACKED) return -1;
+    hipLaunchKernelGGL((attend_kernel<FMT, 4, false, true>), grid, dim3(kAttendThreads), 0, s, p);
+    return 0;
+  }
   switch (M) {
     case 4: hipLaunchKernelGGL((attend_kernel<FMT, 4, PACKED>), grid, dim3(kAttendThreads), 0, s, p); return 0;
     case 8: hipLaunchKernelGGL((attend_kernel<FMT, 8, PACKED>), grid, dim3(kAttendThreads), 0, s, p); return 0;
@@ -1123,6 +1219,25 @@ int launch_grouped(int hkv, int kv_format, int num_layers, int tq, AttendParams&
   int bad = 0;
   const bool packed = p.tok_mask != nullptr || p.causal_off != 0;
   NKV_CHECK_SUPPORTED(!packed || kv_format == NKV_KV_BF16, "nkv_attend: caller-packed keys must be bf16");
+  if (p.splits == 0) {
+    // stream form: one resident round of wavefronts (two workgroups per CU)
+    // share the segment list evenly
+    NKV_CHECK_SUPPORTED(M == 4 && !packed,
+                        "nkv_attend: the stream form (splits 0) takes groups of at most 4 query rows and no "
+                        "caller-packed keys (got %d rows%s)", qpg * p.G, packed ? ", packed keys" : "");
+    const int cus = device_cus();
+    const int64_t waves = cus > 0 ? std::min<int64_t>(static_cast<int64_t>(cus) * 4 * NKV_ATTEND_DECODE_WAVES,
+                                                      kStreamWavesMax)
+                                  : kStreamWavesMax;
+    const int64_t total = static_cast<int64_t>(num_layers) * hkv * p.nqg * p.nseg;
+    const int64_t ipw = (total + waves - 1) / waves;
+    NKV_CHECK_SUPPORTED(total + ipw < (int64_t{1} << 31),
+                        "nkv_attend: %lld segments are too many for the stream form", static_cast<long long>(total));
+    p.stream_ipw = static_cast<int>(ipw);
+    p.prow = kStreamRows;
+    const int64_t used = (total + ipw - 1) / ipw;
+    grid = dim3(static_cast<unsigned>((used + kAttendWaves - 1) / kAttendWaves), 1, 1);
+  }
   switch (kv_format) {
     case NKV_KV_BF16:
       bad = packed ? launch_fmt<NKV_KV_BF16, true>(M, grid, s, p) : launch_fmt<NKV_KV_BF16>(M, grid, s, p);
@@ -1132,7 +1247,7 @@ int launch_grouped(int hkv, int kv_format, int num_layers, int tq, AttendParams&
     default: bad = -1;
   }
   NKV_CHECK_SUPPORTED(bad == 0, "nkv_attend: unsupported row count %d / kv_format %d", M, kv_format);
-  if (p.splits > 1)
+  if (p.splits != 1)
     hipLaunchKernelGGL(attend_merge_kernel, dim3(hkv, num_layers * p.nqg, (qpg * p.G + kMergeRows - 1) / kMergeRows),
                        dim3(kMergeThreads), 0, s, p);
   return NKV_OK;
@@ -1144,10 +1259,16 @@ using namespace nkv;
 
 extern "C" int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads, int num_heads,
                                                int tq, int splits) {
-  if (num_layers < 1 || num_kv_heads < 1 || num_heads < num_kv_heads || tq < 1 || splits < 1) return 0;
+  if (num_layers < 1 || num_kv_heads < 1 || num_heads < num_kv_heads || tq < 1 || splits < 0) return 0;
   int qpg, M;
   group_shape(tq, num_heads / num_kv_heads, &qpg, &M);
   const int64_t nqg = (tq + qpg - 1) / qpg;
+  if (splits == 0) {
+    // stream form: at most one record per resident wavefront and group
+    // boundary (records w + g, w < kStreamWavesMax, g < groups)
+    if (M != 4) return 0;
+    return (kStreamWavesMax + static_cast<int64_t>(num_layers) * num_kv_heads * nqg) * kStreamRows * kPartStride;
+  }
   const int prow = M > kMaxRows ? kWideRows : kMaxRows;
   return static_cast<int64_t>(num_layers) * num_kv_heads * nqg * splits * prow * kPartStride;
 }
@@ -1187,8 +1308,8 @@ int fill_attend_params(const char* who, const nkv_store* st, int layer0, int num
     NKV_CHECK_ARG(lp < rec_lo || lp >= rec_lo + rec_len,
                   "%s: write_slot %d lies inside the attended recent window", who, write_slot);
   }
-  NKV_CHECK_ARG(splits >= 1 && splits <= 64, "%s: splits must be in [1, 64] (got %d)", who, splits);
-  NKV_CHECK_ARG(splits == 1 || partial_ws != nullptr, "%s: splits > 1 needs partial_ws", who);
+  NKV_CHECK_ARG(splits >= 0 && splits <= 64, "%s: splits must be in [0, 64] (got %d; 0 = stream form)", who, splits);
+  NKV_CHECK_ARG(splits == 1 || partial_ws != nullptr, "%s: splits != 1 needs partial_ws", who);
   const int n_sink_seg = (sink_len + kBlock - 1) / kBlock;
   const int n_rec_seg = rec_len > 0 ? (R + kBlock - 1) / kBlock : 0;
   const int n_chunk_seg = (n_chunk + kBlock - 1) / kBlock;
@@ -1253,6 +1374,8 @@ int fill_attend_params(const char* who, const nkv_store* st, int layer0, int num
   p.zero_n = 0;
   p.ids_tile_ls = 0;
   p.sel_tile = 0;
+  p.stream_ipw = 0;
+  p.nlayers = num_layers;
   return NKV_OK;
 }
 
@@ -1326,7 +1449,7 @@ extern "C" int nkv_decode_step_ring(const nkv_store* st, int layer0, int num_lay
     p.zero_n = nblocks;
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  rc = launch_grouped(st->num_kv_heads, st->kv_format, num_layers, 1, p, s);   // with splits > 1 the merge advances the ring
+  rc = launch_grouped(st->num_kv_heads, st->kv_format, num_layers, 1, p, s);   // with splits != 1 the merge advances the ring
   if (rc != NKV_OK) return rc;
   if (splits == 1)
     hipLaunchKernelGGL(ring_advance_kernel, dim3((num_layers + kWave - 1) / kWave), dim3(kWave), 0, s, ring_start,

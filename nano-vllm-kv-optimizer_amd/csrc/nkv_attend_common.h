@@ -18,6 +18,8 @@ constexpr int kPRow = 20;        // floats per key row of the p tile in LDS (16 
 constexpr int kPartStride = 130; // floats per partial row: m, l, acc[128]
 constexpr int kMaxRows = 16;     // MFMA N: query rows per group
 constexpr int kWideRows = 32;    // query rows per group of the two-tile (wide) few-query kernel
+constexpr int kStreamRows = 4;   // rows per partial record of the 4-row kernel's stream form
+constexpr int64_t kStreamWavesMax = 2048;  // wavefronts a stream-form launch uses at most
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -75,8 +77,14 @@ struct AttendParams {
   int64_t ids_tile_ls;
   int sel_tile;
   // few-query kernels: partial records per (group, split) -- the group's row
-  // capacity (kMaxRows, or kWideRows for the wide kernel)
+  // capacity (kMaxRows, or kWideRows for the wide kernel; 4 in the stream
+  // form)
   int prow;
+  // the 4-row kernel's stream form (stream_ipw > 0): wavefront w attends
+  // items [w stream_ipw, (w + 1) stream_ipw) of the nlayers x hkv x nqg x
+  // nseg segment list
+  int stream_ipw;
+  int nlayers;
 };
 
 __device__ __forceinline__ void wave_lds_sync() {

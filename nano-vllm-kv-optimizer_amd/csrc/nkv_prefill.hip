@@ -676,6 +676,7 @@ void launch_prefill_fmt(int cols, const dim3& grid, AttendParams& p, int nqt, hi
 // The matrix-core kernel over (query tile x KV head, layer, split), then the
 // split merge.
 int launch_prefill(int hkv, int kv_format, int num_layers, int tq, AttendParams& p, hipStream_t s) {
+  NKV_CHECK_ARG(p.splits >= 1, "nkv_prefill_attend: splits must be in [1, 64] (got %d)", p.splits);
   NKV_CHECK_SUPPORTED(p.G >= 1 && kPfCols % p.G == 0,
                       "nkv_prefill_attend: query heads per KV head (%d) must divide %d", p.G, kPfCols);
   const int cols = prefill_cols(p, tq);

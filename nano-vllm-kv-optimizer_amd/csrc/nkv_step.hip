@@ -155,7 +155,7 @@ extern "C" int nkv_decode_step(const nkv_store* st, int layer0, int num_layers, 
                     out_ids != nullptr && out != nullptr,
                 "nkv_decode_step: q, k_new, v_new, score_keys, out_ids and out must be non-NULL");
   NKV_CHECK_ARG(n_hist >= 1 && n_hist <= k, "nkv_decode_step: n_hist must be in [1, k] (got %d, k=%d)", n_hist, k);
-  NKV_CHECK_ARG(splits > 1 ? partial_ws != nullptr : true, "nkv_decode_step: splits > 1 needs partial_ws");
+  NKV_CHECK_ARG(splits != 1 ? partial_ws != nullptr : true, "nkv_decode_step: splits != 1 needs partial_ws");
   const int nranges = nstreams < num_layers ? nstreams : num_layers;
 
   // contiguous per-layer strides: q/out [L][1][Hq][D], k/v [L][1][Hkv][D],
@@ -226,7 +226,7 @@ extern "C" int nkv_decode_step_noalloc(const nkv_store* st, int layer0, int num_
   int rc = check_store(st, layer0, num_layers);
   if (rc != NKV_OK) return rc;
   NKV_CHECK_ARG(nblocks >= 1, "nkv_decode_step_noalloc: nblocks must be >= 1 (got %d)", nblocks);
-  NKV_CHECK_ARG(splits >= 1 && splits <= 64, "nkv_decode_step_noalloc: splits must be in [1, 64] (got %d)", splits);
+  NKV_CHECK_ARG(splits >= 0 && splits <= 64, "nkv_decode_step_noalloc: splits must be in [0, 64] (got %d; 0 = stream form)", splits);
   NKV_CHECK_ARG(static_cast<int64_t>(num_layers) * nblocks <= kScratchKeys,
                 "nkv_decode_step_noalloc: num_layers x nblocks = %lld exceeds the scratch's %lld score keys",
                 static_cast<long long>(num_layers) * nblocks, static_cast<long long>(kScratchKeys));

@@ -368,11 +368,21 @@ class _SparseCore:
         return ids, vals, self.effective_k(requested)
 
     # -- attention ------------------------------------------------------------
+    # the stream form pays off once every resident wavefront gets a couple of
+    # segments (one round of ~2048 wavefronts on an MI355X)
+    STREAM_MIN_SEGMENTS = 4096
+
     def _splits(self, nseg: int, nqg: int, rows: int = 4) -> int:
         """Attention split count for nseg segments per (layer, KV head, query
-        group); rows = query rows per group (17-32: the wide few-query kernel)."""
+        group); rows = query rows per group (17-32: the wide few-query kernel).
+        0 = the 4-row kernel's stream form: one resident round of wavefronts
+        shares the launch's whole segment list evenly (no second, partly
+        filled round of workgroups, no wavefront idling at its workgroup's
+        merge)."""
         if self.cfg.attend_splits is not None:
             return self.cfg.attend_splits
+        if rows <= 4 and self.nl * self.store.num_kv_heads * nqg * nseg >= self.STREAM_MIN_SEGMENTS:
+            return 0
         # Workgroups per launch measured best on the 36-layer 32K decode step
         # (tok/s, splits 2 / 3 / 5 / 6 / 7 / 9): bf16 ~1440 (8382 / 8827 /
         # 9261 / 9141 / 8992 / 8838); both int8 forms, whose segments carry

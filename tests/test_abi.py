@@ -202,6 +202,7 @@ def test_noalloc_decode_step_rejects_sizes_beyond_its_scratch_without_device_wor
     assert call(64, 4097, 1) == _lib.NKV_ERR_ARG and b"score keys" in lib.nkv_last_error()
     # 36 layers x 8 heads x 7 splits of 16 x 130 floats = 4193280 > 3932160
     assert call(36, 512, 7) == _lib.NKV_ERR_ARG and b"split partials" in lib.nkv_last_error()
-    assert call(36, 512, 0) == _lib.NKV_ERR_ARG
+    # splits 0 is the stream form; below 0 or above 64 is refused
+    assert call(36, 512, -1) == _lib.NKV_ERR_ARG and call(36, 512, 65) == _lib.NKV_ERR_ARG
     with pytest.raises(ValueError, match="score keys"):
         _lib.check(call(64, 4097, 1), "decode_step_noalloc")

@@ -49,16 +49,23 @@ def test_kv_format_mapping():
 
 def _split_choice(nseg, layers=36, kv_heads=8, nqg=1, rows=4, **cfg):
     from types import SimpleNamespace
-    me = SimpleNamespace(cfg=rt.M12Config(**cfg), store=SimpleNamespace(num_kv_heads=kv_heads), nl=layers)
+    me = SimpleNamespace(cfg=rt.M12Config(**cfg), store=SimpleNamespace(num_kv_heads=kv_heads), nl=layers,
+                         STREAM_MIN_SEGMENTS=rt._SparseCore.STREAM_MIN_SEGMENTS)
     return rt._SparseCore._splits(me, nseg, nqg, rows)
 
 
 def test_decode_split_choice():
-    # 36 layers x 8 KV heads, top-32 + sink + 8 recent pieces = 41 segments
-    assert _split_choice(41) == 5                              # ~1440 workgroups
-    assert _split_choice(41, quant_history=True) == 3          # per-block int8: ~900
-    assert _split_choice(41, quant_history=True, quant_scale_layout="token") == 3   # per-token int8: ~900
+    # 36 layers x 8 KV heads, top-32 + sink + 8 recent pieces = 41 segments:
+    # 11808 segments, the stream form (0) in every history format
+    assert _split_choice(41) == 0
+    assert _split_choice(41, quant_history=True) == 0
+    assert _split_choice(41, quant_history=True, quant_scale_layout="token") == 0
     assert _split_choice(41, attend_splits=8) == 8             # explicit choice kept
+    # below 4096 segments the split form: ~1440 workgroups (bf16), ~900 (int8),
+    # at most one segment per wavefront (12 layers: 11 splits cap bf16's 15)
+    assert _split_choice(41, layers=12) == 11
+    assert _split_choice(41, layers=12, quant_history=True) == 9
+    assert _split_choice(41, layers=13) == 0                   # 13 x 8 x 41 = 4264
     # verify: 6 draft tokens x 4 heads = 24 rows on the wide kernel, 16K history
     # (139 union blocks + sink + 8 recent pieces + the draft chunk = 149 segments)
     assert _split_choice(149, rows=24) == 3                     # bf16: ~900 as well
@@ -67,6 +74,9 @@ def test_decode_split_choice():
     for layers in range(1, 80):
         for nseg in (1, 5, 16, 41, 300):
             s = _split_choice(nseg, layers=layers)
+            if layers * 8 * nseg >= 4096:
+                assert s == 0                                    # the stream form
+                continue
             assert 1 <= s <= max(1, min(-(-nseg // 4), 64))    # at most one segment per wavefront
             assert s == 1 or s % 4 != 0                          # never a multiple of 4
     assert _split_choice(16, layers=4) == 3                    # cap 4 is a multiple of 4: one less

@@ -146,7 +146,13 @@ int nkv_select(const nkv_store* st, int layer0, int num_layers,
  * splits : workgroups per (layer, KV head, query group), 1..64; with
  *          splits > 1 a second kernel on the same stream merges the partial
  *          softmax states.  Queries are processed in groups of 16/G per
- *          workgroup (grid z = layers x groups).
+ *          workgroup (grid z = layers x groups).  splits = 0 (groups of at
+ *          most 4 query rows, tq * G <= 4, e.g. one decode token at G = 4):
+ *          the stream form -- one resident round of wavefronts (two
+ *          workgroups per CU, at most 2048 wavefronts) takes equal runs of
+ *          the launch's whole segment list, each writing one partial per
+ *          (layer, KV head, group) it touches, and the merge kernel
+ *          combines them; other shapes return NKV_ERR_UNSUPPORTED.
  * Constraints: 1 <= tq <= 65536, n_hist <= 4096, n_chunk in {0, tq};
  *          fp32 softmax and accumulation.
  */
@@ -186,8 +192,9 @@ int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads, int num_he
  * score_keys : as nkv_select, [num_layers][nblocks].
  * out_ids    : int32 [num_layers][k]; n_hist: the ids attended per layer
  *              (k_eff of nkv_select, 1 <= n_hist <= k).
- * sink_len, write_slot, ring_base, rec_lo, rec_len, scale, splits: as nkv_attend.
- * partial_ws : >= nkv_decode_step_workspace_floats(...) floats (splits > 1).
+ * sink_len, write_slot, ring_base, rec_lo, rec_len, scale, splits: as nkv_attend
+ *          (splits 0: the stream form).
+ * partial_ws : >= nkv_decode_step_workspace_floats(...) floats (splits != 1).
  */
 int nkv_decode_step(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
                     const uint16_t* k_new, const uint16_t* v_new, int nblocks,
@@ -212,7 +219,8 @@ int64_t nkv_decode_step_workspace_floats(int num_layers, int num_kv_heads, int n
  * 1 MiB of score keys (num_layers x nblocks <= 262144) and 15 MiB of split
  * partials (nkv_attend_workspace_floats(num_layers, Hkv, Hq, 1, splits) <=
  * 3932160 floats: 16 x 130 per layer, KV head and split, e.g. 36 layers x 8
- * KV heads x up to 6 splits).  Larger sizes
+ * KV heads x up to 6 splits; the stream form, splits 0, needs
+ * (2048 + num_layers x Hkv) x 4 x 130).  Larger sizes
  * are rejected with NKV_ERR_ARG before any device work.  The first call on a
  * device looks the array up (hipGetSymbolAddress) and clears its key region
  * with a fill kernel on `stream`; every call leaves the keys it used at zero.
@@ -242,7 +250,7 @@ int nkv_decode_step_noalloc(const nkv_store* st, int layer0, int num_layers, con
  *              each entry by one slot (mod R).
  * score_keys : as nkv_select, [num_layers][nblocks].
  * partial_ws : >= nkv_attend_workspace_floats(num_layers, Hkv, Hq, 1, splits)
- *              floats (splits > 1).
+ *              floats (splits != 1; splits 0: the stream form).
  * Other arguments as nkv_decode_step.
  */
 int nkv_decode_step_ring(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,

@@ -1,8 +1,9 @@
 """nkv_decode_step_noalloc (scratch in the library's device array) against
 nkv_decode_step with caller-allocated workspaces: two calls in a row, the
 second on a smaller model (fewer layers, a shorter history, fewer splits),
-each compared bit for bit with the allocating entry point on the same state
-(same kernels and launch shapes, so ids and outputs are identical)."""
+then a third in the attention's stream form (splits 0), each compared bit
+for bit with the allocating entry point on the same state (same kernels and
+launch shapes, so ids and outputs are identical)."""
 
 import ctypes
 
@@ -59,8 +60,10 @@ def _both(model, q, k, v, splits):
 
 def test_noalloc_decode_step_matches_the_allocating_entry_twice_in_a_row():
     from nanokv_amd import workload
-    # call 1: 6 layers x 16K history, 5 splits; call 2: 2 layers x 4K, 3 splits
-    for L, T, splits, seed in ((6, 16384, 5, 900), (2, 4096, 3, 950)):
+    # call 1: 6 layers x 16K history, 5 splits; call 2: 2 layers x 4K, 3 splits;
+    # call 3: 12 layers x 16K in the stream form (splits 0: one record per
+    # wavefront and group in the partial region)
+    for L, T, splits, seed in ((6, 16384, 5, 900), (2, 4096, 3, 950), (12, 16384, 0, 970)):
         model = _model(L, T, seed)
         qs, ks, vs = workload.decode_inputs(2, seed + 1, layers=L)
         for s in range(2):

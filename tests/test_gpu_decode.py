@@ -237,6 +237,33 @@ def test_layer_streams_identical_to_one_stream(streams):
         assert many.valid_len == one.valid_len
 
 
+def test_layer_streams_in_the_stream_form():
+    """With 16 layers the step's attention takes the stream form, whose
+    partition of the segment list depends on the layers a launch holds: over
+    two streams (two launches of 8 layers) the selected ids are identical and
+    the outputs agree with the one-stream step to one bf16 ulp."""
+    from nanokv_amd import workload
+    from nanokv_amd.sparse import M12Config, M12ModelRuntime
+    L, T, steps = 16, 8192, 3
+    cfg = M12Config(max_model_len=T + 64)
+    one = M12ModelRuntime(L, cfg, layer_streams=1)
+    two = M12ModelRuntime(L, cfg, layer_streams=2)
+    hist = [workload.history(T, 400 + i) for i in range(L)]
+    k = torch.stack([h[0] for h in hist]).cuda()
+    v = torch.stack([h[1] for h in hist]).cuda()
+    one.prefill(k, v)
+    two.prefill(k, v)
+    assert one.core.decode_splits(one.core.effective_k(cfg.top_k_blocks)) == 0
+    qs, ks, vs = workload.decode_inputs(steps, 13, layers=L)
+    for s in range(steps):
+        q, kk, vv = qs[s].cuda(), ks[s].cuda(), vs[s].cuda()
+        a = one.decode(q, kk, vv).float().cpu()
+        b = two.decode(q, kk, vv).float().cpu()
+        n = one.last_n_selected
+        assert torch.equal(one.last_ids_dev[:, :, :n], two.last_ids_dev[:, :, :n])
+        assert ((a - b).abs() <= 2.0 ** -7 * b.abs() + 2e-6).all()
+
+
 @pytest.mark.parametrize("quant", [False, True])
 def test_decode_step_selection_with_tied_scores(quant):
     """nkv_decode_step's selection (protected blocks left unscored by the

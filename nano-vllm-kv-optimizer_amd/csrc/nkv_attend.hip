@@ -507,9 +507,25 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
     wave_lds_sync();
   };
   int sidx = s_begin;
+  int i8_end = min(p.n_hist, s_end);
+  int bf_begin = -1, bf_end = s_end;
+  if constexpr (stream && FMT != NKV_KV_BF16) {
+    // A stream-form run [s_begin, s_end) of the group's items, read as an
+    // even interleaving of its int8 history segments (16 KiB each) and its
+    // bf16 sink / recent / chunk segments (32 KiB): of the group's first x
+    // items, floor(x nb / nseg) are bf16 (nb = nseg - n_hist), kept in order
+    // within each kind.  Consecutive runs still partition both kinds, and
+    // every wavefront carries about the same bytes (in segment order the
+    // wavefronts at a group's end took only bf16 segments, twice the bytes).
+    const int nb16 = p.nseg - p.n_hist;
+    const int c0 = (s_begin * nb16) / p.nseg, c1 = (s_end * nb16) / p.nseg;
+    sidx = s_begin - c0;
+    i8_end = s_end - c1;
+    bf_begin = p.n_hist + c0;
+    bf_end = p.n_hist + c1;
+  }
   int blk = id_at(sidx);
   if constexpr (FMT != NKV_KV_BF16) {
-    const int i8_end = min(p.n_hist, s_end);
     if (sidx < i8_end) {
       const int nb = id_at(sidx + s_step);   // in flight while this segment is attended
       // (an id outside the history attends nothing and issues no loads: bqs
@@ -527,8 +543,9 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
       blk = nb;
     }
     load_bq();
+    if (bf_begin >= 0) sidx = bf_begin;
   }
-  for (; sidx < s_end; sidx += s_step) {
+  for (; sidx < bf_end; sidx += s_step) {
     const int nb = id_at(sidx + s_step);
     segment(sidx, blk, std::false_type{}, std::false_type{});
     blk = nb;

@@ -152,7 +152,13 @@ int nkv_select(const nkv_store* st, int layer0, int num_layers,
  *          workgroups per CU, at most 2048 wavefronts) takes equal runs of
  *          the launch's whole segment list, each writing one partial per
  *          (layer, KV head, group) it touches, and the merge kernel
- *          combines them; other shapes return NKV_ERR_UNSUPPORTED.
+ *          combines them.  splits = 0 with 17-32 query rows per group
+ *          (the wide few-query kernel, e.g. verify's 6 draft tokens at
+ *          G = 4): a tiered plan -- the first groups in larger pieces
+ *          filling one round of workgroups, the rest in pieces about 3/4
+ *          that size filling a second (one workgroup per group once the
+ *          groups alone fill the device).  Other shapes return
+ *          NKV_ERR_UNSUPPORTED.
  * Constraints: 1 <= tq <= 65536, n_hist <= 4096, n_chunk in {0, tq};
  *          fp32 softmax and accumulation.
  */

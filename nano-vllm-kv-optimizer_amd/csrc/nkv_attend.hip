@@ -22,6 +22,11 @@
 // 68.4 us, int8 58.4 -> 51.6 us (the split form left the second, partly
 // filled round of workgroups and each workgroup's slowest wavefront on the
 // critical path: ~20-28% of wavefront time in prologue and merge waits).
+// The wide few-query kernel (verify) keeps workgroups, which share the
+// query operands in LDS; its splits-0 form is a tiered plan instead: the
+// first groups in larger pieces filling one round of workgroups, the rest
+// in pieces about 3/4 that size filling a second, which also back-fill the
+// slots the slower first-round workgroups free late.
 //
 //  * Q.K^T runs on the matrix cores: v_mfma_f32_16x16x32_bf16 with A = 16
 //    keys x 32 dims (each lane loads 16 contiguous bytes of one key row) and
@@ -683,10 +688,36 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
   static_assert(sizeof(s_q) >= 2 * kAttendWaves * kWideRows * sizeof(float), "m, l fit the operand area");
   float (*s_ml)[kAttendWaves][kWideRows] = reinterpret_cast<float (*)[kAttendWaves][kWideRows]>(&s_q[0][0][0][0]);
 
-  const int split = blockIdx.x;
-  const int h = blockIdx.y;
-  const int layer = blockIdx.z / p.nqg;
-  const int qg = blockIdx.z % p.nqg;
+  // (group, split): the grid's coordinates, or the tiered plan's order --
+  // the first wide_ga groups' wide_sa splits each, then the rest's wide_sb
+  int split, ns, layer, h, qg;
+  int64_t grp, rbase;
+  if (p.wide_sa > 0) {
+    const int bid = blockIdx.x;
+    const int na = p.wide_ga * p.wide_sa;
+    if (bid < na) {
+      grp = bid / p.wide_sa;
+      split = bid % p.wide_sa;
+      ns = p.wide_sa;
+      rbase = grp * p.wide_sa;
+    } else {
+      grp = p.wide_ga + (bid - na) / p.wide_sb;
+      split = (bid - na) % p.wide_sb;
+      ns = p.wide_sb;
+      rbase = na + (grp - p.wide_ga) * p.wide_sb;
+    }
+    qg = static_cast<int>(grp % p.nqg);
+    h = static_cast<int>((grp / p.nqg) % p.hkv);
+    layer = static_cast<int>(grp / (static_cast<int64_t>(p.nqg) * p.hkv));
+  } else {
+    split = blockIdx.x;
+    h = blockIdx.y;
+    layer = blockIdx.z / p.nqg;
+    qg = blockIdx.z % p.nqg;
+    ns = p.splits;
+    grp = (static_cast<int64_t>(layer) * p.hkv + h) * p.nqg + qg;
+    rbase = grp * p.splits;
+  }
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int ln = lane & 15;
@@ -777,7 +808,7 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
 #pragma unroll
   for (int q4 = 0; q4 < 4; ++q4)
     vtr[q4] = (4 * lg + (ln >> 2)) * 256 + ((2 * (q4 ^ (ln >> 2)) + ((ln & 3) >> 1)) << 4) + 8 * (ln & 1);
-  const int nwaves = p.splits * kAttendWaves;
+  const int nwaves = ns * kAttendWaves;
 
   // A history segment whose id lies outside the history attends nothing (a
   // fully masked segment would leave m, l and acc as they are): passed over.
@@ -1087,7 +1118,6 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
           oacc[dt][ct];
   __syncthreads();
 
-  const int64_t grp = (static_cast<int64_t>(layer) * p.hkv + h) * p.nqg + qg;
   for (int idx = threadIdx.x; idx < kWideRows * kHeadDim; idx += kAttendThreads) {
     const int n = idx / kHeadDim, d = idx % kHeadDim;
     if (n >= rows) continue;
@@ -1107,7 +1137,7 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
       const int hh = h * p.G + n % p.G;
       p.out[p.q_ls * layer + (static_cast<int64_t>(t) * hq + hh) * kHeadDim + d] = f32_to_bf16(A / L);
     } else {
-      float* part = p.partial + ((grp * p.splits + split) * p.prow + n) * kPartStride;
+      float* part = p.partial + ((rbase + split) * p.prow + n) * kPartStride;
       part[2 + d] = A;
       if (d == 0) {
         part[0] = mt;
@@ -1147,6 +1177,11 @@ __global__ __launch_bounds__(kMergeThreads) void attend_merge_kernel(const Atten
   // wavefronts wf .. wl whose item ranges meet the group's, records w + grp
   int64_t first = grp * p.splits;
   int nrec = p.splits;
+  if (p.wide_sa > 0) {   // the wide kernel's tiered plan
+    const int64_t na = static_cast<int64_t>(p.wide_ga) * p.wide_sa;
+    first = grp < p.wide_ga ? grp * p.wide_sa : na + (grp - p.wide_ga) * p.wide_sb;
+    nrec = grp < p.wide_ga ? p.wide_sa : p.wide_sb;
+  }
   if (p.stream_ipw > 0) {
     const int64_t wf = grp * p.nseg / p.stream_ipw;
     const int64_t wl = ((grp + 1) * p.nseg - 1) / p.stream_ipw;
@@ -1256,7 +1291,36 @@ int launch_grouped(int hkv, int kv_format, int num_layers, int tq, AttendParams&
   int bad = 0;
   const bool packed = p.tok_mask != nullptr || p.causal_off != 0;
   NKV_CHECK_SUPPORTED(!packed || kv_format == NKV_KV_BF16, "nkv_attend: caller-packed keys must be bf16");
-  if (p.splits == 0) {
+  if (p.splits == 0 && M == kWideRows && !packed) {
+    // the wide kernel's tiered plan: its workgroups (two per CU) fill two
+    // rounds of the device, the first with pieces of the first groups'
+    // segment lists, the second with pieces about 3/4 their size of the
+    // rest's, which also back-fill the slots the first round's slower
+    // workgroups free late.  The uniform split form's last round runs partly
+    // empty and latency-bound: 36-layer 16K verify round, 6 tokens, us at the
+    // uniform 3 splits vs this plan (3 / 4 splits) vs 2 / 16: bf16 330 / 327 /
+    // 328, int8 267 / 256 / 268, per-token int8 271 / 260 / 269.
+    const int cus = device_cus();
+    const int64_t slots = std::min<int64_t>(cus > 0 ? 2 * static_cast<int64_t>(cus) : kWidePlanSlotsMax,
+                                            kWidePlanSlotsMax);
+    const int64_t groups = static_cast<int64_t>(num_layers) * hkv * p.nqg;
+    // a piece keeps at least two segments per wavefront
+    const int smax = std::max(1, std::min(64, p.nseg / (2 * kAttendWaves)));
+    int sa = 1, sb = 1;
+    int64_t ga = groups;
+    if (groups < slots) {
+      // ga sa = slots and (groups - ga) sb = slots with sb = 4/3 sa give
+      // sa = 7 slots / (4 groups)
+      sa = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>((7 * slots + 2 * groups) / (4 * groups), smax)));
+      ga = std::min<int64_t>(groups, slots / sa);
+      const int64_t gb = groups - ga;
+      sb = gb > 0 ? static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(slots / gb, smax))) : 1;
+    }
+    p.wide_ga = static_cast<int>(ga);
+    p.wide_sa = sa;
+    p.wide_sb = sb;
+    grid = dim3(static_cast<unsigned>(ga * sa + (groups - ga) * sb), 1, 1);
+  } else if (p.splits == 0) {
     // stream form: one resident round of wavefronts (two workgroups per CU)
     // share the segment list evenly
     NKV_CHECK_SUPPORTED(M == 4 && !packed,
@@ -1301,10 +1365,14 @@ extern "C" int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads,
   group_shape(tq, num_heads / num_kv_heads, &qpg, &M);
   const int64_t nqg = (tq + qpg - 1) / qpg;
   if (splits == 0) {
+    const int64_t groups = static_cast<int64_t>(num_layers) * num_kv_heads * nqg;
+    // the wide kernel's tiered plan: at most two rounds of resident
+    // workgroups' records (or one per group when the groups fill a round)
+    if (M == kWideRows) return std::max<int64_t>(2 * kWidePlanSlotsMax, groups) * kWideRows * kPartStride;
     // stream form: at most one record per resident wavefront and group
     // boundary (records w + g, w < kStreamWavesMax, g < groups)
     if (M != 4) return 0;
-    return (kStreamWavesMax + static_cast<int64_t>(num_layers) * num_kv_heads * nqg) * kStreamRows * kPartStride;
+    return (kStreamWavesMax + groups) * kStreamRows * kPartStride;
   }
   const int prow = M > kMaxRows ? kWideRows : kMaxRows;
   return static_cast<int64_t>(num_layers) * num_kv_heads * nqg * splits * prow * kPartStride;
@@ -1345,7 +1413,8 @@ int fill_attend_params(const char* who, const nkv_store* st, int layer0, int num
     NKV_CHECK_ARG(lp < rec_lo || lp >= rec_lo + rec_len,
                   "%s: write_slot %d lies inside the attended recent window", who, write_slot);
   }
-  NKV_CHECK_ARG(splits >= 0 && splits <= 64, "%s: splits must be in [0, 64] (got %d; 0 = stream form)", who, splits);
+  NKV_CHECK_ARG(splits >= 0 && splits <= 64,
+                "%s: splits must be in [0, 64] (got %d; 0 = stream form / tiered plan)", who, splits);
   NKV_CHECK_ARG(splits == 1 || partial_ws != nullptr, "%s: splits != 1 needs partial_ws", who);
   const int n_sink_seg = (sink_len + kBlock - 1) / kBlock;
   const int n_rec_seg = rec_len > 0 ? (R + kBlock - 1) / kBlock : 0;
@@ -1413,6 +1482,7 @@ int fill_attend_params(const char* who, const nkv_store* st, int layer0, int num
   p.sel_tile = 0;
   p.stream_ipw = 0;
   p.nlayers = num_layers;
+  p.wide_ga = p.wide_sa = p.wide_sb = 0;
   return NKV_OK;
 }
 

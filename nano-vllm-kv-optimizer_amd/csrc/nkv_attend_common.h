@@ -20,6 +20,7 @@ constexpr int kMaxRows = 16;     // MFMA N: query rows per group
 constexpr int kWideRows = 32;    // query rows per group of the two-tile (wide) few-query kernel
 constexpr int kStreamRows = 4;   // rows per partial record of the 4-row kernel's stream form
 constexpr int64_t kStreamWavesMax = 2048;  // wavefronts a stream-form launch uses at most
+constexpr int kWidePlanSlotsMax = 512;     // resident wide-kernel workgroups a tiered plan fills at most
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -85,6 +86,10 @@ struct AttendParams {
   // nseg segment list
   int stream_ipw;
   int nlayers;
+  // the wide kernel's tiered split plan (wide_sa > 0): groups [0, wide_ga)
+  // take wide_sa splits each (records g wide_sa + s), the rest wide_sb
+  // (records after those), one workgroup per (group, split) in that order
+  int wide_ga, wide_sa, wide_sb;
 };
 
 __device__ __forceinline__ void wave_lds_sync() {

@@ -371,6 +371,9 @@ class _SparseCore:
     # the stream form pays off once every resident wavefront gets a couple of
     # segments (one round of ~2048 wavefronts on an MI355X)
     STREAM_MIN_SEGMENTS = 4096
+    # the wide kernel's tiered plan pays off once the groups alone fill a
+    # quarter of the device's workgroup slots (36 layers x 8 KV heads = 288)
+    WIDE_PLAN_MIN_GROUPS = 128
 
     def _splits(self, nseg: int, nqg: int, rows: int = 4) -> int:
         """Attention split count for nseg segments per (layer, KV head, query
@@ -378,10 +381,14 @@ class _SparseCore:
         0 = the 4-row kernel's stream form: one resident round of wavefronts
         shares the launch's whole segment list evenly (no second, partly
         filled round of workgroups, no wavefront idling at its workgroup's
-        merge)."""
+        merge); for the wide kernel, its tiered plan: two rounds of
+        workgroups, large pieces of the first groups' segments, then small
+        pieces of the rest's (no partly filled last round)."""
         if self.cfg.attend_splits is not None:
             return self.cfg.attend_splits
         if rows <= 4 and self.nl * self.store.num_kv_heads * nqg * nseg >= self.STREAM_MIN_SEGMENTS:
+            return 0
+        if 16 < rows <= 32 and self.nl * self.store.num_kv_heads * nqg >= self.WIDE_PLAN_MIN_GROUPS:
             return 0
         # Workgroups per launch measured best on the 36-layer 32K decode step
         # (tok/s, splits 2 / 3 / 5 / 6 / 7 / 9): bf16 ~1440 (8382 / 8827 /

@@ -93,7 +93,9 @@ TV, TQ = 16384, 6
 def test_verify_36_layer_16k_round_matches_oracle(quant, layout, rel, abs_tol):
     """The launch the verify benchmark times: M12ModelRuntime.verify(lossless)
     over 36 layers of 16384-token histories, 6 draft tokens, the automatic
-    kernel choice (the wide few-query kernel, 3 splits), the benchmark's
+    kernel choice (the wide few-query kernel in its tiered plan: 3 splits
+    for the first 170 of the 288 (layer, KV head) groups, 4 for the rest),
+    the benchmark's
     histories (same seeds) and draft tokens of its shapes.  On four sampled
     layers the union of the per-query selections must
     equal the oracle's and the outputs must match the fp64 oracle

@@ -1,4 +1,5 @@
-"""The 4-row attention kernel's stream form (splits = 0) against the split form and the oracle.
+"""The splits-0 forms against the split form and the oracle: the 4-row
+attention kernel's stream form, and the wide few-query kernel's tiered plan.
 
 The batched decode step takes the stream form once a launch holds >= 4096
 segments: one resident round of wavefronts, each attending an equal run of
@@ -137,3 +138,45 @@ def test_stream_form_short_window_and_foreign_ids():
     with pytest.raises(ValueError, match="stream form"):
         st.attend(0, q4, None, None, 0, -1, ids_d, n_hist, n_hist, None, w["sink_len"], w["ring_base"], w["rec_lo"],
                   w["rec_len"], cfg.scale, 0, part, torch.empty_like(q4))
+
+
+@pytest.mark.parametrize("L,T,top_k,quant,seed", [
+    (16, 4096, 16, False, 51),    # 128 groups: 7 splits for the first 73, 9 for the other 55
+    (40, 4096, 16, True, 52),     # 320 groups: 3 splits for the first 170, 3 for the rest
+])
+def test_wide_plan_matches_split_form_and_oracle(L, T, top_k, quant, seed):
+    """Lossless verify (6 draft tokens x G = 4: 24 rows, the wide kernel)
+    with the runtime's automatic choice (splits 0, the tiered plan) against
+    the same round at 3 uniform splits: identical unions, outputs within one
+    bf16 ulp; a sampled layer against the fp64 oracle (m12_runtime.py:656-758)."""
+    from nanokv_amd.sparse import M12Config, M12ModelRuntime
+    hq, hkv, tq = 32, 8, 6
+    kw = dict(max_model_len=T + 64, num_heads=hq, num_kv_heads=hkv, top_k_blocks=top_k, quant_history=quant)
+    plan = M12ModelRuntime(L, M12Config(**kw))
+    split = M12ModelRuntime(L, M12Config(attend_splits=3, **kw))
+    assert plan.core._splits(top_k + 10, 1, tq * hq // hkv) == 0, "the case must take the tiered plan"
+    g = torch.Generator().manual_seed(seed)
+    k = (torch.randn(L, T, hkv, D, generator=g) * D ** -0.5).bfloat16()
+    v = (torch.randn(L, T, hkv, D, generator=g) * D ** -0.5).bfloat16()
+    plan.prefill(k.cuda(), v.cuda())
+    split.prefill(k.cuda(), v.cuda())
+    i = L - 1
+    ob = O.M12Oracle(O.OracleConfig(num_heads=hq, num_kv_heads=hkv, top_k_blocks=top_k, quant_history=quant))
+    ob.store_kv(to_np(k[i]), to_np(v[i]), with_reps=False)
+    nb = plan.nblocks_filled
+    ob.reps[:, :nb] = to_np(plan.store.reps[i, :, :nb])
+    q = torch.randn(L, tq, hq, D, generator=g).bfloat16()
+    kn = (torch.randn(L, tq, hkv, D, generator=g) * D ** -0.5).bfloat16()
+    vn = (torch.randn(L, tq, hkv, D, generator=g) * D ** -0.5).bfloat16()
+    print(f"case L={L} T={T} k={top_k} int8={quant}", flush=True)
+    a = plan.verify(q.cuda(), kn.cuda(), vn.cuda(), lossless=True).float().cpu()
+    b = split.verify(q.cuda(), kn.cuda(), vn.cuda(), lossless=True).float().cpu()
+    assert torch.equal(plan.last_union_count_dev.cpu(), split.last_union_count_dev.cpu())
+    assert torch.equal(plan.last_union_dev.cpu(), split.last_union_dev.cpu())
+    assert ((a - b).abs() <= 2.0 ** -7 * b.abs() + 2e-6).all(), "tiered plan and split form differ"
+    ids_or, o_ref = ob.verify_tokens(to_np(q[i]), to_np(kn[i]), to_np(vn[i]), lossless=True)
+    cnt = int(plan.last_union_count_dev[i])
+    assert plan.last_union_dev[i, :cnt].cpu().tolist() == ids_or.tolist()
+    rel, abs_tol = (2.0 ** -6, 2e-4) if quant else (2.0 ** -7, 2e-5)
+    worst = assert_close_bf16(a[i].numpy(), o_ref, rel=rel, abs_tol=abs_tol)
+    print(f"  plan vs oracle max |err| {worst:.3e}", flush=True)

@@ -50,7 +50,8 @@ def test_kv_format_mapping():
 def _split_choice(nseg, layers=36, kv_heads=8, nqg=1, rows=4, **cfg):
     from types import SimpleNamespace
     me = SimpleNamespace(cfg=rt.M12Config(**cfg), store=SimpleNamespace(num_kv_heads=kv_heads), nl=layers,
-                         STREAM_MIN_SEGMENTS=rt._SparseCore.STREAM_MIN_SEGMENTS)
+                         STREAM_MIN_SEGMENTS=rt._SparseCore.STREAM_MIN_SEGMENTS,
+                         WIDE_PLAN_MIN_GROUPS=rt._SparseCore.WIDE_PLAN_MIN_GROUPS)
     return rt._SparseCore._splits(me, nseg, nqg, rows)
 
 
@@ -68,8 +69,12 @@ def test_decode_split_choice():
     assert _split_choice(41, layers=13) == 0                   # 13 x 8 x 41 = 4264
     # verify: 6 draft tokens x 4 heads = 24 rows on the wide kernel, 16K history
     # (139 union blocks + sink + 8 recent pieces + the draft chunk = 149 segments)
-    assert _split_choice(149, rows=24) == 3                     # bf16: ~900 as well
-    assert _split_choice(149, rows=24, quant_history=True) == 3
+    # 36 x 8 = 288 groups: the wide kernel's tiered plan (0); below 128
+    # groups its ~900-workgroup split form
+    assert _split_choice(149, rows=24) == 0
+    assert _split_choice(149, rows=24, quant_history=True) == 0
+    assert _split_choice(149, rows=24, layers=16) == 0          # 128 groups
+    assert _split_choice(149, rows=24, layers=8) == 14          # 64 groups: ~900 workgroups
     assert _split_choice(149, rows=16) == 5                     # the 16-row kernel keeps ~1440
     for layers in range(1, 80):
         for nseg in (1, 5, 16, 41, 300):

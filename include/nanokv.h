@@ -149,10 +149,10 @@ int nkv_select(const nkv_store* st, int layer0, int num_layers,
  *          workgroup (grid z = layers x groups).  splits = 0 (groups of at
  *          most 4 query rows, tq * G <= 4, e.g. one decode token at G = 4):
  *          the stream form -- one resident round of wavefronts (two
- *          workgroups per CU, at most 2048 wavefronts) takes equal runs of
- *          the launch's whole segment list, each writing one partial per
- *          (layer, KV head, group) it touches, and the merge kernel
- *          combines them.  splits = 0 with 17-32 query rows per group
+ *          workgroups per CU, at most 2048 wavefronts), the same number per
+ *          (layer, KV head, group), each taking an equal run of its group's
+ *          segments and writing one partial, and the merge kernel combines
+ *          them.  splits = 0 with 17-32 query rows per group
  *          (the wide few-query kernel, e.g. verify's 6 draft tokens at
  *          G = 4): a tiered plan -- the first groups in larger pieces
  *          filling one round of workgroups, the rest in pieces about 3/4

@@ -15,13 +15,12 @@
 // buffer; validity is applied as a -inf mask on the logits.  Split form:
 // wavefront w of split s handles segments w + 4 s, w + 4 s + 4 splits, ...
 // with an online softmax.  Stream form (4 query rows, decode): the launch is
-// one resident round of wavefronts, and wavefront w takes items
-// [w ipw, (w + 1) ipw) of the list of every (layer, KV head, group)'s
-// segments, so every wavefront gets the same number of segments and none
-// waits at a workgroup merge; 36-layer 32K decode, bf16 attention 71.3 ->
-// 68.4 us, int8 58.4 -> 51.6 us (the split form left the second, partly
-// filled round of workgroups and each workgroup's slowest wavefront on the
-// critical path: ~20-28% of wavefront time in prologue and merge waits).
+// one resident round of wavefronts, the same number per (layer, KV head,
+// group), each taking an equal run of its group's segments, so none waits
+// at a workgroup merge; 36-layer 32K decode, bf16 attention 71.3 -> 68.4 us,
+// int8 58.4 -> 51.6 us (the split form left the second, partly filled round
+// of workgroups and each workgroup's slowest wavefront on the critical path:
+// ~20-28% of wavefront time in prologue and merge waits).
 // The wide few-query kernel (verify) keeps workgroups, which share the
 // query operands in LDS; its splits-0 form is a tiered plan instead: the
 // first groups in larger pieces filling one round of workgroups, the rest
@@ -640,20 +639,18 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
   };
 
   if constexpr (STREAM && kMfmaPV && !PACKED) {
-    // Stream form: wavefront w attends items [w ipw, (w + 1) ipw) of the
-    // list of every group's segments (group g = (layer Hkv + h) nqg + qg owns
-    // items [g nseg, (g + 1) nseg)) and writes one partial record per group
-    // it touches, record w + g (distinct: a later wavefront never starts in
-    // an earlier group).  The host keeps the item count below 2^31.
+    // Stream form: wpg wavefronts per group (group g = (layer Hkv + h) nqg +
+    // qg); wavefront j of group g attends the group's segments
+    // [j nseg / wpg, (j + 1) nseg / wpg) and writes record w = g wpg + j.
+    // Every run lies in one group (one call of `group`, no loop over groups:
+    // 204-207 VGPRs and no scalar spills, against 231-253 VGPRs and 32-47
+    // spilled scalars for runs that may cross a group boundary).
     const int w = static_cast<int>(blockIdx.x) * kAttendWaves + wave;
-    const int lo = w * p.stream_ipw;
-    const int hi = min(lo + p.stream_ipw, p.nlayers * p.hkv * p.nqg * p.nseg);
-#pragma unroll 1
-    for (int g = lo / p.nseg; g * p.nseg < hi; ++g) {
-      const int lh = g / p.nqg;
-      const int sb = max(lo - g * p.nseg, 0);
-      group(lh / p.hkv, lh % p.hkv, g % p.nqg, sb, 1, min(hi - g * p.nseg, p.nseg), sb == 0, w + g);
-    }
+    const int g = w / p.stream_wpg, j = w % p.stream_wpg;
+    if (g >= p.nlayers * p.hkv * p.nqg) return;
+    const int sb = j * p.nseg / p.stream_wpg, se = (j + 1) * p.nseg / p.stream_wpg;
+    const int lh = g / p.nqg;
+    group(lh / p.hkv, lh % p.hkv, g % p.nqg, sb, 1, se, j == 0, w);
   } else {
     // split form: wavefront w of split s attends segments w + 4 s,
     // w + 4 s + 4 splits, ...
@@ -1174,7 +1171,7 @@ __global__ __launch_bounds__(kMergeThreads) void attend_merge_kernel(const Atten
   if (n >= rows) return;
   const int64_t grp = (static_cast<int64_t>(layer) * p.hkv + h) * p.nqg + qg;
   // split form: records grp * splits .. + splits - 1; stream form: the
-  // wavefronts wf .. wl whose item ranges meet the group's, records w + grp
+  // group's wavefronts' records grp * wpg .. + wpg - 1
   int64_t first = grp * p.splits;
   int nrec = p.splits;
   if (p.wide_sa > 0) {   // the wide kernel's tiered plan
@@ -1182,11 +1179,9 @@ __global__ __launch_bounds__(kMergeThreads) void attend_merge_kernel(const Atten
     first = grp < p.wide_ga ? grp * p.wide_sa : na + (grp - p.wide_ga) * p.wide_sb;
     nrec = grp < p.wide_ga ? p.wide_sa : p.wide_sb;
   }
-  if (p.stream_ipw > 0) {
-    const int64_t wf = grp * p.nseg / p.stream_ipw;
-    const int64_t wl = ((grp + 1) * p.nseg - 1) / p.stream_ipw;
-    first = wf + grp;
-    nrec = static_cast<int>(wl - wf + 1);
+  if (p.stream_wpg > 0) {
+    first = grp * p.stream_wpg;
+    nrec = p.stream_wpg;
   }
   const float* base = p.partial + (first * p.prow + n) * kPartStride;
   const int64_t sstride = static_cast<int64_t>(p.prow) * kPartStride;
@@ -1242,7 +1237,7 @@ __global__ __launch_bounds__(kWave) void ring_advance_kernel(int32_t* ring_start
 
 template <int FMT, bool PACKED = false>
 int launch_fmt(int M, dim3 grid, hipStream_t s, const AttendParams& p) {
-  if (p.stream_ipw > 0) {
+  if (p.stream_wpg > 0) {
     if (M != 4 || PACKED) return -1;
     hipLaunchKernelGGL((attend_kernel<FMT, 4, false, true>), grid, dim3(kAttendThreads), 0, s, p);
     return 0;
@@ -1321,8 +1316,8 @@ int launch_grouped(int hkv, int kv_format, int num_layers, int tq, AttendParams&
     p.wide_sb = sb;
     grid = dim3(static_cast<unsigned>(ga * sa + (groups - ga) * sb), 1, 1);
   } else if (p.splits == 0) {
-    // stream form: one resident round of wavefronts (two workgroups per CU)
-    // share the segment list evenly
+    // stream form: one resident round of wavefronts (two workgroups per CU),
+    // the same number per group, sharing each group's segments evenly
     NKV_CHECK_SUPPORTED(M == 4 && !packed,
                         "nkv_attend: the stream form (splits 0) takes groups of at most 4 query rows and no "
                         "caller-packed keys (got %d rows%s)", qpg * p.G, packed ? ", packed keys" : "");
@@ -1330,14 +1325,13 @@ int launch_grouped(int hkv, int kv_format, int num_layers, int tq, AttendParams&
     const int64_t waves = cus > 0 ? std::min<int64_t>(static_cast<int64_t>(cus) * 4 * NKV_ATTEND_DECODE_WAVES,
                                                       kStreamWavesMax)
                                   : kStreamWavesMax;
-    const int64_t total = static_cast<int64_t>(num_layers) * hkv * p.nqg * p.nseg;
-    const int64_t ipw = (total + waves - 1) / waves;
-    NKV_CHECK_SUPPORTED(total + ipw < (int64_t{1} << 31),
-                        "nkv_attend: %lld segments are too many for the stream form", static_cast<long long>(total));
-    p.stream_ipw = static_cast<int>(ipw);
+    const int64_t groups = static_cast<int64_t>(num_layers) * hkv * p.nqg;
+    const int64_t wpg = std::max<int64_t>(1, std::min<int64_t>(waves / groups, p.nseg));
+    NKV_CHECK_SUPPORTED(groups * wpg < (int64_t{1} << 31),
+                        "nkv_attend: %lld groups are too many for the stream form", static_cast<long long>(groups));
+    p.stream_wpg = static_cast<int>(wpg);
     p.prow = kStreamRows;
-    const int64_t used = (total + ipw - 1) / ipw;
-    grid = dim3(static_cast<unsigned>((used + kAttendWaves - 1) / kAttendWaves), 1, 1);
+    grid = dim3(static_cast<unsigned>((groups * wpg + kAttendWaves - 1) / kAttendWaves), 1, 1);
   }
   switch (kv_format) {
     case NKV_KV_BF16:
@@ -1369,8 +1363,8 @@ extern "C" int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads,
     // the wide kernel's tiered plan: at most two rounds of resident
     // workgroups' records (or one per group when the groups fill a round)
     if (M == kWideRows) return std::max<int64_t>(2 * kWidePlanSlotsMax, groups) * kWideRows * kPartStride;
-    // stream form: at most one record per resident wavefront and group
-    // boundary (records w + g, w < kStreamWavesMax, g < groups)
+    // stream form: one record per wavefront, groups x wpg <= max(groups,
+    // kStreamWavesMax) of them
     if (M != 4) return 0;
     return (kStreamWavesMax + groups) * kStreamRows * kPartStride;
   }
@@ -1480,7 +1474,7 @@ int fill_attend_params(const char* who, const nkv_store* st, int layer0, int num
   p.zero_n = 0;
   p.ids_tile_ls = 0;
   p.sel_tile = 0;
-  p.stream_ipw = 0;
+  p.stream_wpg = 0;
   p.nlayers = num_layers;
   p.wide_ga = p.wide_sa = p.wide_sb = 0;
   return NKV_OK;

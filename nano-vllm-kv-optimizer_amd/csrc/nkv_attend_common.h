@@ -81,10 +81,10 @@ struct AttendParams {
   // capacity (kMaxRows, or kWideRows for the wide kernel; 4 in the stream
   // form)
   int prow;
-  // the 4-row kernel's stream form (stream_ipw > 0): wavefront w attends
-  // items [w stream_ipw, (w + 1) stream_ipw) of the nlayers x hkv x nqg x
-  // nseg segment list
-  int stream_ipw;
+  // the 4-row kernel's stream form (stream_wpg > 0): stream_wpg wavefronts
+  // per (layer, KV head, query group); wavefront j of group g attends its
+  // segments [j nseg / wpg, (j + 1) nseg / wpg) and writes record g wpg + j
+  int stream_wpg;
   int nlayers;
   // the wide kernel's tiered split plan (wide_sa > 0): groups [0, wide_ga)
   // take wide_sa splits each (records g wide_sa + s), the rest wide_sb

@@ -103,7 +103,7 @@ def dynamic_top_k_from_scores(top_scores: torch.Tensor, max_k: int, target_mass:
 class M12Config:
     """Same fields, defaults and validation as the reference (m12_runtime.py:98-166).
 
-    Extra fields of this build: ``quant_scale_layout`` ("channel_block" = the
+    Extra fields (no reference counterpart): ``quant_scale_layout`` ("channel_block" = the
     reference's K-per-channel / V-per-block fp32 scales, "token" = per-token
     per-KV-head fp16 scales) and ``attend_splits`` (workgroups per KV head in
     the attention kernel; None = automatic) and ``mfma_chunk_min_tokens``

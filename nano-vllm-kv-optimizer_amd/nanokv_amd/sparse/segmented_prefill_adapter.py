@@ -20,7 +20,7 @@ Backends:
   long chunks, P rounded to bf16 for P.V as in flash attention).
 * ``"operator"`` -- the reference loads a frozen external operator package
   (``llm_gpu_kernels``, segmented_prefill_adapter.py:16-38) that is not part
-  of the reference repository; this build does not ship it, and constructing
+  of the reference repository; this package does not ship it, and constructing
   the adapter with it raises ``ValueError``.
 
 Staging: the reference gathers the selected blocks into pinned host memory
@@ -61,7 +61,7 @@ class SegmentedPrefillAdapter:
             raise ValueError("expected explicit experimental backend")
         if backend == "operator":
             raise ValueError("the 'operator' backend loads the external llm_gpu_kernels segmented operator, "
-                             "which this build does not ship; use backend='flash_reuse' (the packed "
+                             "which this package does not ship; use backend='flash_reuse' (the packed "
                              "matrix-core attention of this library)")
         self.backend, self.scale, self.geometry = backend, float(scale), geometry
         self.stream = torch.cuda.current_stream()

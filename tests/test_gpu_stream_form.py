@@ -143,6 +143,8 @@ def test_stream_form_short_window_and_foreign_ids():
 @pytest.mark.parametrize("L,T,top_k,quant,seed", [
     (16, 4096, 16, False, 51),    # 128 groups: 7 splits for the first 73, 9 for the other 55
     (40, 4096, 16, True, 52),     # 320 groups: 3 splits for the first 170, 3 for the rest
+    (56, 2048, 8, False, 53),     # 448 groups: 2 splits for the first 256, 2 for the rest
+    (72, 2048, 8, True, 54),      # 576 groups fill the 512 slots: one workgroup per group
 ])
 def test_wide_plan_matches_split_form_and_oracle(L, T, top_k, quant, seed):
     """Lossless verify (6 draft tokens x G = 4: 24 rows, the wide kernel)

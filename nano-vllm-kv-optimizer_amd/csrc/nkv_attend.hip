@@ -46,7 +46,7 @@
 //  * split form: the 4 wavefronts merge through LDS; with splits > 1 each
 //    workgroup writes a partial (m, l, acc[128]) per query row and a second
 //    kernel merges them (stream order makes the partials visible).  Stream
-//    form: each wavefront writes its own partial per group it touches.
+//    form: each wavefront writes its own partial.
 //
 // Same result as the reference's gather + pack + fp32 einsum attention
 // (nanovllm/sparse/m12_runtime.py:1212-1320 and :845-896) up to fp32
@@ -88,7 +88,7 @@ static_assert(2 * kAttendWaves * kMaxRows + kAttendWaves * 4 * kHeadDim <= kAtte
 // causal_off and an optional per-token mask applies; its own instantiation,
 // so the decode and verify paths carry none of that code.
 // STREAM: the stream form (see the end of the kernel); its own instantiation,
-// so the split form carries none of its loop.
+// so neither form carries the other's code.
 template <int FMT, int M, bool PACKED, bool STREAM = false>
 __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 1) void attend_kernel(const AttendParams p) {
   constexpr bool kMfmaPV = attend_mfma_pv<FMT, M>();

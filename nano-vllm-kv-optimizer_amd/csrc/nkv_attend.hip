@@ -266,11 +266,14 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
     // are in flight at once (the registers fit 2 waves per SIMD); wider
     // accumulators issue V after the MFMAs so K and V are not live together.
     constexpr bool kVEarly = (M == 4);
-    // bf16 with 4 query rows: one query group per (layer, KV head), so every
-    // block is read once per launch -> streamed past the caches (measured
-    // +1-5% on the 32K bf16 step; slower for int8, whose 8-byte loads keep
-    // the default policy)
+    // 4 query rows: one query group per (layer, KV head), so every selected
+    // block is read once per launch -> history streamed past the caches
+    // (non-temporal).  Under int8 history the bf16 sink / recent / chunk
+    // segments, which the next step reads again, keep the default policy
+    // (36-layer int8 32K step +3%); bf16 history streams them too (the
+    // default policy there: no gain at 8K / 32K, slower at 128K).
     constexpr bool kStream = (M == 4);
+    const bool nt_seg = kStream && (FMT == NKV_KV_BF16 || g.type == kSegHist);
     f32x4 c[4];
     uint4 va[16];
     // int8 history: the block's V scale (per-channel form, one scalar load)
@@ -293,7 +296,8 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
       } else {
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-          va[j] = kv_load16<kStream>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 16);
+          va[j] = nt_seg ? kv_load16<true>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 16)
+                         : kv_load16<false>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 16);
       }
     };
     if (int8_seg) {
@@ -342,7 +346,7 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
       for (int i = 0; i < 4; ++i) {
         const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 16;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) ka[i][s] = kv_load16<kStream>(rp + s * 64);
+        for (int s = 0; s < 4; ++s) ka[i][s] = nt_seg ? kv_load16<true>(rp + s * 64) : kv_load16<false>(rp + s * 64);
       }
       if (kVEarly) load_v();
 #pragma unroll
@@ -835,6 +839,11 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
   //   history): V goes global -> LDS without registers, issued with K, and
   //   the next segment's K loads go out once Q.K^T is done (per-token int8
   //   324 vs 338 us).
+  // With one query group per (layer, KV head) (verify's draft tokens) each
+  // history block is read once per launch: its loads are non-temporal, while
+  // the sink / recent / chunk segments keep the default policy (the 36-layer
+  // 16K verify round -4% bf16, -3% int8; all segments non-temporal -2%).
+  const bool nt_hist = p.nqg == 1;
   auto run_phase = [&](int sidx, int end, auto int8_tag) __attribute__((always_inline)) {
     constexpr bool int8_seg = decltype(int8_tag)::value;
     constexpr bool reg_v = int8_seg || FMT == NKV_KV_BF16;
@@ -851,12 +860,13 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
       for (int i = 0; i < 4; ++i) {
         if constexpr (int8_seg) {
           const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 16;
-          ka[i][0] = kv_load16<false>(rp);
-          ka[i][1] = kv_load16<false>(rp + 64);
+          ka[i][0] = nt_hist ? kv_load16<true>(rp) : kv_load16<false>(rp);
+          ka[i][1] = nt_hist ? kv_load16<true>(rp + 64) : kv_load16<false>(rp + 64);
         } else {
           const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 16;
+          const bool nt = nt_hist && g.type == kSegHist;
 #pragma unroll
-          for (int s = 0; s < 4; ++s) ka[i][s] = kv_load16<false>(rp + s * 64);
+          for (int s = 0; s < 4; ++s) ka[i][s] = nt ? kv_load16<true>(rp + s * 64) : kv_load16<false>(rp + s * 64);
         }
       }
     };
@@ -889,7 +899,8 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
       if constexpr (int8_seg) {
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          va8[j] = kv_load16<false>(g.vbase + min(8 * j + (lane >> 3), last) * g.rowb + (lane & 7) * 16);
+          va8[j] = nt_hist ? kv_load16<true>(g.vbase + min(8 * j + (lane >> 3), last) * g.rowb + (lane & 7) * 16)
+                           : kv_load16<false>(g.vbase + min(8 * j + (lane >> 3), last) * g.rowb + (lane & 7) * 16);
         if (FMT == NKV_KV_INT8_CHANNEL)
           vs_blk = ((const cfloat*)p.v_scale)[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap + g.blk];
         if (FMT == NKV_KV_INT8_TOKEN) {
@@ -944,7 +955,10 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
       uint4 va[reg_v && !int8_seg ? 16 : 1];
       if constexpr (reg_v && !int8_seg) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) va[j] = kv_load16<false>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 16);
+        for (int j = 0; j < 16; ++j)
+          va[j] = nt_hist && g.type == kSegHist
+                      ? kv_load16<true>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 16)
+                      : kv_load16<false>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 16);
       }
       // the next segment's K, issued after this segment's V
       if constexpr (prefetch_k) {

@@ -290,6 +290,29 @@ int nkv_select_union(const int32_t* ids, int num_layers, int tq, int k, int k_ef
                      int32_t* out_union, int32_t* out_count, uint8_t* out_allowed, void* stream);
 
 /*
+ * Per-query selection and its union in two launches: the scorer of
+ * nkv_select (per_query = 1), then one workgroup per layer that takes each
+ * query's Top-K (the selection, order NKV_ORDER_SCORE_DESC, of nkv_select)
+ * and forms the union and mask of those ids (nkv_select_union) without a
+ * launch in between.
+ *
+ * Replaces M12LayerRuntime._gpu_select_per_query whole
+ * (nanovllm/sparse/m12_runtime.py:1057-1087: scores per query, torch.topk per
+ * query, torch.unique, searchsorted, scatter into `allowed`).
+ *
+ * Outputs: those of nkv_select (score_keys left zeroed, out_scores, out_ids
+ * [num_layers][nq][k], out_vals) and of nkv_select_union with tq = nq and
+ * k_eff = the number of ids each row holds (min(k, selectable blocks)).
+ * Constraints: 1 <= nq <= 16, 1 <= k <= 64, 1 <= nblocks <= 2048,
+ *              umax >= nq * min(k, nblocks); others as nkv_select.
+ */
+int nkv_select_per_query(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
+                         int64_t q_layer_stride, int nq, int nblocks, const int32_t* protected_ids,
+                         int n_protected, int k, uint32_t* score_keys, float* out_scores, int32_t* out_ids,
+                         float* out_vals, int umax, int32_t* out_union, int32_t* out_count,
+                         uint8_t* out_allowed, void* stream);
+
+/*
  * Segmented causal GQA attention for a chunk of many queries, on the matrix
  * cores (bf16 MFMA for Q.K^T and P.V, fp32 softmax and accumulation).
  *

@@ -50,10 +50,19 @@ int device_cus();
 // scorer leaves the protected blocks' keys at zero and the top-k neither
 // reads the protected list nor clears the keys -- the caller's attention
 // launch must clear them (AttendParams.zero_keys).  Same ids either way.
+// With uo non-NULL (per_query, nq <= 16, k <= 64, nblocks <= 2048) the per-query
+// top-k and the union of the selections (nkv_select_union's outputs) are one
+// launch.
+struct UnionOut {
+  int umax;
+  int32_t* out_union;
+  int32_t* out_count;
+  uint8_t* out_allowed;
+};
 int select_impl(const nkv_store* st, int layer0, int num_layers, const uint16_t* q, int64_t q_layer_stride, int nq,
                 int per_query, int nblocks, const int32_t* protected_ids, int n_protected, int k, int order,
                 uint32_t* score_keys, float* out_scores, int32_t* out_ids, float* out_vals, bool step,
-                void* stream);
+                void* stream, const UnionOut* uo = nullptr);
 // Whether select_impl takes the step form for these sizes (out_scores and
 // out_vals NULL, per_query 0).
 bool select_step_form(int nq, int n_protected, int nblocks);

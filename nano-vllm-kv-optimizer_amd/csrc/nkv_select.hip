@@ -104,7 +104,8 @@ __device__ __forceinline__ unsigned long long sel_entry(uint32_t key, int id) {
 // Same selection as topk_kernel (identical ids, values and order) for one row
 // of at most 64 J blocks, computed by ONE wavefront with no workgroup barrier
 // (pmask: 2 J words of LDS, sel: LDS for max(k, 64) rounded up to a power of
-// two entries).
+// two entries).  Returns the number of ids written: k_req, or the number of
+// selectable blocks when that is smaller (at least 1).
 // Lane l holds the keys of blocks 64 j + l (j < J) in registers.  The k-th
 // largest key T is found by a bitwise search of at most 32 steps: T is the
 // largest value with count(key >= T) >= k, built from the high bit down, each
@@ -118,7 +119,7 @@ __device__ __forceinline__ unsigned long long sel_entry(uint32_t key, int id) {
 // protected list nor the zeroing stores; key 0 is read as score_key(-inf),
 // exactly the protected mask of the general form.
 template <int J, bool STEP>
-__device__ __forceinline__ void select_row_wave(
+__device__ __forceinline__ int select_row_wave(
     uint32_t* __restrict__ sk, int nblocks, const int32_t* __restrict__ prot, int nprot,
     int k_req, int order, int32_t* __restrict__ ids, float* __restrict__ vals,
     float* __restrict__ scores, uint32_t* pmask, unsigned long long* sel, int lane) {
@@ -221,7 +222,7 @@ __device__ __forceinline__ void select_row_wave(
         ids[pos] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(e & 0xffffffffull));
         if (vals) vals[pos] = key_score(static_cast<uint32_t>(e >> 32));
       }
-      return;
+      return k;
     }
   }
 
@@ -294,7 +295,7 @@ __device__ __forceinline__ void select_row_wave(
       ids[rank] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(e & 0xffffffffull));
       if (vals) vals[rank] = key_score(static_cast<uint32_t>(e >> 32));
     }
-    return;
+    return k;
   }
   if (order == NKV_ORDER_SCORE_DESC && k > 1) {
     int n2 = 1;
@@ -322,6 +323,7 @@ __device__ __forceinline__ void select_row_wave(
     ids[i] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(e & 0xffffffffull));
     if (vals) vals[i] = key_score(static_cast<uint32_t>(e >> 32));
   }
+  return k;
 }
 
 
@@ -805,96 +807,148 @@ __global__ __launch_bounds__(kWave) void topk_wave_kernel(
 constexpr int kUnionThreads = 256;
 constexpr int kUnionMax = 4096;  // tq * k_eff ids per layer
 
-// Union of one layer's per-query selections (one workgroup per layer),
-// through a bitmap of block ids in LDS: every selected id sets its bit, a
-// prefix count over the bitmap words gives each set bit its position in the
-// ascending union, and each query's ids find their mask columns by the same
-// count.  Five barriers, no sort.  Ids are block ids of nkv_select (below
-// kMaxSelectBlocks); any other value is left out of the union and the mask.
+// Union of one layer's per-query selections (one workgroup of NT threads per
+// layer), through a bitmap of block ids in LDS: every selected id sets its
+// bit, a prefix count over the bitmap words gives each set bit its position
+// in the ascending union, and each query's ids find their mask columns by the
+// same count.  Five barriers, no sort.  Ids are block ids of nkv_select
+// (below kMaxSelectBlocks); any other value is left out of the union and the
+// mask.  src: the layer's ids, row t at src + t * k (global memory, or LDS
+// for the fused top-k + union).
 constexpr int kUnionWords = kMaxSelectBlocks / 32;
-__global__ __launch_bounds__(kUnionThreads) void union_kernel(
-    const int32_t* __restrict__ ids, int tq, int k, int k_eff, int umax, int32_t* __restrict__ out_union,
-    int32_t* __restrict__ out_count, uint8_t* __restrict__ out_allowed) {
-  __shared__ uint32_t bits[kUnionWords];
-  __shared__ int32_t pre[kUnionWords];     // set bits in the words before
-  __shared__ int32_t wsum[kUnionThreads / kWave];
-  __shared__ int32_t s_max;
-  const int layer = blockIdx.x;
-  const int tid = threadIdx.x;
+template <int NT>
+struct UnionLds {
+  uint32_t bits[kUnionWords];
+  int32_t pre[kUnionWords];   // set bits in the words before
+  int32_t wsum[NT / kWave];
+  int32_t s_max;
+};
+
+template <int NT>
+__device__ __forceinline__ void union_layer(const int32_t* src, int layer, int tq, int k, int k_eff, int umax,
+                                            int32_t* __restrict__ out_union, int32_t* __restrict__ out_count,
+                                            uint8_t* __restrict__ out_allowed, UnionLds<NT>& sh, int tid) {
   const int lane = tid & 63, wave = tid >> 6;
   const int n = tq * k_eff;
-  const int32_t* src = ids + static_cast<int64_t>(layer) * tq * k;
   auto id_at = [&](int i) { return src[(i / k_eff) * k + i % k_eff]; };
   auto valid = [](int32_t id) { return id >= 0 && id < kMaxSelectBlocks; };
 
   // the largest id bounds the words to clear and count
   int32_t mx = -1;
-  for (int i = tid; i < n; i += kUnionThreads) {
+  for (int i = tid; i < n; i += NT) {
     const int32_t id = id_at(i);
     if (valid(id)) mx = max(mx, id);
   }
   for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o));
-  if (tid == 0) s_max = -1;
+  if (tid == 0) sh.s_max = -1;
   __syncthreads();
-  if (lane == 0) atomicMax(&s_max, mx);
+  if (lane == 0) atomicMax(&sh.s_max, mx);
   __syncthreads();
-  const int nwords = (s_max + 32) >> 5;   // 0 when no id is valid
-  for (int w = tid; w < nwords; w += kUnionThreads) bits[w] = 0u;
+  const int nwords = (sh.s_max + 32) >> 5;   // 0 when no id is valid
+  for (int w = tid; w < nwords; w += NT) sh.bits[w] = 0u;
   __syncthreads();
-  for (int i = tid; i < n; i += kUnionThreads) {
+  for (int i = tid; i < n; i += NT) {
     const int32_t id = id_at(i);
-    if (valid(id)) atomicOr(&bits[id >> 5], 1u << (id & 31));
+    if (valid(id)) atomicOr(&sh.bits[id >> 5], 1u << (id & 31));
   }
   __syncthreads();
 
   // exclusive prefix count of set bits over the words (thread t owns a
   // contiguous run of words)
-  const int per = (nwords + kUnionThreads - 1) / kUnionThreads;
+  const int per = (nwords + NT - 1) / NT;
   const int w0 = min(tid * per, nwords), w1 = min(w0 + per, nwords);
   int cnt = 0;
-  for (int w = w0; w < w1; ++w) cnt += __popc(bits[w]);
+  for (int w = w0; w < w1; ++w) cnt += __popc(sh.bits[w]);
   int incl = cnt;
   for (int o = 1; o < kWave; o <<= 1) {
     const int t = __shfl_up(incl, o);
     if (lane >= o) incl += t;
   }
-  if (lane == kWave - 1) wsum[wave] = incl;
+  if (lane == kWave - 1) sh.wsum[wave] = incl;
   __syncthreads();
   int base = 0;
-  for (int w = 0; w < wave; ++w) base += wsum[w];
+  for (int w = 0; w < wave; ++w) base += sh.wsum[w];
   int run = base + incl - cnt;
   for (int w = w0; w < w1; ++w) {
-    pre[w] = run;
-    run += __popc(bits[w]);
+    sh.pre[w] = run;
+    run += __popc(sh.bits[w]);
   }
   int U = 0;
-  for (int w = 0; w < kUnionThreads / kWave; ++w) U += wsum[w];
+  for (int w = 0; w < NT / kWave; ++w) U += sh.wsum[w];
   __syncthreads();
 
   // the union, ascending, then -1
   int32_t* ou = out_union + static_cast<int64_t>(layer) * umax;
-  for (int w = tid; w < nwords; w += kUnionThreads) {
-    uint32_t b = bits[w];
-    int pos = pre[w];
+  for (int w = tid; w < nwords; w += NT) {
+    uint32_t b = sh.bits[w];
+    int pos = sh.pre[w];
     while (b != 0u) {
       const int bit = __builtin_ctz(b);
       ou[pos++] = 32 * w + bit;
       b &= b - 1u;
     }
   }
-  for (int i = U + tid; i < umax; i += kUnionThreads) ou[i] = -1;
+  for (int i = U + tid; i < umax; i += NT) ou[i] = -1;
   if (tid == 0) out_count[layer] = U;
 
   // mask rows: zeros, then each query's ids at their union positions
   uint8_t* oa = out_allowed + static_cast<int64_t>(layer) * tq * umax;
-  for (int i = tid; i < tq * umax; i += kUnionThreads) oa[i] = 0;
+  for (int i = tid; i < tq * umax; i += NT) oa[i] = 0;
   __syncthreads();  // the zeros are written before the ones
-  for (int i = tid; i < n; i += kUnionThreads) {
+  for (int i = tid; i < n; i += NT) {
     const int32_t id = id_at(i);
     if (!valid(id)) continue;
-    const int pos = pre[id >> 5] + __popc(bits[id >> 5] & ((1u << (id & 31)) - 1u));
+    const int pos = sh.pre[id >> 5] + __popc(sh.bits[id >> 5] & ((1u << (id & 31)) - 1u));
     oa[static_cast<int64_t>(i / k_eff) * umax + pos] = 1;
   }
+}
+
+__global__ __launch_bounds__(kUnionThreads) void union_kernel(
+    const int32_t* __restrict__ ids, int tq, int k, int k_eff, int umax, int32_t* __restrict__ out_union,
+    int32_t* __restrict__ out_count, uint8_t* __restrict__ out_allowed) {
+  __shared__ UnionLds<kUnionThreads> sh;
+  const int layer = blockIdx.x;
+  union_layer<kUnionThreads>(ids + static_cast<int64_t>(layer) * tq * k, layer, tq, k, k_eff, umax, out_union,
+                             out_count, out_allowed, sh, threadIdx.x);
+}
+
+// Per-query Top-K and their union in one launch (one workgroup per layer):
+// wavefront w selects rows w, w + kFusedWaves, ... of the layer (the same
+// selection as topk_wave_kernel, written to out_ids / out_vals / out_scores
+// and kept in LDS), then the workgroup forms the union and mask of those ids
+// as union_kernel does.  For k <= 64 and at most 16 queries.
+constexpr int kFusedWaves = 8;
+constexpr int kFusedMaxK = kWave;
+constexpr int kFusedMaxQ = 16;
+template <int J>
+__global__ __launch_bounds__(kFusedWaves * kWave) void topk_union_kernel(
+    uint32_t* __restrict__ score_keys, int nblocks, const int32_t* __restrict__ prot, int nprot, int k_req, int tq,
+    int order, int32_t* __restrict__ out_ids, float* __restrict__ out_vals, float* __restrict__ out_scores, int umax,
+    int32_t* __restrict__ out_union, int32_t* __restrict__ out_count, uint8_t* __restrict__ out_allowed) {
+  __shared__ uint32_t pmask[kFusedWaves][J * 2];
+  __shared__ unsigned long long sel[kFusedWaves][kFusedMaxK];
+  __shared__ int32_t sids[kFusedMaxQ * kFusedMaxK];
+  __shared__ int32_t s_keff;
+  __shared__ UnionLds<kFusedWaves * kWave> sh;
+  const int layer = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  for (int t = wave; t < tq; t += kFusedWaves) {
+    const int64_t row = static_cast<int64_t>(layer) * tq + t;
+    const int ke = select_row_wave<J, false>(score_keys + row * nblocks, nblocks, prot, nprot, k_req, order,
+                                             sids + t * k_req, out_vals ? out_vals + row * k_req : nullptr,
+                                             out_scores ? out_scores + row * nblocks : nullptr, pmask[wave],
+                                             sel[wave], lane);
+    if (t == 0 && lane == 0) s_keff = ke;   // the same for every row: one protected set per layer
+  }
+  __syncthreads();
+  const int k_eff = s_keff;
+  for (int i = tid; i < tq * k_eff; i += kFusedWaves * kWave) {
+    const int t = i / k_eff, j = i % k_eff;
+    out_ids[(static_cast<int64_t>(layer) * tq + t) * k_req + j] = sids[t * k_req + j];
+  }
+  union_layer<kFusedWaves * kWave>(sids, layer, tq, k_req, k_eff, umax, out_union, out_count, out_allowed, sh, tid);
 }
 
 struct ScoreLaunch {
@@ -956,7 +1010,7 @@ namespace nkv {
 int select_impl(const nkv_store* st, int layer0, int num_layers, const uint16_t* q, int64_t q_layer_stride, int nq,
                 int per_query, int nblocks, const int32_t* protected_ids, int n_protected, int k, int order,
                 uint32_t* score_keys, float* out_scores, int32_t* out_ids, float* out_vals, bool step,
-                void* stream) {
+                void* stream, const UnionOut* uo) {
   int rc = check_store(st, layer0, num_layers);
   if (rc != NKV_OK) return rc;
   NKV_CHECK_ARG(q != nullptr && score_keys != nullptr && out_ids != nullptr,
@@ -1029,6 +1083,20 @@ int select_impl(const nkv_store* st, int layer0, int num_layers, const uint16_t*
   rc = launch_status("nkv_select/score");
   if (rc != NKV_OK) return rc;
 
+  if (uo != nullptr) {
+    NKV_CHECK_SUPPORTED(per_query && nq <= kFusedMaxQ && k <= kFusedMaxK && nblocks <= 32 * kWave,
+                        "nkv_select_per_query: needs nq <= %d, k <= %d and nblocks <= %d (got %d, %d, %d)",
+                        kFusedMaxQ, kFusedMaxK, 32 * kWave, nq, k, nblocks);
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3(num_layers), dim3(kFusedWaves * kWave), 0, s, score_keys, nblocks, protected_ids,
+                         n_protected, k, nq, order, out_ids, out_vals, out_scores, uo->umax, uo->out_union,
+                         uo->out_count, uo->out_allowed);
+    };
+    if (nblocks <= 8 * kWave) go(topk_union_kernel<8>);
+    else if (nblocks <= 16 * kWave) go(topk_union_kernel<16>);
+    else go(topk_union_kernel<32>);
+    return launch_status("nkv_select_per_query/topk+union");
+  }
   const dim3 rows(num_layers * nqo);
   if (step) {
     launch_topk_wave<true>(nblocks, rows, s, score_keys, nullptr, 0, k, order, out_ids, nullptr, nullptr);
@@ -1059,6 +1127,25 @@ extern "C" int nkv_select(const nkv_store* st, int layer0, int num_layers, const
                           float* out_vals, void* stream) {
   return select_impl(st, layer0, num_layers, q, q_layer_stride, nq, per_query, nblocks, protected_ids, n_protected,
                      k, order, score_keys, out_scores, out_ids, out_vals, false, stream);
+}
+
+extern "C" int nkv_select_per_query(const nkv_store* st, int layer0, int num_layers, const uint16_t* q,
+                                    int64_t q_layer_stride, int nq, int nblocks, const int32_t* protected_ids,
+                                    int n_protected, int k, uint32_t* score_keys, float* out_scores,
+                                    int32_t* out_ids, float* out_vals, int umax, int32_t* out_union,
+                                    int32_t* out_count, uint8_t* out_allowed, void* stream) {
+  NKV_CHECK_ARG(out_union != nullptr && out_count != nullptr && out_allowed != nullptr,
+                "nkv_select_per_query: out_union, out_count and out_allowed must be non-NULL");
+  NKV_CHECK_ARG(nq >= 1 && nq <= kFusedMaxQ, "nkv_select_per_query: nq must be in [1, %d] (got %d)", kFusedMaxQ, nq);
+  NKV_CHECK_ARG(k >= 1 && k <= kFusedMaxK, "nkv_select_per_query: k must be in [1, %d] (got %d)", kFusedMaxK, k);
+  NKV_CHECK_ARG(nblocks >= 1, "nkv_select_per_query: selection needs at least one history block (nblocks=%d)",
+                nblocks);
+  NKV_CHECK_SUPPORTED(nblocks <= 32 * kWave, "nkv_select_per_query: nblocks %d exceeds %d", nblocks, 32 * kWave);
+  const int kmax = k < nblocks ? k : nblocks;   // bounds every row's selection
+  NKV_CHECK_ARG(umax >= nq * kmax, "nkv_select_per_query: umax %d < nq * min(k, nblocks) = %d", umax, nq * kmax);
+  const UnionOut uo{umax, out_union, out_count, out_allowed};
+  return select_impl(st, layer0, num_layers, q, q_layer_stride, nq, 1, nblocks, protected_ids, n_protected, k,
+                     NKV_ORDER_SCORE_DESC, score_keys, out_scores, out_ids, out_vals, false, stream, &uo);
 }
 
 extern "C" int nkv_select_union(const int32_t* ids, int num_layers, int tq, int k, int k_eff, int umax,

@@ -83,6 +83,8 @@ SIGNATURES = {
                                 _I, _I, _I, _I, _F, _I, _P, _P, _P]),
     "nkv_prefill_workspace_floats": (_I64, [_I, _I, _I, _I, _I]),
     "nkv_select_union": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
+    "nkv_select_per_query": (_I, [_SP, _I, _I, _P, _I64, _I, _I, _P, _I, _I, _P, _P, _P, _P, _I, _P, _P, _P,
+                                  _P]),
     "nkv_store_chunk": (_I, [_SP, _I, _I, _P, _P, _I64, _I, _I, _I, _I, _P]),
     "nkv_build_reps": (_I, [_SP, _I, _I, _P, _I64, _I, _I, _P]),
     "nkv_recent_update": (_I, [_SP, _I, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _P]),

@@ -367,6 +367,43 @@ class _SparseCore:
         self._last_scores = scores.view(nl, nqo, nb)
         return ids, vals, self.effective_k(requested)
 
+    # per-query Top-K and union in one launch (36-layer 16K verify round: one
+    # launch fewer between the scorer and the attention)
+    FUSED_SELECT_UNION = True
+
+    def select_per_query_union(self, q: torch.Tensor, requested: int):
+        """Per-query selection and its union for every layer (m12_runtime.py:1057-1087):
+        q [nl, nq, Hq, D] -> (union [nl, umax] ascending then -1, counts [nl],
+        allowed [nl, nq, umax] uint8).  One launch for the Top-K and the union
+        (nkv_select_per_query, umax = nq * min(requested, nblocks)) where its
+        limits allow, else nkv_select + nkv_select_union (umax = nq * k_eff)."""
+        nb = self.nblocks_filled
+        if nb <= 0:
+            raise ValueError("selection needs at least one history block")
+        if requested < 1:
+            raise ValueError("the block budget must be >= 1")
+        q = q.contiguous()
+        nl, nq = q.shape[0], q.shape[1]
+        fused = self.FUSED_SELECT_UNION and nq <= 16 and requested <= 64 and nb <= 2048
+        kk = self.effective_k(requested)
+        umax = nq * (min(requested, nb) if fused else kk)
+        union = self._buf("union", nl * umax, torch.int32).view(nl, umax)
+        count = self._buf("union_count", nl, torch.int32)
+        allowed = self._buf("allowed", nl * nq * umax, torch.uint8).view(nl, nq, umax)
+        if fused:
+            prot, n_prot = self.protected_dev()
+            keys = self._zeroed_keys(nl * nq * nb, "")
+            scores = self._buf("scores", nl * nq * nb, torch.float32)
+            ids = self._buf("ids", nl * nq * requested, torch.int32).view(nl, nq, requested)
+            vals = self._buf("vals", nl * nq * requested, torch.float32).view(nl, nq, requested)
+            self.store.select_per_query(self.layer0, q, nb, prot, n_prot, requested, keys, scores, ids, vals,
+                                        umax, union, count, allowed)
+            self._last_scores = scores.view(nl, nq, nb)
+        else:
+            ids, _, kk = self.select(q, requested, per_query=True)
+            self.store.select_union(ids, kk, umax, union, count, allowed)
+        return union, count, allowed, umax
+
     # -- attention ------------------------------------------------------------
     # the stream form pays off once every resident wavefront gets a couple of
     # segments (one round of ~2048 wavefronts on an MI355X)
@@ -1460,13 +1497,7 @@ class M12ModelRuntime:
         if lossless:
             if tq > 16:
                 raise ValueError("per-query selection supports at most 16 queries")
-            ids, _, kk = core.select(q, req, per_query=True)
-            umax = tq * kk
-            dev = self.store.device
-            union = core._buf("union", L * umax, torch.int32).view(L, umax)
-            count = core._buf("union_count", L, torch.int32)
-            allowed = core._buf("allowed", L * tq * umax, torch.uint8).view(L, tq, umax)
-            self.store.select_union(ids, kk, umax, union, count, allowed)
+            union, count, allowed, umax = core.select_per_query_union(q, req)
             out, _, _ = core.chunk_attend(q, k, v, union, umax, umax, allowed, allowed_stride=tq * umax)
             self.last_union_dev, self.last_union_count_dev = union, count
         else:

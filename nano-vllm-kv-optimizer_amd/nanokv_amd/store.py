@@ -225,6 +225,23 @@ class SparseKVStore:
                                              _ptr(out_count), _ptr(out_allowed), _stream()),
                    "select_union")
 
+    def select_per_query(self, layer0: int, q, nblocks: int, prot_dev, n_prot: int, k: int, score_keys,
+                         out_scores, out_ids, out_vals, umax: int, out_union, out_count, out_allowed) -> None:
+        """nkv_select_per_query: select(per_query=True) and select_union in two launches
+        (q [L, nq, Hq, D] with nq <= 16, k <= 64, nblocks <= 2048)."""
+        self._bf16(q, "q")
+        nl, nq = q.shape[0], q.shape[1]
+        need = nl * nq * nblocks
+        if score_keys.numel() < need or score_keys.dtype not in (torch.int32, torch.uint32):
+            raise ValueError(f"select_per_query: score_keys needs {need} 32-bit words, got {score_keys.numel()}")
+        if (out_ids.numel() < nl * nq * k or out_union.numel() < nl * umax or out_count.numel() < nl
+                or out_allowed.numel() < nl * nq * umax):
+            raise ValueError("select_per_query: output buffers too small")
+        _lib.check(self.lib.nkv_select_per_query(
+            self._desc_ref, layer0, nl, _ptr(q), q.stride(0), nq, nblocks, _ptr(prot_dev), n_prot, k,
+            _ptr(score_keys), _ptr(out_scores), _ptr(out_ids), _ptr(out_vals), umax, _ptr(out_union),
+            _ptr(out_count), _ptr(out_allowed), _stream()), "select_per_query")
+
     def attend_workspace_floats(self, nl: int, tq: int, splits: int) -> int:
         return int(self.lib.nkv_attend_workspace_floats(nl, self.num_kv_heads, self.num_heads,
                                                         tq, splits))

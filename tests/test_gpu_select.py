@@ -213,6 +213,84 @@ def test_select_union_matches_unique_and_searchsorted(L, tq, k, k_eff, hi, seed)
         assert np.array_equal(allowed[l], want)
 
 
+@pytest.mark.parametrize("L,nq,nb,k,prot,seed", [
+    (36, 6, 256, 32, (), 0),                 # the 36-layer 16K verify round: 6 queries, J = 8
+    (3, 16, 700, 64, (0, 5, 699), 1),        # 16 queries, k = 64, 11 wavefront rows each: J = 16
+    (2, 1, 2048, 17, (3, 3, 4000, -1), 2),   # one query, J = 32; repeated / outside protected ids
+    (2, 3, 40, 64, (1,), 3),                 # k above the selectable blocks (k_eff 39)
+    (2, 5, 100, 32, tuple(range(90)), 4),    # 10 selectable blocks: k_eff 10
+    (1, 9, 513, 1, (), 5),                   # k = 1, a ragged 9th tile
+])
+def test_select_per_query_matches_select_then_union(L, nq, nb, k, prot, seed):
+    """nkv_select_per_query (per-query Top-K and union in one launch) gives the
+    bytes of nkv_select(per_query) followed by nkv_select_union: scores, ids
+    (rows past k_eff untouched), values, union, counts and mask identical, the
+    score keys left zeroed; a sampled layer against the oracle's
+    select_per_query (m12_runtime.py:1057-1087)."""
+    from nanokv_amd import _lib
+    from nanokv_amd.store import SparseKVStore
+    st = SparseKVStore(L, num_heads=HQ, num_kv_heads=HKV, head_dim=D, block_size=64, r=4, cap_blocks=nb,
+                       sink_tokens=64, recent_tokens=512, kv_format="bf16")
+    g = torch.Generator().manual_seed(seed)
+    reps = (torch.randn(L, HKV, nb, 4, D, generator=g) / D ** 0.5).to(torch.bfloat16)
+    st.reps[:, :, :nb].copy_(reps.cuda())
+    q = torch.randn(L, nq, HQ, D, generator=g).to(torch.bfloat16)
+    prot_dev = torch.tensor(list(prot) or [0], dtype=torch.int32, device="cuda")
+    k_eff = min(k, max(1, nb - len({p for p in prot if 0 <= p < nb})))
+    umax = nq * min(k, nb)
+    dev = "cuda"
+
+    def outs():
+        return (torch.zeros(L * nq * nb, dtype=torch.int32, device=dev),
+                torch.full((L * nq * nb,), -3.0, dtype=torch.float32, device=dev),
+                torch.full((L, nq, k), -5, dtype=torch.int32, device=dev),
+                torch.full((L, nq, k), -7.0, dtype=torch.float32, device=dev),
+                torch.full((L, umax), 123, dtype=torch.int32, device=dev),
+                torch.zeros(L, dtype=torch.int32, device=dev),
+                torch.full((L, nq, umax), 9, dtype=torch.uint8, device=dev))
+
+    a = outs()
+    st.select(0, q.cuda(), nb, prot_dev, len(prot), k, _lib.NKV_ORDER_SCORE_DESC, True, a[0], a[1], a[2], a[3])
+    st.select_union(a[2], k_eff, umax, a[4], a[5], a[6])
+    b = outs()
+    st.select_per_query(0, q.cuda(), nb, prot_dev, len(prot), k, b[0], b[1], b[2], b[3], umax, b[4], b[5], b[6])
+    torch.cuda.synchronize()
+    assert not b[0].any(), "score keys not left zeroed"
+    for name, x, y in zip(("scores", "ids", "vals", "union", "count", "allowed"), a[1:], b[1:]):
+        assert torch.equal(x.cpu().view(torch.int32) if x.dtype == torch.float32 else x.cpu(),
+                           y.cpu().view(torch.int32) if y.dtype == torch.float32 else y.cpu()), name
+    lyr = L - 1
+    u_or, a_or, tops = O.select_per_query(to_np(q[lyr]), to_np(reps[lyr]), nb, HKV, set(prot), k)
+    cnt = int(b[5][lyr])
+    assert tops.shape[1] == k_eff
+    assert b[2][lyr, :, :k_eff].cpu().numpy().tolist() == tops.tolist()
+    assert cnt == u_or.size and b[4][lyr, :cnt].cpu().tolist() == u_or.tolist()
+    assert (b[4][lyr, cnt:].cpu() == -1).all()
+    assert np.array_equal(b[6][lyr, :, :cnt].cpu().numpy().astype(bool), a_or)
+    assert not b[6][lyr, :, cnt:].cpu().any()
+
+
+def test_select_per_query_rejects_shapes_outside_its_limits():
+    from nanokv_amd.store import SparseKVStore
+    st = SparseKVStore(1, num_heads=HQ, num_kv_heads=HKV, head_dim=D, block_size=64, r=4, cap_blocks=4096,
+                       sink_tokens=64, recent_tokens=512, kv_format="bf16")
+    prot = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for nq, nb, k, match in ((17, 256, 32, "nq must be"), (6, 256, 65, "k must be"), (2, 2049, 32, "nblocks 2049 exceeds")):
+        q = torch.zeros(1, nq, HQ, D, dtype=torch.bfloat16, device="cuda")
+        keys = torch.zeros(nq * nb, dtype=torch.int32, device="cuda")
+        f = torch.empty(nq * nb, dtype=torch.float32, device="cuda")
+        ids = torch.empty(1, nq, k, dtype=torch.int32, device="cuda")
+        vals = torch.empty(1, nq, k, dtype=torch.float32, device="cuda")
+        umax = nq * min(k, nb)
+        u = torch.empty(1, umax, dtype=torch.int32, device="cuda")
+        c = torch.empty(1, dtype=torch.int32, device="cuda")
+        al = torch.empty(1, nq, umax, dtype=torch.uint8, device="cuda")
+        with pytest.raises(ValueError, match=match):
+            st.select_per_query(0, q, nb, prot, 0, k, keys, f, ids, vals, umax, u, c, al)
+        with pytest.raises(ValueError, match="umax"):
+            st.select_per_query(0, q[:, :1], 8, prot, 0, 4, keys, f, ids, vals, 3, u, c, al)
+
+
 def _pattern_reps(pattern, nb, r, seed):
     """Representatives whose scores tie a lot: 'zero_half' (every other block
     all-zero: score 0), 'levels' (reps = +-1/16 patterns shared by groups of

@@ -84,3 +84,44 @@ def test_batched_verify_matches_per_layer(lossless, quant, kernel):
         n = model.last_n_selected
         assert model.last_ids_dev[i, 0, :n].cpu().tolist() == rt.last_block_ids.tolist()
         assert _close(out[i], o_i, 2.0 ** -7, 1e-6)
+
+
+@pytest.mark.parametrize("top_k", [32, 80])
+def test_lossless_verify_one_launch_selection_matches_two_launches(top_k):
+    """M12ModelRuntime.verify's per-query selection in one launch
+    (nkv_select_per_query, budgets up to 64) against nkv_select +
+    nkv_select_union (the runtime's path above 64, forced here for 32 through
+    the class switch): the same unions and the same outputs bit for bit; at
+    80 the unions also against the per-layer runtime's host union."""
+    from nanokv_amd.sparse import M12Config, M12LayerRuntime, M12ModelRuntime
+    L, T, tq = 4, 8192, 6
+    cfg = M12Config(max_model_len=T + 64, top_k_blocks=top_k)
+    model = M12ModelRuntime(L, cfg)
+    k0 = torch.stack([_rand((T, 8, 128), 1500 + i, 0.09) for i in range(L)]).cuda()
+    v0 = torch.stack([_rand((T, 8, 128), 1600 + i, 0.09) for i in range(L)]).cuda()
+    model.prefill(k0, v0)
+    q = torch.stack([_rand((tq, 32, 128), 1700 + i) for i in range(L)]).cuda()
+    k = torch.stack([_rand((tq, 8, 128), 1800 + i, 0.09) for i in range(L)]).cuda()
+    v = torch.stack([_rand((tq, 8, 128), 1900 + i, 0.09) for i in range(L)]).cuda()
+    core_cls = type(model.core)
+    outs = {}
+    try:
+        for fused in (True, False):
+            core_cls.FUSED_SELECT_UNION = fused
+            o = model.verify(q, k, v, lossless=True)
+            outs[fused] = (o.cpu(), model.last_union_count_dev.cpu(), model.last_union_dev.cpu())
+            model.rollback_verified()
+    finally:
+        core_cls.FUSED_SELECT_UNION = True
+    (oa, na, ua), (ob, nb, ub) = outs[True], outs[False]
+    assert torch.equal(na, nb)
+    for i in range(L):
+        assert torch.equal(ua[i, :na[i]], ub[i, :nb[i]])
+    assert torch.equal(oa.view(torch.int16), ob.view(torch.int16))
+    if top_k > 64:
+        for i in range(L):
+            rt = M12LayerRuntime(i, cfg)
+            rt.prefill_first(None, k0[i], v0[i])
+            rt.verify_lossless = True
+            rt.verify_tokens(q[i], k[i], v[i])
+            assert ua[i, :na[i]].tolist() == rt.last_verify_block_ids.tolist()

@@ -11,9 +11,11 @@
 //
 // Mapping: a wavefront owns one (16-block tile, KV head) unit = 64 rows of
 // r representatives; the 4 waves of a workgroup take 4 consecutive tiles of
-// one KV head.  A wave streams its 16 KiB tile with fully coalesced 16-byte
-// loads (lane i reads bytes [1024*c + 16*i, +16)), transposes it through LDS
-// with an XOR swizzle (conflict-free ds_read_b128), and then every lane dots
+// one KV head.  A wave streams its 16 KiB tile with 16-byte loads (each
+// instruction reads 64-byte row quarters of 16 rows), transposes it through
+// LDS a quarter at a time with an XOR swizzle (conflict-free ds_read_b128;
+// 4 KiB of LDS per wave, so LDS does not bound the occupancy its 92 VGPRs
+// allow), and then every lane dots
 // its own row with the G query rows of that head, whose values come from
 // scalar loads (wave-uniform) after one warm-up touch of their cache lines.
 // Every vector load is unconditional (rows past nblocks are clamped and
@@ -336,9 +338,10 @@ struct ScoreTile {
 };
 
 // Issues every load of unit `unit` of `layer` (no wait).  The tile is 64 rows
-// x 256 B, read with fully coalesced 16-byte loads; half c8 of chunk c holds
-// rows (64 c + lane) / 16 of dims 64 (c / 8) .. +63.  Rows past nblocks are
-// clamped to the last valid row and zeroed, so every load is issued.
+// x 256 B, read with 16-byte loads: load c holds dims 32 (c / 4) .. +31 (one
+// 64-byte quarter) of rows 16 (c % 4) .. +15, lane l the chunk l % 4 of row
+// 16 (c % 4) + l / 4.  Rows past nblocks are clamped to the last valid row
+// and zeroed, so every load is issued.
 template <int R, int G>
 __device__ __forceinline__ void score_load(
     const uint16_t* __restrict__ q, int64_t q_ls, const uint16_t* __restrict__ reps,
@@ -352,19 +355,20 @@ __device__ __forceinline__ void score_load(
   const int last_row = (nblocks - b0) * R - 1;  // rows past it belong to blocks >= nblocks
 #pragma unroll
   for (int c = 0; c < 16; ++c) {
-    // half hf = c / 8 holds row chunks 8 hf .. 8 hf + 7; chunk index within
-    // the tile: row * 16 + 8 hf + (i & 7) with i = (c % 8) * 64 + lane
-    const int i = (c & 7) * 64 + lane;
-    const int row = i >> 3;
-    const int col = (c >> 3) * 8 + (i & 7);
+    // quarter qt = c / 4 holds row chunks 4 qt .. 4 qt + 3; chunk index within
+    // the tile: row * 16 + 4 qt + (i & 3) with i = (c % 4) * 64 + lane
+    const int i = (c & 3) * 64 + lane;
+    const int row = i >> 2;
+    const int col = (c >> 2) * 4 + (i & 3);
     t.v[c] = and_mask(src[min(row, last_row) * 16 + col], row <= last_row);
   }
   t.qc.load(qL, hkv * G, h, 0, lane);
 }
 
-// The dots and block maxima of one loaded unit.  Per query n: dot over both
-// halves in ascending d (half 0 then half 1); each half is re-staged from
-// registers through `my` (8 KiB of LDS per wave).
+// The dots and block maxima of one loaded unit.  Per query n: dot over the
+// four quarters in ascending d; each quarter is re-staged from registers
+// through `my` (4 KiB of LDS per wave; against halves through 8 KiB: 36-layer
+// 32K decode step +0.6-1.0%).
 template <int R, int G>
 __device__ __forceinline__ void score_dots(
     const uint16_t* __restrict__ q, int64_t q_ls, int nq, int per_query, int hkv, int nblocks,
@@ -382,13 +386,13 @@ __device__ __forceinline__ void score_dots(
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g] = 0.0f;
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      wave_lds_sync();  // previous half fully consumed
+    for (int qt = 0; qt < 4; ++qt) {
+      wave_lds_sync();  // previous quarter fully consumed
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
+      for (int c = 0; c < 4; ++c) {
         const int i = c * 64 + lane;
-        const int row = i >> 3, col = i & 7;
-        my[row * 8 + (col ^ (row & 7))] = t.v[hf * 8 + c];
+        const int row = i >> 2, col = i & 3;
+        my[row * 4 + (col ^ ((row >> 2) & 3))] = t.v[qt * 4 + c];
       }
       wave_lds_sync();
       // two chunks per iteration for G <= 4 (the next chunk's reads issue
@@ -396,15 +400,15 @@ __device__ __forceinline__ void score_dots(
       // rows the second chunk's scalar operands would spill
       if constexpr (G <= 4) {
 #pragma unroll 2
-        for (int c = 0; c < 8; ++c) {
-          const uint4 rv = my[lane * 8 + (c ^ (lane & 7))];
-          t.qc.fma_chunk(rv, hf * 8 + c, acc);
+        for (int c = 0; c < 4; ++c) {
+          const uint4 rv = my[lane * 4 + (c ^ ((lane >> 2) & 3))];
+          t.qc.fma_chunk(rv, qt * 4 + c, acc);
         }
       } else {
 #pragma unroll 1
-        for (int c = 0; c < 8; ++c) {
-          const uint4 rv = my[lane * 8 + (c ^ (lane & 7))];
-          t.qc.fma_chunk(rv, hf * 8 + c, acc);
+        for (int c = 0; c < 4; ++c) {
+          const uint4 rv = my[lane * 4 + (c ^ ((lane >> 2) & 3))];
+          t.qc.fma_chunk(rv, qt * 4 + c, acc);
         }
       }
     }
@@ -443,7 +447,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_kernel(
     const uint16_t* __restrict__ q, int64_t q_ls, int nq, int per_query,
     const uint16_t* __restrict__ reps, int64_t reps_ls, int hkv, int cap,
     int nblocks, int units, uint32_t* __restrict__ keys, const int32_t* __restrict__ skip_ids, int n_skip) {
-  __shared__ uint4 stage[kScoreWaves][64 * 8];  // per wave: 64 rows x 8 chunks (one half), swizzled
+  __shared__ uint4 stage[kScoreWaves][64 * 4];  // per wave: 64 rows x 4 chunks (one quarter), swizzled
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // the 4 waves of a workgroup take 4 consecutive tiles of one KV head
   const int hh = blockIdx.x % hkv;

@@ -854,17 +854,30 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
     // bf16 keys: dims [32 s + 8 lg, +8) of key 16 i + ln in ka[i][s]; int8
     // keys: dims [16 lg, +16) and [64 + 16 lg, +16) in ka[i][0..1] (16-byte loads)
     uint4 ka[4][4];
+    // (int8 segments choose the policy by one uniform branch around their
+    // loads -- a policy selected per load compiles to a branch per load:
+    // int8 verify round -2.7%; the bf16 segments keep the per-load choice,
+    // which measured faster for them)
     auto load_k = [&](const Seg& g) __attribute__((always_inline)) {
       const int last = g.len - 1;
+      if constexpr (int8_seg) {
+        auto ld = [&](auto nt_tag) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if constexpr (int8_seg) {
+          for (int i = 0; i < 4; ++i) {
+            const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 16;
+            ka[i][0] = kv_load16<decltype(nt_tag)::value>(rp);
+            ka[i][1] = kv_load16<decltype(nt_tag)::value>(rp + 64);
+          }
+        };
+        if (nt_hist)
+          ld(std::true_type{});
+        else
+          ld(std::false_type{});
+      } else {
+        const bool nt = nt_hist && g.type == kSegHist;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
           const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 16;
-          ka[i][0] = nt_hist ? kv_load16<true>(rp) : kv_load16<false>(rp);
-          ka[i][1] = nt_hist ? kv_load16<true>(rp + 64) : kv_load16<false>(rp + 64);
-        } else {
-          const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 16;
-          const bool nt = nt_hist && g.type == kSegHist;
 #pragma unroll
           for (int s = 0; s < 4; ++s) ka[i][s] = nt ? kv_load16<true>(rp + s * 64) : kv_load16<false>(rp + s * 64);
         }
@@ -897,10 +910,16 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
       float vs_blk = 1.0f;
       uint2 kts[4], vts[4];
       if constexpr (int8_seg) {
+        auto ld = [&](auto nt_tag) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          va8[j] = nt_hist ? kv_load16<true>(g.vbase + min(8 * j + (lane >> 3), last) * g.rowb + (lane & 7) * 16)
-                           : kv_load16<false>(g.vbase + min(8 * j + (lane >> 3), last) * g.rowb + (lane & 7) * 16);
+          for (int j = 0; j < 8; ++j)
+            va8[j] = kv_load16<decltype(nt_tag)::value>(g.vbase + min(8 * j + (lane >> 3), last) * g.rowb +
+                                                        (lane & 7) * 16);
+        };
+        if (nt_hist)
+          ld(std::true_type{});
+        else
+          ld(std::false_type{});
         if (FMT == NKV_KV_INT8_CHANNEL)
           vs_blk = ((const cfloat*)p.v_scale)[(static_cast<int64_t>(layer) * p.hkv + h) * p.cap + g.blk];
         if (FMT == NKV_KV_INT8_TOKEN) {

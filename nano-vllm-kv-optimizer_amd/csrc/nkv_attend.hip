@@ -271,9 +271,11 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
     // (non-temporal).  Under int8 history the bf16 sink / recent / chunk
     // segments, which the next step reads again, keep the default policy
     // (36-layer int8 32K step +3%); bf16 history streams them too (the
-    // default policy there: no gain at 8K / 32K, slower at 128K).
+    // default policy there: no gain at 8K / 32K, slower at 128K).  Under
+    // int8 history this body's bf16 instantiation sees no history segment,
+    // so the choice is a compile-time one.
     constexpr bool kStream = (M == 4);
-    const bool nt_seg = kStream && (FMT == NKV_KV_BF16 || g.type == kSegHist);
+    constexpr bool nt_seg = kStream && (FMT == NKV_KV_BF16 || int8_seg);
     f32x4 c[4];
     uint4 va[16];
     // int8 history: the block's V scale (per-channel form, one scalar load)
@@ -296,8 +298,7 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
       } else {
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-          va[j] = nt_seg ? kv_load16<true>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 16)
-                         : kv_load16<false>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 16);
+          va[j] = kv_load16<nt_seg>(g.vbase + min(4 * j + lg, last) * g.rowb + ln * 16);
       }
     };
     if (int8_seg) {
@@ -346,7 +347,7 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
       for (int i = 0; i < 4; ++i) {
         const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 16;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) ka[i][s] = nt_seg ? kv_load16<true>(rp + s * 64) : kv_load16<false>(rp + s * 64);
+        for (int s = 0; s < 4; ++s) ka[i][s] = kv_load16<nt_seg>(rp + s * 64);
       }
       if (kVEarly) load_v();
 #pragma unroll

@@ -875,7 +875,8 @@ __global__ __launch_bounds__(kAttendThreads, 2) void attend_wide_kernel(const At
         else
           ld(std::false_type{});
       } else {
-        const bool nt = nt_hist && g.type == kSegHist;
+        // (under int8 history the bf16 segments are never history blocks)
+        const bool nt = FMT == NKV_KV_BF16 && nt_hist && g.type == kSegHist;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const char* rp = g.kbase + min(i * 16 + ln, last) * g.rowb + lg * 16;

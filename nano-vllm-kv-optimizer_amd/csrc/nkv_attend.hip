@@ -373,35 +373,46 @@ __global__ __launch_bounds__(kAttendThreads, M == 4 ? NKV_ATTEND_DECODE_WAVES : 
     const bool seg_allowed = allow_row == nullptr || allow_row[g.u] != 0;
     float x[4][4];
     float cmax = -INFINITY;
+    // the segment kind is uniform: one branch per segment picks the element
+    // loop (a kind test per element compiles to a branch per element)
+    auto mask = [&](auto kind_tag) __attribute__((always_inline)) {
+      constexpr int KIND = decltype(kind_tag)::value;   // 0 history / sink, 1 ring, 2 chunk
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int tk = i * 16 + lg * 4 + e;
-        float v = c[i][e];
-        bool ok = row_ok && tk < g.vlen && seg_allowed;
-        if (g.type == kSegRecent) {
-          int lp = g.off + tk - ring_base;
-          if (lp < 0) lp += p.R;
-          ok = ok && static_cast<unsigned>(lp - p.rec_lo) < static_cast<unsigned>(p.rec_len);
-        } else if (g.type == kSegChunk) {
-          if constexpr (PACKED) {
-            ok = ok && (g.off + tk) - p.causal_off <= my_t;
-            if (ok && p.tok_mask != nullptr)
-              ok = p.tok_mask[static_cast<int64_t>(my_t) * p.n_chunk + g.off + tk] == 0;
-          } else {
-            ok = ok && (g.off + tk) <= my_t;
+        for (int e = 0; e < 4; ++e) {
+          const int tk = i * 16 + lg * 4 + e;
+          float v = c[i][e];
+          bool ok = row_ok && tk < g.vlen && seg_allowed;
+          if constexpr (KIND == 1) {
+            int lp = g.off + tk - ring_base;
+            if (lp < 0) lp += p.R;
+            ok = ok && static_cast<unsigned>(lp - p.rec_lo) < static_cast<unsigned>(p.rec_len);
+          } else if constexpr (KIND == 2) {
+            if constexpr (PACKED) {
+              ok = ok && (g.off + tk) - p.causal_off <= my_t;
+              if (ok && p.tok_mask != nullptr)
+                ok = p.tok_mask[static_cast<int64_t>(my_t) * p.n_chunk + g.off + tk] == 0;
+            } else {
+              ok = ok && (g.off + tk) <= my_t;
+            }
           }
+          if (FMT == NKV_KV_INT8_TOKEN && int8_seg) {
+            const uint32_t w = e < 2 ? kts[i].x : kts[i].y;
+            v *= f16_bits_to_f32(static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu)));
+          }
+          v = ok ? v * p.scale_log2 : -INFINITY;
+          x[i][e] = v;
+          cmax = fmaxf(cmax, v);
         }
-        if (FMT == NKV_KV_INT8_TOKEN && int8_seg) {
-          const uint32_t w = e < 2 ? kts[i].x : kts[i].y;
-          v *= f16_bits_to_f32(static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu)));
-        }
-        v = ok ? v * p.scale_log2 : -INFINITY;
-        x[i][e] = v;
-        cmax = fmaxf(cmax, v);
       }
-    }
+    };
+    if (!int8_seg && g.type == kSegRecent)
+      mask(std::integral_constant<int, 1>{});
+    else if (!int8_seg && g.type == kSegChunk)
+      mask(std::integral_constant<int, 2>{});
+    else
+      mask(std::integral_constant<int, 0>{});
     cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
     cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
     const float m_new = fmaxf(m_run, cmax);

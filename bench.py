@@ -581,38 +581,56 @@ def main():
     # Two timed regions over the same workload.  A: K steps bracketed by one
     # event pair -> the step time and `value` (model.decode: the layers split
     # over --layer-streams streams).  B: K more steps, all layers on one
-    # stream, with an event pair around each step's attention launches
-    # (attend + merge) -> the kernel's average launch duration for the
-    # roofline.  A record leaves the GPU idle for a few microseconds, so
-    # region B's launch durations include part of that idle time (conservative).
+    # stream, each step's attention launch bracketed by events with a third
+    # recorded by the library between the attention kernel and its split
+    # merge (nkv_set_merge_mark) -> the attention kernel's average launch
+    # duration for the roofline, and the merge's.  A record leaves the GPU
+    # idle briefly, so these durations include part of that idle time
+    # (conservative).
     K = args.steps
     if args.step_events == "torch":
-        tev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * K + 2)]
+        tev = [torch.cuda.Event(enable_timing=True) for _ in range(3 * K + 2)]
+        for e in tev:
+            e.record()   # the HIP event exists from its first record on
         rec = lambda i: tev[i].record()
         elapsed = lambda i, j: tev[i].elapsed_time(tev[j])
+        handle = lambda i: tev[i].cuda_event
     else:
-        dev_ev = DeviceEvents(2 * K + 2)
+        dev_ev = DeviceEvents(3 * K + 2)
         rec = dev_ev.record
         elapsed = dev_ev.elapsed_ms
+        handle = lambda i: dev_ev.ev[i].value
     torch.cuda.synchronize()
     host_t0 = time.perf_counter()
-    rec(2 * K)
+    rec(3 * K)
     for i in range(K):
         s = args.warmup + i
         model.decode(qs[s], ks[s], vs[s])
-    rec(2 * K + 1)
+    rec(3 * K + 1)
     host_us = (time.perf_counter() - host_t0) / K * 1e6  # launch-side time per step
     torch.cuda.synchronize()
-    ms_step = elapsed(2 * K, 2 * K + 1) / K
+    ms_step = elapsed(3 * K, 3 * K + 1) / K
 
-    for i in range(K):
-        s = args.warmup + K + i
-        ids, _, n = model.select(qs[s])
-        rec(2 * i)
-        model.core.decode_attend(qs[s], ks[s], vs[s], ids, ids.shape[-1], n)
-        rec(2 * i + 1)
+    from nanokv_amd import _lib
+    splits = model.core._splits(args.top_k + 9, 1) if args.splits is None else args.splits
+    try:
+        for i in range(K):
+            s = args.warmup + K + i
+            ids, _, n = model.select(qs[s])
+            if splits != 1:
+                _lib.set_merge_mark(handle(3 * i + 1))
+            rec(3 * i)
+            model.core.decode_attend(qs[s], ks[s], vs[s], ids, ids.shape[-1], n)
+            rec(3 * i + 2)
+    finally:
+        _lib.set_merge_mark(None)
     torch.cuda.synchronize()
-    attend_us = sum(elapsed(2 * i, 2 * i + 1) for i in range(K)) / K * 1e3
+    if splits != 1:
+        attend_us = sum(elapsed(3 * i, 3 * i + 1) for i in range(K)) / K * 1e3
+        merge_us = sum(elapsed(3 * i + 1, 3 * i + 2) for i in range(K)) / K * 1e3
+    else:   # one split: no merge launch
+        attend_us = sum(elapsed(3 * i, 3 * i + 2) for i in range(K)) / K * 1e3
+        merge_us = 0.0
     if args.step_events != "torch":
         dev_ev.close()
 
@@ -622,7 +640,7 @@ def main():
     prof = os.path.join(ROOT, "profiles", "decode32k_bf16_traffic.json")
     if (args.kv_format, L, T, args.top_k) == ("bf16", 36, 32768, 32) and os.path.exists(prof):
         with open(prof) as f:
-            traffic = json.load(f)["attend_op_traffic_bytes"]
+            traffic = json.load(f)["traffic_bytes_per_launch"]["attend_kernel<0, 4, false, true>"]
     us_layer = ms_step * 1e3 / L
     step_gbps = by["total"] * L / (ms_step * 1e-3) / 1e9
     attend_gbps = by["attend"] * L / (attend_us * 1e-6) / 1e9
@@ -652,18 +670,21 @@ def main():
         "us_per_layer_step": round(us_layer, 4),
         "hbm_gbps": round(step_gbps, 1),
         "bytes_per_layer_step": by["total"],
-        "attend_splits": model.core._splits(args.top_k + 9, 1) if args.splits is None else args.splits,
+        "attend_splits": splits,
         "roofline": {
             "bound": "hbm",
-            "kernel": "attend_kernel + attend_merge_kernel (in-place gather + segmented attention, all layers)",
+            "kernel": "attend_kernel (in-place gather + segmented attention, all layers; one launch per step)",
             "achieved": round(attend_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(attend_gbps / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
-            "traffic_source": "profiles/decode32k_bf16_traffic.json (calibrated FETCH_SIZE+WRITE_SIZE)" if traffic else None,
+            "traffic_source": ("profiles/decode32k_bf16_traffic.json (calibrated FETCH_SIZE+WRITE_SIZE "
+                               "of attend_kernel)") if traffic else None,
             "bytes_per_launch": by["attend"] * L,
             "avg_launch_us": round(attend_us, 2),
+            "merge_us": round(merge_us, 2),
+            "op_frac": round(by["attend"] * L / ((attend_us + merge_us) * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
         },
         "step_roofline_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
         "host_launch_us_per_step": round(host_us, 1),

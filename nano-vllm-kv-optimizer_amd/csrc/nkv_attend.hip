@@ -1322,6 +1322,10 @@ void group_shape(int tq, int G, int* qpg, int* M) {
 
 // The few-query kernel over (split, KV head, layer x query group), then the
 // split merge.
+// Timing mark of the calling host thread (nkv_set_merge_mark): recorded on the
+// launch stream between the attention kernel and its split merge; null: none.
+thread_local hipEvent_t g_merge_mark = nullptr;
+
 int launch_grouped(int hkv, int kv_format, int num_layers, int tq, AttendParams& p, hipStream_t s) {
   int qpg, M;
   group_shape(tq, p.G, &qpg, &M);
@@ -1388,15 +1392,29 @@ int launch_grouped(int hkv, int kv_format, int num_layers, int tq, AttendParams&
     default: bad = -1;
   }
   NKV_CHECK_SUPPORTED(bad == 0, "nkv_attend: unsupported row count %d / kv_format %d", M, kv_format);
-  if (p.splits != 1)
+  if (p.splits != 1) {
+    if (g_merge_mark != nullptr) {
+      const hipError_t e = hipEventRecord(g_merge_mark, s);
+      if (e != hipSuccess) {
+        (void)hipGetLastError();
+        set_error("nkv_attend: recording the merge mark failed (%s)", hipGetErrorString(e));
+        return NKV_ERR_HIP;
+      }
+    }
     hipLaunchKernelGGL(attend_merge_kernel, dim3(hkv, num_layers * p.nqg, (qpg * p.G + kMergeRows - 1) / kMergeRows),
                        dim3(kMergeThreads), 0, s, p);
+  }
   return NKV_OK;
 }
 
 }  // namespace nkv
 
 using namespace nkv;
+
+extern "C" int nkv_set_merge_mark(void* event) {
+  g_merge_mark = static_cast<hipEvent_t>(event);
+  return NKV_OK;
+}
 
 extern "C" int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads, int num_heads,
                                                int tq, int splits) {

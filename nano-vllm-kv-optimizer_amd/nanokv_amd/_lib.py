@@ -69,6 +69,7 @@ SIGNATURES = {
     "nkv_attend": (_I, [_SP, _I, _I, _P, _I64, _I, _P, _P, _I64, _I, _I, _P, _I64, _I, _P, _I64,
                         _I, _I, _I, _I, _F, _I, _P, _P, _P]),
     "nkv_attend_workspace_floats": (_I64, [_I, _I, _I, _I, _I]),
+    "nkv_set_merge_mark": (_I, [_P]),
     "nkv_decode_step": (_I, [_SP, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F,
                              _I, _P, _P, _P, _P, _I, ctypes.POINTER(ctypes.c_void_p)]),
     "nkv_decode_step_workspace_floats": (_I64, [_I, _I, _I, _I, _I]),
@@ -128,6 +129,14 @@ def host_device_pointer(host_ptr: int) -> int:
     check(lib.nkv_host_device_pointer(ctypes.c_void_p(host_ptr), ctypes.byref(out)),
           "host_device_pointer")
     return out.value
+
+
+def set_merge_mark(event) -> None:
+    """Record `event` (a hipEvent_t handle; None: stop) between the attention
+    kernel and its split merge on this thread's later launches
+    (nkv_set_merge_mark): times the kernel apart from the merge."""
+    lib = load()
+    check(lib.nkv_set_merge_mark(ctypes.c_void_p(event or None)), "nkv_set_merge_mark")
 
 
 def check(rc: int, what: str) -> None:

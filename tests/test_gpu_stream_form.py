@@ -182,3 +182,49 @@ def test_wide_plan_matches_split_form_and_oracle(L, T, top_k, quant, seed):
     rel, abs_tol = (2.0 ** -6, 2e-4) if quant else (2.0 ** -7, 2e-5)
     worst = assert_close_bf16(a[i].numpy(), o_ref, rel=rel, abs_tol=abs_tol)
     print(f"  plan vs oracle max |err| {worst:.3e}", flush=True)
+
+
+def test_merge_mark_splits_the_attention_launch():
+    """nkv_set_merge_mark: with a mark event set, the stream-form decode
+    attention records it between the attention kernel and the merge (so
+    start <= mark <= end on the stream, both spans positive) and the output is
+    bit-identical to the same call without the mark; after clearing it no
+    later launch records the event again."""
+    from nanokv_amd import _lib
+    from nanokv_amd.sparse import M12Config, M12ModelRuntime
+    L, T = 16, 8192
+    model = M12ModelRuntime(L, M12Config(max_model_len=T + 64, top_k_blocks=32))
+    g = torch.Generator().manual_seed(61)
+    k = (torch.randn(L, T, 8, D, generator=g) * D ** -0.5).bfloat16()
+    v = (torch.randn(L, T, 8, D, generator=g) * D ** -0.5).bfloat16()
+    model.prefill(k.cuda(), v.cuda())
+    core = model.core
+    q = torch.randn(L, 1, 32, D, generator=g).bfloat16().cuda()
+    kn = (torch.randn(L, 1, 8, D, generator=g) * D ** -0.5).bfloat16().cuda()
+    vn = (torch.randn(L, 1, 8, D, generator=g) * D ** -0.5).bfloat16().cuda()
+    ids, _, n = model.select(q)
+    assert core.decode_splits(n) == 0, "the case must take the stream form"
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    for e in ev:
+        e.record()
+    torch.cuda.synchronize()
+    outs = []
+    for mark in (True, False):
+        if mark:
+            _lib.set_merge_mark(ev[1].cuda_event)
+        try:
+            ev[0].record()
+            o, _, _ = core.decode_attend(q, kn, vn, ids, ids.shape[-1], n, advance=False)
+            ev[2].record()
+        finally:
+            _lib.set_merge_mark(None)
+        torch.cuda.synchronize()
+        outs.append(o.clone())
+        if mark:
+            a, b = ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])
+            assert a > 0 and b > 0, (a, b)
+            t_mark = ev[1].elapsed_time(ev[2])
+    assert torch.equal(outs[0], outs[1])
+    # cleared: the second call did not record the mark again (its span from
+    # the mark to the end covers the whole second call)
+    assert ev[1].elapsed_time(ev[2]) > t_mark

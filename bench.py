@@ -458,6 +458,25 @@ def bench_verify(args, dev):
     ms_round = start.elapsed_time(stop) / args.steps
     u_mean = float(model.last_union_count_dev.float().mean())  # the last round's unions
     by = verify_bytes(u_mean, model.nblocks_filled, tq, args.kv_format) * L
+
+    # region B: the same rounds again with events the library records right
+    # before and right after the attention kernel (nkv_set_attend_marks) ->
+    # the kernel's average launch duration for the roofline
+    from nanokv_amd import _lib
+    ev = DeviceEvents(2 * args.steps)
+    try:
+        for i in range(args.steps):
+            _lib.set_attend_marks(ev.ev[2 * i].value, ev.ev[2 * i + 1].value)
+            model.verify(qs[args.warmup + i], ks[args.warmup + i], vs[args.warmup + i], lossless=True)
+            model.rollback_verified()
+    finally:
+        _lib.set_attend_marks(None, None)
+    torch.cuda.synchronize()
+    attend_us = sum(ev.elapsed_ms(2 * i, 2 * i + 1) for i in range(args.steps)) / args.steps * 1e3
+    ev.close()
+    reps_b = model.nblocks_filled * 8 * 4 * 128 * 2   # read by the scorer, not the attention
+    by_att = (verify_bytes(u_mean, model.nblocks_filled, tq, args.kv_format) - reps_b) * L
+    att_gbps = by_att / (attend_us * 1e-6) / 1e9
     return {
         "metric": "µs per lossless speculative-verify round (all layers)",
         "value": round(ms_round * 1e3, 2),
@@ -482,6 +501,17 @@ def bench_verify(args, dev):
         "union_blocks_mean": round(u_mean, 1),
         "hbm_gbps": round(by / (ms_round * 1e-3) / 1e9, 1),
         "step_roofline_frac": round(by / (ms_round * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "attend_wide_kernel (union blocks + sink + recent + draft tokens, all layers)",
+            "achieved": round(att_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(att_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "bytes_per_launch": int(by_att),
+            "avg_launch_us": round(attend_us, 2),
+        },
     }
 
 
@@ -581,12 +611,11 @@ def main():
     # Two timed regions over the same workload.  A: K steps bracketed by one
     # event pair -> the step time and `value` (model.decode: the layers split
     # over --layer-streams streams).  B: K more steps, all layers on one
-    # stream, each step's attention launch bracketed by events with a third
-    # recorded by the library between the attention kernel and its split
-    # merge (nkv_set_merge_mark) -> the attention kernel's average launch
-    # duration for the roofline, and the merge's.  A record leaves the GPU
-    # idle briefly, so these durations include part of that idle time
-    # (conservative).
+    # stream, with events the library records right before and right after
+    # each step's attention kernel (nkv_set_attend_marks) and one after the
+    # split merge -> the attention kernel's average launch duration for the
+    # roofline, and the merge's.  A record leaves the GPU idle briefly, so
+    # these durations include part of that idle time (conservative).
     K = args.steps
     if args.step_events == "torch":
         tev = [torch.cuda.Event(enable_timing=True) for _ in range(3 * K + 2)]
@@ -617,20 +646,14 @@ def main():
         for i in range(K):
             s = args.warmup + K + i
             ids, _, n = model.select(qs[s])
-            if splits != 1:
-                _lib.set_merge_mark(handle(3 * i + 1))
-            rec(3 * i)
+            _lib.set_attend_marks(handle(3 * i), handle(3 * i + 1))
             model.core.decode_attend(qs[s], ks[s], vs[s], ids, ids.shape[-1], n)
             rec(3 * i + 2)
     finally:
-        _lib.set_merge_mark(None)
+        _lib.set_attend_marks(None, None)
     torch.cuda.synchronize()
-    if splits != 1:
-        attend_us = sum(elapsed(3 * i, 3 * i + 1) for i in range(K)) / K * 1e3
-        merge_us = sum(elapsed(3 * i + 1, 3 * i + 2) for i in range(K)) / K * 1e3
-    else:   # one split: no merge launch
-        attend_us = sum(elapsed(3 * i, 3 * i + 2) for i in range(K)) / K * 1e3
-        merge_us = 0.0
+    attend_us = sum(elapsed(3 * i, 3 * i + 1) for i in range(K)) / K * 1e3
+    merge_us = sum(elapsed(3 * i + 1, 3 * i + 2) for i in range(K)) / K * 1e3 if splits != 1 else 0.0
     if args.step_events != "torch":
         dev_ev.close()
 

@@ -177,17 +177,18 @@ int64_t nkv_attend_workspace_floats(int num_layers, int num_kv_heads, int num_he
                                     int tq, int splits);
 
 /*
- * Timing mark between the attention kernel and its split merge.  No
- * counterpart in the reference (its attention is one library call); for
- * callers that time the attention kernel apart from the merge with events of
- * their own.  While `event` (a hipEvent_t) is non-NULL, every launch of the
- * few-query attention kernels with a split merge (splits != 1) made by this
- * host thread -- nkv_attend, nkv_decode_step*, and nkv_attend_packed below
- * its matrix-core threshold -- records it on the launch stream right after
- * the attention kernel; NULL (the initial state) turns it off.  Per host
- * thread; the library never creates or destroys the event.
+ * Timing marks around the attention kernel.  No counterpart in the
+ * reference (its attention is one library call); for callers that time the
+ * attention kernel apart from the selection before it and the split merge
+ * after it with events of their own.  While set, every launch of the
+ * few-query attention kernels made by this host thread -- nkv_attend,
+ * nkv_decode_step*, and nkv_attend_packed below its matrix-core threshold --
+ * records `before` (a hipEvent_t) on the launch stream right before the
+ * attention kernel and `after` right after it, ahead of the split merge if
+ * there is one.  NULL (the initial state of both) turns a mark off.  Per
+ * host thread; the library never creates or destroys the events.
  */
-int nkv_set_merge_mark(void* event);
+int nkv_set_attend_marks(void* before, void* after);
 
 /*
  * The whole sparse decode layer-step for `num_layers` layers in one call:

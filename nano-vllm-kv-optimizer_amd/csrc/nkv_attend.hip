@@ -1322,9 +1322,22 @@ void group_shape(int tq, int G, int* qpg, int* M) {
 
 // The few-query kernel over (split, KV head, layer x query group), then the
 // split merge.
-// Timing mark of the calling host thread (nkv_set_merge_mark): recorded on the
-// launch stream between the attention kernel and its split merge; null: none.
-thread_local hipEvent_t g_merge_mark = nullptr;
+// Timing marks of the calling host thread (nkv_set_attend_marks): recorded on
+// the launch stream right before and right after the attention kernel (before
+// its split merge); null: none.
+thread_local hipEvent_t g_mark_before = nullptr;
+thread_local hipEvent_t g_mark_after = nullptr;
+
+int record_mark(hipEvent_t e, hipStream_t s) {
+  if (e == nullptr) return NKV_OK;
+  const hipError_t err = hipEventRecord(e, s);
+  if (err != hipSuccess) {
+    (void)hipGetLastError();
+    set_error("nkv_attend: recording a timing mark failed (%s)", hipGetErrorString(err));
+    return NKV_ERR_HIP;
+  }
+  return NKV_OK;
+}
 
 int launch_grouped(int hkv, int kv_format, int num_layers, int tq, AttendParams& p, hipStream_t s) {
   int qpg, M;
@@ -1383,6 +1396,7 @@ int launch_grouped(int hkv, int kv_format, int num_layers, int tq, AttendParams&
     p.prow = kStreamRows;
     grid = dim3(static_cast<unsigned>((groups * wpg + kAttendWaves - 1) / kAttendWaves), 1, 1);
   }
+  if (const int rc = record_mark(g_mark_before, s); rc != NKV_OK) return rc;
   switch (kv_format) {
     case NKV_KV_BF16:
       bad = packed ? launch_fmt<NKV_KV_BF16, true>(M, grid, s, p) : launch_fmt<NKV_KV_BF16>(M, grid, s, p);
@@ -1392,18 +1406,10 @@ int launch_grouped(int hkv, int kv_format, int num_layers, int tq, AttendParams&
     default: bad = -1;
   }
   NKV_CHECK_SUPPORTED(bad == 0, "nkv_attend: unsupported row count %d / kv_format %d", M, kv_format);
-  if (p.splits != 1) {
-    if (g_merge_mark != nullptr) {
-      const hipError_t e = hipEventRecord(g_merge_mark, s);
-      if (e != hipSuccess) {
-        (void)hipGetLastError();
-        set_error("nkv_attend: recording the merge mark failed (%s)", hipGetErrorString(e));
-        return NKV_ERR_HIP;
-      }
-    }
+  if (const int rc = record_mark(g_mark_after, s); rc != NKV_OK) return rc;
+  if (p.splits != 1)
     hipLaunchKernelGGL(attend_merge_kernel, dim3(hkv, num_layers * p.nqg, (qpg * p.G + kMergeRows - 1) / kMergeRows),
                        dim3(kMergeThreads), 0, s, p);
-  }
   return NKV_OK;
 }
 
@@ -1411,8 +1417,9 @@ int launch_grouped(int hkv, int kv_format, int num_layers, int tq, AttendParams&
 
 using namespace nkv;
 
-extern "C" int nkv_set_merge_mark(void* event) {
-  g_merge_mark = static_cast<hipEvent_t>(event);
+extern "C" int nkv_set_attend_marks(void* before, void* after) {
+  g_mark_before = static_cast<hipEvent_t>(before);
+  g_mark_after = static_cast<hipEvent_t>(after);
   return NKV_OK;
 }
 

@@ -69,7 +69,7 @@ SIGNATURES = {
     "nkv_attend": (_I, [_SP, _I, _I, _P, _I64, _I, _P, _P, _I64, _I, _I, _P, _I64, _I, _P, _I64,
                         _I, _I, _I, _I, _F, _I, _P, _P, _P]),
     "nkv_attend_workspace_floats": (_I64, [_I, _I, _I, _I, _I]),
-    "nkv_set_merge_mark": (_I, [_P]),
+    "nkv_set_attend_marks": (_I, [_P, _P]),
     "nkv_decode_step": (_I, [_SP, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F,
                              _I, _P, _P, _P, _P, _I, ctypes.POINTER(ctypes.c_void_p)]),
     "nkv_decode_step_workspace_floats": (_I64, [_I, _I, _I, _I, _I]),
@@ -131,12 +131,14 @@ def host_device_pointer(host_ptr: int) -> int:
     return out.value
 
 
-def set_merge_mark(event) -> None:
-    """Record `event` (a hipEvent_t handle; None: stop) between the attention
-    kernel and its split merge on this thread's later launches
-    (nkv_set_merge_mark): times the kernel apart from the merge."""
+def set_attend_marks(before, after) -> None:
+    """Record the hipEvent_t handles `before` / `after` (None: off) right before
+    and right after the attention kernel of this thread's later attention
+    launches (nkv_set_attend_marks): times the kernel apart from the
+    selection before it and the split merge after it."""
     lib = load()
-    check(lib.nkv_set_merge_mark(ctypes.c_void_p(event or None)), "nkv_set_merge_mark")
+    check(lib.nkv_set_attend_marks(ctypes.c_void_p(before or None), ctypes.c_void_p(after or None)),
+          "nkv_set_attend_marks")
 
 
 def check(rc: int, what: str) -> None:

@@ -184,12 +184,12 @@ def test_wide_plan_matches_split_form_and_oracle(L, T, top_k, quant, seed):
     print(f"  plan vs oracle max |err| {worst:.3e}", flush=True)
 
 
-def test_merge_mark_splits_the_attention_launch():
-    """nkv_set_merge_mark: with a mark event set, the stream-form decode
-    attention records it between the attention kernel and the merge (so
-    start <= mark <= end on the stream, both spans positive) and the output is
-    bit-identical to the same call without the mark; after clearing it no
-    later launch records the event again."""
+def test_attend_marks_bracket_the_attention_kernel():
+    """nkv_set_attend_marks: with marks set, the stream-form decode attention
+    records `before` right before the attention kernel and `after` right after
+    it, ahead of the merge (so start <= before <= after <= end on the stream,
+    both spans positive), and the output is bit-identical to the same call
+    without marks; after clearing them no later launch records them again."""
     from nanokv_amd import _lib
     from nanokv_amd.sparse import M12Config, M12ModelRuntime
     L, T = 16, 8192
@@ -204,27 +204,27 @@ def test_merge_mark_splits_the_attention_launch():
     vn = (torch.randn(L, 1, 8, D, generator=g) * D ** -0.5).bfloat16().cuda()
     ids, _, n = model.select(q)
     assert core.decode_splits(n) == 0, "the case must take the stream form"
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]   # start, before, after, end
     for e in ev:
         e.record()
     torch.cuda.synchronize()
     outs = []
     for mark in (True, False):
         if mark:
-            _lib.set_merge_mark(ev[1].cuda_event)
+            _lib.set_attend_marks(ev[1].cuda_event, ev[2].cuda_event)
         try:
             ev[0].record()
             o, _, _ = core.decode_attend(q, kn, vn, ids, ids.shape[-1], n, advance=False)
-            ev[2].record()
+            ev[3].record()
         finally:
-            _lib.set_merge_mark(None)
+            _lib.set_attend_marks(None, None)
         torch.cuda.synchronize()
         outs.append(o.clone())
         if mark:
-            a, b = ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])
-            assert a > 0 and b > 0, (a, b)
-            t_mark = ev[1].elapsed_time(ev[2])
+            spans = [ev[j].elapsed_time(ev[j + 1]) for j in range(3)]
+            assert spans[0] >= 0 and spans[1] > 0 and spans[2] > 0, spans
+            t_after = spans[2]
     assert torch.equal(outs[0], outs[1])
-    # cleared: the second call did not record the mark again (its span from
-    # the mark to the end covers the whole second call)
-    assert ev[1].elapsed_time(ev[2]) > t_mark
+    # cleared: the second call did not record the marks again (the span from
+    # the first call's `after` to the second call's end covers that call)
+    assert ev[2].elapsed_time(ev[3]) > t_after
